@@ -1,0 +1,335 @@
+// k_groupnorm.hip -- GroupNorm launchers (reference src/kernels.cu:719-745 and
+// the fused GroupNorm+activation additions) and the shape-generic kernels.
+//
+// Path choice per call:
+//   * register-resident (gn_kernels.h): cpg in {4, 8, 16}, 16-byte aligned
+//     tensors, group of at most 32768 floats.  One HBM pass.
+//   * generic (below): any cpg / size / alignment.  Streams the group twice
+//     (statistics, then output) and computes the dgamma/dbeta partials in a
+//     separate coalesced kernel.  Same maths, same reduction discipline.
+#include "gn_kernels.h"
+
+namespace {
+
+using namespace nnk;
+using namespace nnk::gn;
+
+constexpr int kGenTpb = 256;
+constexpr int kGenNw = kGenTpb / kWave;
+
+template <int ACT>
+__global__ __launch_bounds__(kGenTpb) void gn_fwd_generic(float* __restrict__ y,
+    float* __restrict__ mu_out, float* __restrict__ rstd_out, const float* __restrict__ x,
+    const float* __restrict__ gamma, const float* __restrict__ beta, int G, int HW, int C,
+    int cpg, FastDiv div_cpg, float eps) {
+    __shared__ float red[2 * kGenNw];
+    const int work = blockIdx.x;
+    const int b = work / G;
+    const int g = work - b * G;
+    const int n = HW * cpg;
+    const size_t base = (size_t)b * HW * C + (size_t)g * cpg;
+    const float* xb = x + base;
+
+    float s = 0.0f;
+    for (int i = threadIdx.x; i < n; i += kGenTpb) {
+        uint32_t hw, cl;
+        div_cpg.divmod((uint32_t)i, hw, cl);
+        s += xb[(size_t)hw * C + cl];
+    }
+    const float nf = (float)n;
+    const float mean = block_sum<kGenNw>(s, red) / nf;
+    float q = 0.0f;
+    for (int i = threadIdx.x; i < n; i += kGenTpb) {
+        uint32_t hw, cl;
+        div_cpg.divmod((uint32_t)i, hw, cl);
+        const float d = xb[(size_t)hw * C + cl] - mean;
+        q += d * d;
+    }
+    const float var = block_sum<kGenNw>(q, red + kGenNw) / nf;
+    const float rs = rsqrtf(var + eps);
+    if (threadIdx.x == 0) {
+        mu_out[work] = mean;
+        rstd_out[work] = rs;
+    }
+    for (int i = threadIdx.x; i < n; i += kGenTpb) {
+        uint32_t hw, cl;
+        div_cpg.divmod((uint32_t)i, hw, cl);
+        const size_t o = (size_t)hw * C + cl;
+        const int c = g * cpg + (int)cl;
+        y[base + o] = act_fwd<ACT>(gamma[c] * ((xb[o] - mean) * rs) + beta[c]);
+    }
+}
+
+template <int ACT>
+__global__ __launch_bounds__(kGenTpb) void gn_bwd_dx_generic(float* __restrict__ dx,
+    const float* __restrict__ dy, const float* __restrict__ x, const float* __restrict__ gamma,
+    const float* __restrict__ beta, const float* __restrict__ mu, const float* __restrict__ rstd,
+    int G, int HW, int C, int cpg, FastDiv div_cpg) {
+    __shared__ float red[2 * kGenNw];
+    const int work = blockIdx.x;
+    const int b = work / G;
+    const int g = work - b * G;
+    const int n = HW * cpg;
+    const size_t base = (size_t)b * HW * C + (size_t)g * cpg;
+    const float mean = mu[work];
+    const float rs = rstd[work];
+
+    float pg = 0.0f, pgx = 0.0f;
+    for (int i = threadIdx.x; i < n; i += kGenTpb) {
+        uint32_t hw, cl;
+        div_cpg.divmod((uint32_t)i, hw, cl);
+        const size_t o = base + (size_t)hw * C + cl;
+        const int c = g * cpg + (int)cl;
+        const float xh = (x[o] - mean) * rs;
+        float d = dy[o];
+        if constexpr (ACT != ACT_IDENTITY) d = d * act_grad<ACT>(gamma[c] * xh + beta[c]);
+        const float gg = d * gamma[c];
+        pg += gg;
+        pgx += gg * xh;
+    }
+    block_sum2<kGenNw>(pg, pgx, red);
+    const float inv_n = 1.0f / (float)n;
+    const float m1 = pg * inv_n;
+    for (int i = threadIdx.x; i < n; i += kGenTpb) {
+        uint32_t hw, cl;
+        div_cpg.divmod((uint32_t)i, hw, cl);
+        const size_t o = base + (size_t)hw * C + cl;
+        const int c = g * cpg + (int)cl;
+        const float xh = (x[o] - mean) * rs;
+        float d = dy[o];
+        if constexpr (ACT != ACT_IDENTITY) d = d * act_grad<ACT>(gamma[c] * xh + beta[c]);
+        const float gg = d * gamma[c];
+        dx[o] = rs * ((gg - m1) - xh * pgx * inv_n);
+    }
+}
+
+// part_g[b*C+c] = sum_hw d*xhat, part_b[b*C+c] = sum_hw d.  Grid (ceil(C/64), B);
+// lanes walk 64 consecutive channels (coalesced), the 4 waves split the pixels.
+template <int ACT>
+__global__ __launch_bounds__(kGenTpb) void gn_param_partial_generic(float* __restrict__ part_g,
+    float* __restrict__ part_b, const float* __restrict__ dy, const float* __restrict__ x,
+    const float* __restrict__ gamma, const float* __restrict__ beta,
+    const float* __restrict__ mu, const float* __restrict__ rstd, int G, int HW, int C, int cpg) {
+    __shared__ float lg[kGenNw][kWave];
+    __shared__ float lb[kGenNw][kWave];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wid = threadIdx.x / kWave;
+    const int c = blockIdx.x * kWave + lane;
+    const int b = blockIdx.y;
+    float sg = 0.0f, sb = 0.0f;
+    if (c < C) {
+        const int g = c / cpg;
+        const float mean = mu[b * G + g];
+        const float rs = rstd[b * G + g];
+        const float gmc = gamma[c];
+        float btc = 0.0f;
+        if constexpr (ACT != ACT_IDENTITY) btc = beta[c];
+        for (int hw = wid; hw < HW; hw += kGenNw) {
+            const size_t o = ((size_t)b * HW + hw) * C + c;
+            const float xh = (x[o] - mean) * rs;
+            float d = dy[o];
+            if constexpr (ACT != ACT_IDENTITY) d = d * act_grad<ACT>(gmc * xh + btc);
+            sg += d * xh;
+            sb += d;
+        }
+    }
+    lg[wid][lane] = sg;
+    lb[wid][lane] = sb;
+    __syncthreads();
+    if (wid == 0 && c < C) {
+        float ag = lg[0][lane], ab = lb[0][lane];
+#pragma unroll
+        for (int w = 1; w < kGenNw; ++w) {
+            ag += lg[w][lane];
+            ab += lb[w][lane];
+        }
+        part_g[(size_t)b * C + c] = ag;
+        part_b[(size_t)b * C + c] = ab;
+    }
+}
+
+// ggamma[c] = sum_b part_g[b*C+c] (and gbeta), fixed order: wave w sums
+// b = w, w+4, ... ascending, then the 4 wave sums are added in wave order.
+__global__ __launch_bounds__(kGenTpb) void gn_param_reduce(float* __restrict__ ggamma,
+    float* __restrict__ gbeta, const float* __restrict__ part_g,
+    const float* __restrict__ part_b, int B, int C) {
+    __shared__ float lg[kGenNw][kWave];
+    __shared__ float lb[kGenNw][kWave];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wid = threadIdx.x / kWave;
+    const int c = blockIdx.x * kWave + lane;
+    float sg = 0.0f, sb = 0.0f;
+    if (c < C) {
+        for (int b = wid; b < B; b += kGenNw) {
+            sg += part_g[(size_t)b * C + c];
+            sb += part_b[(size_t)b * C + c];
+        }
+    }
+    lg[wid][lane] = sg;
+    lb[wid][lane] = sb;
+    __syncthreads();
+    if (wid == 0 && c < C) {
+        float ag = lg[0][lane], ab = lb[0][lane];
+#pragma unroll
+        for (int w = 1; w < kGenNw; ++w) {
+            ag += lg[w][lane];
+            ab += lb[w][lane];
+        }
+        ggamma[c] = ag;
+        gbeta[c] = ab;
+    }
+}
+
+__global__ void fill_zero2(float* __restrict__ a, float* __restrict__ b, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) {
+        a[i] = 0.0f;
+        b[i] = 0.0f;
+    }
+}
+
+bool valid_act(int act) { return act >= ACT_IDENTITY && act <= ACT_MP_SILU; }
+
+// v4pp for the register path, or 0 when the shape/alignment needs the generic path.
+int reg_v4pp(int cpg, long long HW, const void* p0, const void* p1, const void* p2,
+    const void* p3, int& cfg) {
+    if (cpg % 4 != 0) return 0;
+    const int v4pp = cpg / 4;
+    if (v4pp != 1 && v4pp != 2 && v4pp != 4) return 0;
+    if (!aligned16(p0) || !aligned16(p1) || !aligned16(p2) || (p3 && !aligned16(p3))) return 0;
+    cfg = pick_reg_config(HW * v4pp);
+    return cfg < 0 ? 0 : v4pp;
+}
+
+bool shape_ok(const char* what, int B, int HW, int C, int G) {
+    if (B < 0 || HW <= 0 || C <= 0 || G <= 0) {
+        nnk_set_error(hipErrorInvalidValue, "%s: bad shape batch=%d HW=%d C=%d G=%d", what, B, HW, C, G);
+        return false;
+    }
+    if (C % G != 0) {
+        nnk_set_error(hipErrorInvalidValue, "%s: C=%d is not divisible by G=%d", what, C, G);
+        return false;
+    }
+    if ((long long)HW * (C / G) >= (1LL << 31) || (long long)B * G >= (1LL << 31)) {
+        nnk_set_error(hipErrorInvalidValue, "%s: group too large (HW*C/G=%lld)", what,
+            (long long)HW * (C / G));
+        return false;
+    }
+    return true;
+}
+
+void gn_forward_impl(const char* what, float* y, float* mu, float* rstd, const float* x,
+    const float* gamma, const float* beta, int B, int HW, int C, int G, float eps, int act,
+    hipStream_t s) {
+    if (!shape_ok(what, B, HW, C, G)) return;
+    NNK_REQUIRE(valid_act(act), what, "%s: unknown activation %d", what, act);
+    if (B == 0) return;
+    NNK_REQUIRE(y && mu && rstd && x && gamma && beta, what, "%s: null pointer", what);
+    const int cpg = C / G;
+    int cfg = -1;
+    const int v4pp = reg_v4pp(cpg, HW, x, y, gamma, beta, cfg);
+    bool launched = false;
+    if (v4pp) launched = nnk_gn_fwd_reg_dispatch(cfg, v4pp, act, y, mu, rstd, x, gamma, beta, B, G, HW, C, eps, s);
+    if (!launched) {
+        const FastDiv dv((uint32_t)cpg);
+        const dim3 grid((unsigned)(B * G)), block(kGenTpb);
+        NNK_ACT_DISPATCH(act, A,
+            gn_fwd_generic<A><<<grid, block, 0, s>>>(y, mu, rstd, x, gamma, beta, G, HW, C, cpg, dv, eps));
+    }
+    nnk_after_launch(what, s);
+}
+
+void gn_backward_impl(const char* what, float* dx, float* ggamma, float* gbeta, const float* dy,
+    const float* x, const float* gamma, const float* beta, const float* mu, const float* rstd,
+    int B, int HW, int C, int G, int act, float* ws, hipStream_t s) {
+    if (!shape_ok(what, B, HW, C, G)) return;
+    NNK_REQUIRE(valid_act(act), what, "%s: unknown activation %d", what, act);
+    NNK_REQUIRE(ggamma && gbeta, what, "%s: null pointer", what);
+    if (B == 0) {
+        fill_zero2<<<dim3((unsigned)((C + 255) / 256)), dim3(256), 0, s>>>(ggamma, gbeta, C);
+        nnk_after_launch(what, s);
+        return;
+    }
+    NNK_REQUIRE(dx && dy && x && gamma && mu && rstd, what, "%s: null pointer", what);
+    NNK_REQUIRE(act == ACT_IDENTITY || beta, what, "%s: beta is required with an activation", what);
+    NNK_REQUIRE(ws == nullptr || aligned16(ws), what, "%s: workspace must be 16-byte aligned", what);
+    float* scratch = ws;
+    if (!scratch) {
+        scratch = nnk_scratch_acquire((size_t)2 * B * C, s, what);
+        if (!scratch) return;
+    }
+    float* part_g = scratch;
+    float* part_b = scratch + (size_t)B * C;
+    const int cpg = C / G;
+    int cfg = -1;
+    const int v4pp = reg_v4pp(cpg, HW, x, dy, dx, gamma, cfg);
+    const bool beta_ok = act == ACT_IDENTITY || aligned16(beta);
+    bool launched = false;
+    if (v4pp && beta_ok)
+        launched = nnk_gn_bwd_reg_dispatch(cfg, v4pp, act, dx, part_g, part_b, dy, x, gamma, beta,
+            mu, rstd, B, G, HW, C, s);
+    if (!launched) {
+        const FastDiv dv((uint32_t)cpg);
+        NNK_ACT_DISPATCH(act, A,
+            gn_bwd_dx_generic<A><<<dim3((unsigned)(B * G)), dim3(kGenTpb), 0, s>>>(dx, dy, x, gamma,
+                beta, mu, rstd, G, HW, C, cpg, dv);
+            gn_param_partial_generic<A><<<dim3((unsigned)((C + kWave - 1) / kWave), (unsigned)B),
+                dim3(kGenTpb), 0, s>>>(part_g, part_b, dy, x, gamma, beta, mu, rstd, G, HW, C, cpg));
+    }
+    gn_param_reduce<<<dim3((unsigned)((C + kWave - 1) / kWave)), dim3(kGenTpb), 0, s>>>(ggamma,
+        gbeta, part_g, part_b, B, C);
+    if (!ws) nnk_scratch_release(scratch, s);
+    nnk_after_launch(what, s);
+}
+
+}  // namespace
+
+extern "C" {
+
+void launch_groupnorm_forward(float* y, float* mu, float* rstd, const float* x,
+    const float* gamma, const float* beta, int batch, int HW, int C, int G, float eps,
+    hipStream_t s) {
+    gn_forward_impl("launch_groupnorm_forward", y, mu, rstd, x, gamma, beta, batch, HW, C, G,
+        eps, ACT_IDENTITY, s);
+}
+
+void launch_groupnorm_act_forward(float* y, float* mu, float* rstd, const float* x,
+    const float* gamma, const float* beta, int batch, int HW, int C, int G, float eps,
+    Activation act, hipStream_t s) {
+    gn_forward_impl("launch_groupnorm_act_forward", y, mu, rstd, x, gamma, beta, batch, HW, C,
+        G, eps, (int)act, s);
+}
+
+void launch_groupnorm_backward(float* dx, float* ggamma, float* gbeta, const float* dy,
+    const float* x, const float* gamma, const float* mu, const float* rstd, int batch, int HW,
+    int C, int G, hipStream_t s) {
+    gn_backward_impl("launch_groupnorm_backward", dx, ggamma, gbeta, dy, x, gamma, nullptr, mu,
+        rstd, batch, HW, C, G, ACT_IDENTITY, nullptr, s);
+}
+
+void launch_groupnorm_act_backward(float* dx, float* ggamma, float* gbeta, const float* dy,
+    const float* x, const float* gamma, const float* beta, const float* mu, const float* rstd,
+    int batch, int HW, int C, int G, Activation act, hipStream_t s) {
+    gn_backward_impl("launch_groupnorm_act_backward", dx, ggamma, gbeta, dy, x, gamma, beta, mu,
+        rstd, batch, HW, C, G, (int)act, nullptr, s);
+}
+
+void launch_groupnorm_act_backward_ws(float* dx, float* ggamma, float* gbeta, const float* dy,
+    const float* x, const float* gamma, const float* beta, const float* mu, const float* rstd,
+    int batch, int HW, int C, int G, Activation act, float* workspace, hipStream_t s) {
+    if (!workspace) {
+        nnk_set_error(hipErrorInvalidValue, "launch_groupnorm_act_backward_ws: null workspace");
+        return;
+    }
+    gn_backward_impl("launch_groupnorm_act_backward_ws", dx, ggamma, gbeta, dy, x, gamma, beta,
+        mu, rstd, batch, HW, C, G, (int)act, workspace, s);
+}
+
+size_t nnhip_groupnorm_backward_workspace(int batch, int HW, int C, int G) {
+    (void)HW;
+    (void)G;
+    if (batch <= 0 || C <= 0) return 0;
+    return (size_t)2 * batch * C;
+}
+
+}  // extern "C"

@@ -1,0 +1,416 @@
+// k_layernorm.hip -- per-row LayerNorm forward/backward.
+// Reference maths: src/kernels.cu:491-567 (two-pass mean/variance, eps inside
+// the rsqrt; dx = rstd*(g - mean(g) - xhat*mean(g*xhat)), g = dy*gamma;
+// dgamma/dbeta are column sums over the rows) with launchers 594-616.
+//
+// Fast path (C % 4 == 0, C <= 1024, 16-byte aligned): one wave per row, lane
+// l owns float4 slots l, l+64, ...; each wave keeps RB rows in flight.
+//   forward : read x, write y           =  8 B/elem
+//   backward: read x, dy, write dx      = 12 B/elem
+//             + per-workgroup channel partials (2*C floats per 64 rows),
+//               summed over workgroups in a fixed order by ln_colsum2.
+// Generic path: one 256-thread block per row plus a coalesced partial kernel.
+#include "nnk_common.h"
+
+namespace {
+
+using namespace nnk;
+
+constexpr int kTpb = 256;
+constexpr int kNw = kTpb / kWave;
+constexpr int kRowsPerWg = 64;  // backward partial granularity (both paths)
+
+// ----------------------------------------------------------------------------
+// Fast forward: NV float4 per lane per row, RB rows per wave at a time.
+// ----------------------------------------------------------------------------
+template <int NV, int RB>
+__global__ __launch_bounds__(kTpb) void ln_fwd_wave(float* __restrict__ y,
+    float* __restrict__ mu, float* __restrict__ rstd, const float* __restrict__ x,
+    const float* __restrict__ gamma, const float* __restrict__ beta, int rows, int C, float eps) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wid = threadIdx.x / kWave;
+    const int C4 = C / 4;
+    const int r0 = (blockIdx.x * kNw + wid) * RB;
+    const float cf = (float)C;
+
+    float4 v[RB][NV];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+        const int row = r0 + r;
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            const int c4 = lane + k * kWave;
+            if (row < rows && c4 < C4) v[r][k] = ld4(x + (size_t)row * C + 4 * c4);
+            else v[r][k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+        const int row = r0 + r;
+        float s = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NV; ++k) s += (v[r][k].x + v[r][k].y) + (v[r][k].z + v[r][k].w);
+        const float m = wave_sum(s) / cf;
+        float q = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            if (lane + k * kWave < C4) {
+                const float a = v[r][k].x - m, b = v[r][k].y - m;
+                const float c = v[r][k].z - m, d = v[r][k].w - m;
+                q += (a * a + b * b) + (c * c + d * d);
+            }
+        }
+        const float rs = rsqrtf(wave_sum(q) / cf + eps);
+        if (row < rows) {
+            if (lane == 0) {
+                mu[row] = m;
+                rstd[row] = rs;
+            }
+#pragma unroll
+            for (int k = 0; k < NV; ++k) {
+                const int c4 = lane + k * kWave;
+                if (c4 < C4) {
+                    const float4 gm = ld4(gamma + 4 * c4), bt = ld4(beta + 4 * c4);
+                    float4 o;
+                    o.x = gm.x * ((v[r][k].x - m) * rs) + bt.x;
+                    o.y = gm.y * ((v[r][k].y - m) * rs) + bt.y;
+                    o.z = gm.z * ((v[r][k].z - m) * rs) + bt.z;
+                    o.w = gm.w * ((v[r][k].w - m) * rs) + bt.w;
+                    st4(y + (size_t)row * C + 4 * c4, o);
+                }
+            }
+        }
+    }
+}
+
+// ----------------------------------------------------------------------------
+// Fast backward: workgroup b owns rows [64b, 64b+64); each wave walks 16 of
+// them RB at a time, then the 4 waves' channel sums are combined in LDS into
+// part_g/part_b[b*C + c].
+// ----------------------------------------------------------------------------
+template <int NV, int RB>
+__global__ __launch_bounds__(kTpb) void ln_bwd_wave(float* __restrict__ dx,
+    float* __restrict__ part_g, float* __restrict__ part_b, const float* __restrict__ dy,
+    const float* __restrict__ x, const float* __restrict__ gamma,
+    const float* __restrict__ mu, const float* __restrict__ rstd, int rows, int C) {
+    __shared__ float4 lds[kNw][2][NV][kWave];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wid = threadIdx.x / kWave;
+    const int C4 = C / 4;
+    const float invC = 1.0f / (float)C;
+
+    float4 gm[NV];
+    float4 cg[NV], cb[NV];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int c4 = lane + k * kWave;
+        gm[k] = c4 < C4 ? ld4(gamma + 4 * c4) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        cg[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        cb[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+
+    constexpr int kRowsPerWave = kRowsPerWg / kNw;
+    const int wrow0 = blockIdx.x * kRowsPerWg + wid * kRowsPerWave;
+    for (int it = 0; it < kRowsPerWave; it += RB) {
+        float4 xv[RB][NV], gv[RB][NV];
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            const int row = wrow0 + it + r;
+#pragma unroll
+            for (int k = 0; k < NV; ++k) {
+                const int c4 = lane + k * kWave;
+                if (row < rows && c4 < C4) {
+                    xv[r][k] = ld4(x + (size_t)row * C + 4 * c4);
+                    gv[r][k] = ld4(dy + (size_t)row * C + 4 * c4);
+                } else {
+                    xv[r][k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    gv[r][k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            const int row = wrow0 + it + r;
+            if (row >= rows) break;  // wave-uniform
+            const float m = mu[row], rs = rstd[row];
+            float pg = 0.0f, pgx = 0.0f;
+#pragma unroll
+            for (int k = 0; k < NV; ++k) {
+                if (lane + k * kWave < C4) {
+                    float4 xh, g;
+                    xh.x = (xv[r][k].x - m) * rs;
+                    xh.y = (xv[r][k].y - m) * rs;
+                    xh.z = (xv[r][k].z - m) * rs;
+                    xh.w = (xv[r][k].w - m) * rs;
+                    const float4 d = gv[r][k];
+                    cg[k].x += d.x * xh.x;
+                    cg[k].y += d.y * xh.y;
+                    cg[k].z += d.z * xh.z;
+                    cg[k].w += d.w * xh.w;
+                    cb[k].x += d.x;
+                    cb[k].y += d.y;
+                    cb[k].z += d.z;
+                    cb[k].w += d.w;
+                    g.x = d.x * gm[k].x;
+                    g.y = d.y * gm[k].y;
+                    g.z = d.z * gm[k].z;
+                    g.w = d.w * gm[k].w;
+                    pg += (g.x + g.y) + (g.z + g.w);
+                    pgx += (g.x * xh.x + g.y * xh.y) + (g.z * xh.z + g.w * xh.w);
+                    xv[r][k] = xh;
+                    gv[r][k] = g;
+                }
+            }
+            const float S1 = wave_sum(pg), S2 = wave_sum(pgx);
+            const float m1 = S1 * invC;
+#pragma unroll
+            for (int k = 0; k < NV; ++k) {
+                const int c4 = lane + k * kWave;
+                if (c4 < C4) {
+                    float4 o;
+                    o.x = rs * ((gv[r][k].x - m1) - xv[r][k].x * S2 * invC);
+                    o.y = rs * ((gv[r][k].y - m1) - xv[r][k].y * S2 * invC);
+                    o.z = rs * ((gv[r][k].z - m1) - xv[r][k].z * S2 * invC);
+                    o.w = rs * ((gv[r][k].w - m1) - xv[r][k].w * S2 * invC);
+                    st4(dx + (size_t)row * C + 4 * c4, o);
+                }
+            }
+        }
+    }
+
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        lds[wid][0][k][lane] = cg[k];
+        lds[wid][1][k][lane] = cb[k];
+    }
+    __syncthreads();
+    // thread t < 2*NV*64 combines one (kind, k, lane) float4 over the 4 waves
+    for (int t = threadIdx.x; t < 2 * NV * kWave; t += kTpb) {
+        const int kind = t / (NV * kWave);
+        const int k = (t / kWave) % NV;
+        const int l = t % kWave;
+        const int c4 = l + k * kWave;
+        if (c4 < C4) {
+            float4 a = lds[0][kind][k][l];
+#pragma unroll
+            for (int w = 1; w < kNw; ++w) {
+                const float4 b = lds[w][kind][k][l];
+                a.x += b.x;
+                a.y += b.y;
+                a.z += b.z;
+                a.w += b.w;
+            }
+            st4((kind == 0 ? part_g : part_b) + (size_t)blockIdx.x * C + 4 * c4, a);
+        }
+    }
+}
+
+// ----------------------------------------------------------------------------
+// Generic path.
+// ----------------------------------------------------------------------------
+__global__ __launch_bounds__(kTpb) void ln_fwd_generic(float* __restrict__ y,
+    float* __restrict__ mu, float* __restrict__ rstd, const float* __restrict__ x,
+    const float* __restrict__ gamma, const float* __restrict__ beta, int C, float eps) {
+    __shared__ float red[2 * kNw];
+    const int row = blockIdx.x;
+    const float* xr = x + (size_t)row * C;
+    float s = 0.0f;
+    for (int c = threadIdx.x; c < C; c += kTpb) s += xr[c];
+    const float m = block_sum<kNw>(s, red) / (float)C;
+    float q = 0.0f;
+    for (int c = threadIdx.x; c < C; c += kTpb) {
+        const float d = xr[c] - m;
+        q += d * d;
+    }
+    const float rs = rsqrtf(block_sum<kNw>(q, red + kNw) / (float)C + eps);
+    if (threadIdx.x == 0) {
+        mu[row] = m;
+        rstd[row] = rs;
+    }
+    float* yr = y + (size_t)row * C;
+    for (int c = threadIdx.x; c < C; c += kTpb) yr[c] = gamma[c] * ((xr[c] - m) * rs) + beta[c];
+}
+
+__global__ __launch_bounds__(kTpb) void ln_bwd_dx_generic(float* __restrict__ dx,
+    const float* __restrict__ dy, const float* __restrict__ x, const float* __restrict__ gamma,
+    const float* __restrict__ mu, const float* __restrict__ rstd, int C) {
+    __shared__ float red[2 * kNw];
+    const int row = blockIdx.x;
+    const size_t base = (size_t)row * C;
+    const float m = mu[row], rs = rstd[row];
+    float pg = 0.0f, pgx = 0.0f;
+    for (int c = threadIdx.x; c < C; c += kTpb) {
+        const float xh = (x[base + c] - m) * rs;
+        const float g = dy[base + c] * gamma[c];
+        pg += g;
+        pgx += g * xh;
+    }
+    block_sum2<kNw>(pg, pgx, red);
+    const float invC = 1.0f / (float)C;
+    for (int c = threadIdx.x; c < C; c += kTpb) {
+        const float xh = (x[base + c] - m) * rs;
+        const float g = dy[base + c] * gamma[c];
+        dx[base + c] = rs * ((g - pg * invC) - xh * pgx * invC);
+    }
+}
+
+// part[chunk*C + c] over rows [64*chunk, 64*chunk+64): lanes walk 64 channels.
+__global__ __launch_bounds__(kTpb) void ln_param_partial_generic(float* __restrict__ part_g,
+    float* __restrict__ part_b, const float* __restrict__ dy, const float* __restrict__ x,
+    const float* __restrict__ mu, const float* __restrict__ rstd, int rows, int C) {
+    __shared__ float lg[kNw][kWave];
+    __shared__ float lb[kNw][kWave];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wid = threadIdx.x / kWave;
+    const int c = blockIdx.x * kWave + lane;
+    const int r0 = blockIdx.y * kRowsPerWg;
+    const int r1 = min(rows, r0 + kRowsPerWg);
+    float sg = 0.0f, sb = 0.0f;
+    if (c < C) {
+        for (int r = r0 + wid; r < r1; r += kNw) {
+            const float xh = (x[(size_t)r * C + c] - mu[r]) * rstd[r];
+            const float d = dy[(size_t)r * C + c];
+            sg += d * xh;
+            sb += d;
+        }
+    }
+    lg[wid][lane] = sg;
+    lb[wid][lane] = sb;
+    __syncthreads();
+    if (wid == 0 && c < C) {
+        part_g[(size_t)blockIdx.y * C + c] = ((lg[0][lane] + lg[1][lane]) + lg[2][lane]) + lg[3][lane];
+        part_b[(size_t)blockIdx.y * C + c] = ((lb[0][lane] + lb[1][lane]) + lb[2][lane]) + lb[3][lane];
+    }
+}
+
+// out[c] = sum_p part[p*C + c] over P partial rows; wave w takes p = w, w+4, ...
+__global__ __launch_bounds__(kTpb) void ln_colsum2(float* __restrict__ og, float* __restrict__ ob,
+    const float* __restrict__ pg, const float* __restrict__ pb, int P, int C) {
+    __shared__ float lg[kNw][kWave];
+    __shared__ float lb[kNw][kWave];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wid = threadIdx.x / kWave;
+    const int c = blockIdx.x * kWave + lane;
+    float sg = 0.0f, sb = 0.0f;
+    if (c < C) {
+        for (int p = wid; p < P; p += kNw) {
+            sg += pg[(size_t)p * C + c];
+            sb += pb[(size_t)p * C + c];
+        }
+    }
+    lg[wid][lane] = sg;
+    lb[wid][lane] = sb;
+    __syncthreads();
+    if (wid == 0 && c < C) {
+        og[c] = ((lg[0][lane] + lg[1][lane]) + lg[2][lane]) + lg[3][lane];
+        ob[c] = ((lb[0][lane] + lb[1][lane]) + lb[2][lane]) + lb[3][lane];
+    }
+}
+
+__global__ void fill_zero2(float* __restrict__ a, float* __restrict__ b, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) {
+        a[i] = 0.0f;
+        b[i] = 0.0f;
+    }
+}
+
+// NV for the fast path, or 0.
+int fast_nv(int C, const void* a, const void* b, const void* c, const void* d) {
+    if (C % 4 != 0 || C > 1024) return 0;
+    if (!aligned16(a) || !aligned16(b) || !aligned16(c) || !aligned16(d)) return 0;
+    const int c4 = C / 4;
+    return c4 <= 64 ? 1 : (c4 <= 128 ? 2 : 4);
+}
+
+int num_chunks(int rows) { return (rows + kRowsPerWg - 1) / kRowsPerWg; }
+
+void ln_backward_impl(const char* what, float* dx, float* ggamma, float* gbeta, const float* dy,
+    const float* x, const float* gamma, const float* mu, const float* rstd, int rows, int C,
+    float* ws, hipStream_t s) {
+    NNK_REQUIRE(rows >= 0 && C > 0, what, "%s: bad shape batch=%d C=%d", what, rows, C);
+    NNK_REQUIRE(ggamma && gbeta, what, "%s: null pointer", what);
+    if (rows == 0) {
+        fill_zero2<<<dim3((unsigned)((C + 255) / 256)), dim3(256), 0, s>>>(ggamma, gbeta, C);
+        nnk_after_launch(what, s);
+        return;
+    }
+    NNK_REQUIRE(dx && dy && x && gamma && mu && rstd, what, "%s: null pointer", what);
+    NNK_REQUIRE(ws == nullptr || aligned16(ws), what, "%s: workspace must be 16-byte aligned", what);
+    const int P = num_chunks(rows);
+    float* scratch = ws;
+    if (!scratch) {
+        scratch = nnk_scratch_acquire((size_t)2 * P * C, s, what);
+        if (!scratch) return;
+    }
+    float* part_g = scratch;
+    float* part_b = scratch + (size_t)P * C;
+    const int nv = fast_nv(C, dx, dy, x, gamma);
+    if (nv && (C % 4 == 0) && aligned16(part_b)) {
+        switch (nv) {
+        case 1: ln_bwd_wave<1, 4><<<P, kTpb, 0, s>>>(dx, part_g, part_b, dy, x, gamma, mu, rstd, rows, C); break;
+        case 2: ln_bwd_wave<2, 2><<<P, kTpb, 0, s>>>(dx, part_g, part_b, dy, x, gamma, mu, rstd, rows, C); break;
+        default: ln_bwd_wave<4, 1><<<P, kTpb, 0, s>>>(dx, part_g, part_b, dy, x, gamma, mu, rstd, rows, C); break;
+        }
+    } else {
+        ln_bwd_dx_generic<<<rows, kTpb, 0, s>>>(dx, dy, x, gamma, mu, rstd, C);
+        ln_param_partial_generic<<<dim3((unsigned)((C + kWave - 1) / kWave), (unsigned)P), kTpb, 0, s>>>(
+            part_g, part_b, dy, x, mu, rstd, rows, C);
+    }
+    ln_colsum2<<<dim3((unsigned)((C + kWave - 1) / kWave)), kTpb, 0, s>>>(ggamma, gbeta, part_g, part_b, P, C);
+    if (!ws) nnk_scratch_release(scratch, s);
+    nnk_after_launch(what, s);
+}
+
+}  // namespace
+
+extern "C" {
+
+void launch_layernorm_forward(float* y, float* mu, float* rstd, const float* x, const float* gamma,
+    const float* beta, int batch, int C, float eps, hipStream_t s) {
+    const char* what = "launch_layernorm_forward";
+    NNK_REQUIRE(batch >= 0 && C > 0, what, "%s: bad shape batch=%d C=%d", what, batch, C);
+    if (batch == 0) return;
+    NNK_REQUIRE(y && mu && rstd && x && gamma && beta, what, "%s: null pointer", what);
+    const int nv = fast_nv(C, y, x, gamma, beta);
+    if (nv == 1) {
+        constexpr int RB = 4;
+        ln_fwd_wave<1, RB><<<(unsigned)((batch + kNw * RB - 1) / (kNw * RB)), kTpb, 0, s>>>(y, mu, rstd, x, gamma, beta, batch, C, eps);
+    } else if (nv == 2) {
+        constexpr int RB = 2;
+        ln_fwd_wave<2, RB><<<(unsigned)((batch + kNw * RB - 1) / (kNw * RB)), kTpb, 0, s>>>(y, mu, rstd, x, gamma, beta, batch, C, eps);
+    } else if (nv == 4) {
+        constexpr int RB = 1;
+        ln_fwd_wave<4, RB><<<(unsigned)((batch + kNw * RB - 1) / (kNw * RB)), kTpb, 0, s>>>(y, mu, rstd, x, gamma, beta, batch, C, eps);
+    } else {
+        ln_fwd_generic<<<(unsigned)batch, kTpb, 0, s>>>(y, mu, rstd, x, gamma, beta, C, eps);
+    }
+    nnk_after_launch(what, s);
+}
+
+void launch_layernorm_backward(float* grad_in, float* ggamma, float* gbeta, const float* grad_out,
+    const float* x, const float* gamma, const float* mu, const float* rstd, int batch, int C,
+    hipStream_t s) {
+    ln_backward_impl("launch_layernorm_backward", grad_in, ggamma, gbeta, grad_out, x, gamma, mu,
+        rstd, batch, C, nullptr, s);
+}
+
+void launch_layernorm_backward_ws(float* grad_in, float* ggamma, float* gbeta,
+    const float* grad_out, const float* x, const float* gamma, const float* mu,
+    const float* rstd, int batch, int C, float* workspace, hipStream_t s) {
+    if (!workspace) {
+        nnk_set_error(hipErrorInvalidValue, "launch_layernorm_backward_ws: null workspace");
+        return;
+    }
+    ln_backward_impl("launch_layernorm_backward_ws", grad_in, ggamma, gbeta, grad_out, x, gamma,
+        mu, rstd, batch, C, workspace, s);
+}
+
+size_t nnhip_layernorm_backward_workspace(int batch, int C) {
+    if (batch <= 0 || C <= 0) return 0;
+    // 2*P*C floats; P*C is padded to a float4 multiple so part_b stays aligned
+    const size_t pc = (size_t)num_chunks(batch) * C;
+    return 2 * ((pc + 3) / 4 * 4);
+}
+
+}  // extern "C"

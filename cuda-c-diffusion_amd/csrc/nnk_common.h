@@ -1,0 +1,261 @@
+// nnk_common.h -- device helpers shared by the gfx950 kernels of the launch layer.
+//
+// Numerical conventions (all kernels):
+//   * fp32 storage and arithmetic; the library is compiled with
+//     -ffp-contract=off, so a*b+c is a multiply and an add unless a kernel
+//     writes __builtin_fmaf explicitly.  The CPU oracle is compiled the same
+//     way, which makes the elementwise kernels bit-identical to it.
+//   * Division and sqrt are the correctly rounded IEEE operations (hipcc's
+//     default); rsqrtf maps to the hardware reciprocal square root.
+//   * Reductions are fixed-shape trees (DPP within a row of 16 lanes, lane
+//     reads across the 4 rows, LDS across waves), so every result is
+//     reproducible run to run.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "nn_hip.h"
+
+namespace nnk {
+
+// ---------------------------------------------------------------------------
+// Activation family.  Reference: src/kernels.cu:6-68.
+// The tanh is the Pade [7/6] approximant of the Lambert continued fraction
+// x/(1+x^2/(3+x^2/(5+x^2/(7+...)))), clamped to [-1,1]; the sigmoid is built
+// on it as (tanh(x/2)+1)/2.  Backward formulas are the reference's (the SiLU
+// derivative uses the approximate sigmoid, it is not the derivative of the
+// approximate SiLU).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float pade_tanh(float x) {
+    const float x2 = x * x;
+    const float p = x * (135135.0f + x2 * (17325.0f + x2 * (378.0f + x2)));
+    const float q = 135135.0f + x2 * (62370.0f + x2 * (3150.0f + x2 * 28.0f));
+    return fmaxf(-1.0f, fminf(1.0f, p / q));
+}
+
+__device__ __forceinline__ float pade_sigmoid(float x) {
+    return fmaxf(0.0f, fminf(1.0f, (pade_tanh(x * 0.5f) + 1.0f) * 0.5f));
+}
+
+constexpr float kGeluC = 0.7978845608f;
+constexpr float kGeluA = 0.044715f;
+constexpr float kMpSiluScale = 1.0f / 0.596f;
+
+template <int ACT>
+__device__ __forceinline__ float act_fwd(float v) {
+    if constexpr (ACT == ACT_RELU) {
+        return v > 0.0f ? v : 0.0f;
+    } else if constexpr (ACT == ACT_GELU) {
+        return 0.5f * v * (1.0f + pade_tanh(kGeluC * (v + kGeluA * v * v * v)));
+    } else if constexpr (ACT == ACT_SILU) {
+        return v * pade_sigmoid(v);
+    } else if constexpr (ACT == ACT_MP_SILU) {
+        return v * pade_sigmoid(v) * kMpSiluScale;
+    } else if constexpr (ACT == ACT_TANH) {
+        return pade_tanh(v);
+    } else {
+        return v;
+    }
+}
+
+template <int ACT>
+__device__ __forceinline__ float act_grad(float z) {
+    if constexpr (ACT == ACT_RELU) {
+        return z > 0.0f ? 1.0f : 0.0f;
+    } else if constexpr (ACT == ACT_TANH) {
+        const float t = pade_tanh(z);
+        return 1.0f - t * t;
+    } else if constexpr (ACT == ACT_SILU) {
+        const float s = pade_sigmoid(z);
+        return s * (1.0f + z * (1.0f - s));
+    } else if constexpr (ACT == ACT_MP_SILU) {
+        const float s = pade_sigmoid(z);
+        return s * (1.0f + z * (1.0f - s)) * kMpSiluScale;
+    } else if constexpr (ACT == ACT_GELU) {
+        const float u = kGeluC * (z + kGeluA * z * z * z);
+        const float t = pade_tanh(u);
+        const float du = kGeluC * (1.0f + 3.0f * kGeluA * z * z);
+        return 0.5f * (1.0f + t) + 0.5f * z * (1.0f - t * t) * du;
+    } else {
+        return 1.0f;
+    }
+}
+
+// Instantiate `F<ACT>` for a runtime activation; returns false for an unknown kind.
+#define NNK_ACT_DISPATCH(act, ACTV, ...)                              \
+    [&]() -> bool {                                                   \
+        switch (act) {                                                \
+        case ACT_IDENTITY: { constexpr int ACTV = ACT_IDENTITY; __VA_ARGS__; return true; } \
+        case ACT_RELU:     { constexpr int ACTV = ACT_RELU;     __VA_ARGS__; return true; } \
+        case ACT_GELU:     { constexpr int ACTV = ACT_GELU;     __VA_ARGS__; return true; } \
+        case ACT_SILU:     { constexpr int ACTV = ACT_SILU;     __VA_ARGS__; return true; } \
+        case ACT_TANH:     { constexpr int ACTV = ACT_TANH;     __VA_ARGS__; return true; } \
+        case ACT_MP_SILU:  { constexpr int ACTV = ACT_MP_SILU;  __VA_ARGS__; return true; } \
+        default: return false;                                        \
+        }                                                             \
+    }()
+
+// ---------------------------------------------------------------------------
+// Wave64 reductions.
+// ---------------------------------------------------------------------------
+constexpr int kWave = 64;
+
+// DPP controls (CDNA ISA): quad_perm [1,0,3,2], quad_perm [2,3,0,1],
+// row_half_mirror, row_mirror.
+constexpr int kDppQuadXor1 = 0xb1;
+constexpr int kDppQuadXor2 = 0x4e;
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __builtin_bit_cast(float,
+        __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf, 0xf, true));
+}
+
+__device__ __forceinline__ float lane_read(float v, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// Sum over the 64 lanes of a full wave; the result is wave-uniform.
+// Every lane of the wave must be active.
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dpp_mov<kDppQuadXor1>(v);
+    v += dpp_mov<kDppQuadXor2>(v);
+    v += dpp_mov<kDppRowHalfMirror>(v);
+    v += dpp_mov<kDppRowMirror>(v);
+    return ((lane_read(v, 0) + lane_read(v, 16)) + lane_read(v, 32)) + lane_read(v, 48);
+}
+
+// Sum over the lanes whose index agrees with this lane's modulo STRIDE
+// (STRIDE a power of two < 64); the result lands in every such lane.
+template <int STRIDE>
+__device__ __forceinline__ float wave_sum_strided(float v) {
+#pragma unroll
+    for (int m = STRIDE; m < kWave; m <<= 1) v += __shfl_xor(v, m, kWave);
+    return v;
+}
+
+// Block-wide sum of one value per thread.  `slots` is an LDS array of NW floats
+// used by this call only (a second reduction in the same kernel needs other
+// slots).  Every thread of the block must call it.
+template <int NW>
+__device__ __forceinline__ float block_sum(float v, float* slots) {
+    const float w = wave_sum(v);
+    if ((threadIdx.x & (kWave - 1)) == 0) slots[threadIdx.x / kWave] = w;
+    __syncthreads();
+    float s = slots[0];
+#pragma unroll
+    for (int i = 1; i < NW; ++i) s += slots[i];
+    return s;
+}
+
+// Two block sums sharing one barrier; slots holds 2*NW floats.
+template <int NW>
+__device__ __forceinline__ void block_sum2(float& a, float& b, float* slots) {
+    const float wa = wave_sum(a);
+    const float wb = wave_sum(b);
+    if ((threadIdx.x & (kWave - 1)) == 0) {
+        slots[threadIdx.x / kWave] = wa;
+        slots[NW + threadIdx.x / kWave] = wb;
+    }
+    __syncthreads();
+    float sa = slots[0], sb = slots[NW];
+#pragma unroll
+    for (int i = 1; i < NW; ++i) {
+        sa += slots[i];
+        sb += slots[NW + i];
+    }
+    a = sa;
+    b = sb;
+}
+
+// ---------------------------------------------------------------------------
+// XCD-aware block order.  The dispatcher deals consecutive workgroup ids to
+// the 8 XCDs of an MI355X in turn, and each XCD has its own L2.  Remapping
+// makes each XCD walk a contiguous range of work items in dispatch order, so
+// neighbouring items (which share cache lines, e.g. the 4 GroupNorm groups of
+// one 128-byte pixel slice) meet in the same L2.  A bijection on [0, n).
+// ---------------------------------------------------------------------------
+constexpr int kNumXcd = 8;
+
+__device__ __forceinline__ int xcd_swizzle(int bid, int n) {
+    const int xcd = bid % kNumXcd;
+    const int k = bid / kNumXcd;
+    const int per = n / kNumXcd;
+    const int rem = n % kNumXcd;
+    const int start = xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per;
+    return start + k;
+}
+
+// ---------------------------------------------------------------------------
+// Division by a runtime constant d (1 <= d < 2^31) for numerators < 2^31:
+// q = (umulhi(n, magic) + n) >> shift  (round-up magic-number method of
+// Granlund and Montgomery, "Division by invariant integers using
+// multiplication", PLDI 1994).
+// ---------------------------------------------------------------------------
+struct FastDiv {
+    uint32_t d;
+    uint32_t magic;
+    uint32_t shift;
+
+    __host__ __device__ FastDiv() : d(1), magic(0), shift(0) {}
+    __host__ explicit FastDiv(uint32_t divisor) : d(divisor) {
+        uint32_t s = 0;
+        while ((1ull << s) < divisor) ++s;
+        shift = s;
+        magic = (uint32_t)(((1ull << 32) * ((1ull << s) - divisor)) / divisor + 1ull);
+        if (divisor == 1) magic = 0;
+    }
+    __device__ __forceinline__ uint32_t div(uint32_t n) const {
+        const uint32_t t = __umulhi(n, magic);
+        return (uint32_t)(((uint64_t)t + n) >> shift);
+    }
+    __device__ __forceinline__ void divmod(uint32_t n, uint32_t& q, uint32_t& r) const {
+        q = div(n);
+        r = n - q * d;
+    }
+};
+
+// ---------------------------------------------------------------------------
+// 128-bit global accesses.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ __forceinline__ void st4(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 ld4_stream(const float* p) {
+    const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void st4_stream(float* p, float4 v) {
+    const f32x4 w = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(w, reinterpret_cast<f32x4*>(p));
+}
+
+__host__ __device__ __forceinline__ bool aligned16(const void* p) {
+    return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+
+}  // namespace nnk
+
+// ---------------------------------------------------------------------------
+// Host side of the launch layer: error record and scratch.
+// ---------------------------------------------------------------------------
+
+// Record an error (first one wins until read by nnhip_get_last_error).
+void nnk_set_error(int code, const char* fmt, ...);
+// Check the launch just made on `s` (and, in NNHIP_CHECK=1 mode, synchronise
+// the stream and abort on failure).  `what` names the launcher.
+void nnk_after_launch(const char* what, hipStream_t s);
+// Stream-ordered scratch for launchers that need partial sums.
+float* nnk_scratch_acquire(size_t n_floats, hipStream_t s, const char* what);
+void nnk_scratch_release(float* p, hipStream_t s);
+
+#define NNK_REQUIRE(cond, what, ...)                         \
+    do {                                                     \
+        if (!(cond)) {                                       \
+            nnk_set_error(hipErrorInvalidValue, __VA_ARGS__);\
+            return;                                          \
+        }                                                    \
+    } while (0)

@@ -1,0 +1,61 @@
+/* nn_hip_rt.h -- runtime plumbing exported beside the launch layer.
+ *
+ * The reference reaches device memory, copies and streams through the CUDA
+ * runtime directly (cudaMalloc in src/nn.h:54-59, cudaMemcpy in the modules).
+ * These few wrappers give foreign callers that do not link the HIP runtime
+ * themselves (Python via ctypes, the bench harness) the same facilities, plus
+ * the error record of the launch layer. They are plumbing, not part of the
+ * kernel path. Every function returns 0 on success and a HIP error code
+ * otherwise unless stated.
+ */
+#ifndef NN_HIP_RT_H
+#define NN_HIP_RT_H
+
+#include <stddef.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- error record of the launch layer (thread-local) ---- */
+/* Returns the first error recorded since the last call (0 = none) and clears
+   it; the message is copied into buf when buf != NULL. */
+int nnhip_get_last_error(char* buf, int buflen);
+
+/* ---- device ---- */
+int nnhip_device_count(void);
+int nnhip_set_device(int dev);
+/* Writes "<name>|<gcnArchName>|<CUs>|<memory bytes>" into buf. */
+int nnhip_device_info(char* buf, int buflen);
+
+/* ---- memory ---- */
+void* nnhip_malloc(size_t bytes); /* NULL on failure */
+int nnhip_free(void* p);
+int nnhip_memcpy_htod(void* dst, const void* src, size_t bytes);
+int nnhip_memcpy_dtoh(void* dst, const void* src, size_t bytes);
+int nnhip_memcpy_dtod(void* dst, const void* src, size_t bytes);
+int nnhip_memset(void* dst, int value, size_t bytes);
+int nnhip_memset_async(void* dst, int value, size_t bytes, hipStream_t s);
+int nnhip_device_synchronize(void);
+
+/* ---- streams and events ---- */
+hipStream_t nnhip_stream_create(void); /* NULL stream on failure */
+int nnhip_stream_destroy(hipStream_t s);
+int nnhip_stream_synchronize(hipStream_t s);
+hipEvent_t nnhip_event_create(void);
+int nnhip_event_destroy(hipEvent_t e);
+int nnhip_event_record(hipEvent_t e, hipStream_t s);
+int nnhip_event_synchronize(hipEvent_t e);
+float nnhip_event_elapsed_ms(hipEvent_t start, hipEvent_t stop); /* < 0 on error */
+
+/* ---- calibration ---- */
+/* dst[i] = src[i] for n floats with the same 128-bit vector access pattern
+   as the path's streaming kernels; used to scale HBM counters. */
+void nnhip_copy_f32(float* dst, const float* src, size_t n, hipStream_t s);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NN_HIP_RT_H */

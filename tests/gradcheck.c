@@ -1,0 +1,227 @@
+/* gradcheck.c -- finite-difference check of the host modules' backward passes,
+ * the method of the reference's only test (reference tests/gradcheck.c:1-321):
+ * L = <forward(in), g> for a fixed random cotangent g; central differences
+ * with EPS = 1e-3 on up to 20 sampled elements of the input and of every
+ * parameter tensor; pass iff |num - ana| <= ATOL + rtol*(|num| + |ana|) with
+ * ATOL = 1e-2 and rtol = 2e-2 (reference gradcheck.c:15-21, 51-56, 290-306).
+ * Magnitude-preserving layers normalise their weights in place, so a warm-up
+ * forward projects them first and every numeric forward restores the snapshot.
+ *
+ * Built as tests/_build/libgradcheck.so; nn_gradcheck_run() returns the number
+ * of failing modules (0 = all pass).  Needs a GPU.
+ */
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "nn_modules.h"
+
+#define K_SAMPLES 20
+#define GC_EPS 1.0e-3f
+#define GC_ATOL 1.0e-2
+
+static Context g_ctx;
+static int g_verbose = 1;
+
+static void d2h(float* h, const float* d, int n)
+{
+    NN_HIP_CHECK(hipMemcpy(h, d, (size_t)n * sizeof(float), hipMemcpyDeviceToHost));
+}
+
+static void h2d(float* d, const float* h, int n)
+{
+    NN_HIP_CHECK(hipMemcpy(d, h, (size_t)n * sizeof(float), hipMemcpyHostToDevice));
+}
+
+static double dot_host(const float* a, const float* b, int n)
+{
+    double s = 0.0;
+    for (int i = 0; i < n; ++i) s += (double)a[i] * (double)b[i];
+    return s;
+}
+
+static double viol_ratio(double num, double ana, double rtol)
+{
+    return fabs(num - ana) / (GC_ATOL + rtol * (fabs(num) + fabs(ana)));
+}
+
+static int pick_indices(int size, int* idx)
+{
+    if (size <= K_SAMPLES) {
+        for (int i = 0; i < size; ++i) idx[i] = i;
+        return size;
+    }
+    for (int i = 0; i < K_SAMPLES; ++i) idx[i] = (int)(nn_rng_uniform(&g_ctx) * size) % size;
+    return K_SAMPLES;
+}
+
+static double loss_at(Module* m, const float* d_in, float* d_out, float* h_out, const float* h_g,
+    int batch, int n_out)
+{
+    m->forward(m, d_in, d_out, batch, &g_ctx);
+    d2h(h_out, d_out, n_out);
+    return dot_host(h_out, h_g, n_out);
+}
+
+static void restore(const ParamList* pl, float** snap)
+{
+    for (int k = 0; k < pl->count; ++k) h2d(pl->items[k].param, snap[k], pl->items[k].size);
+}
+
+static int check_module(const char* tag, Module* m, int batch, double rtol)
+{
+    int n_in = batch * m->in_dim, n_out = batch * m->out_dim;
+    float* d_in = nn_device_alloc((size_t)n_in);
+    float* d_out = nn_device_alloc((size_t)n_out);
+    float* d_gout = nn_device_alloc((size_t)n_out);
+    float* d_gin = nn_device_alloc((size_t)n_in);
+    float* h_in = (float*)malloc((size_t)n_in * sizeof(float));
+    float* h_out = (float*)malloc((size_t)n_out * sizeof(float));
+    float* h_g = (float*)malloc((size_t)n_out * sizeof(float));
+    float* h_gin = (float*)malloc((size_t)n_in * sizeof(float));
+    for (int i = 0; i < n_in; ++i) h_in[i] = (float)nn_rng_normal(&g_ctx);
+    for (int i = 0; i < n_out; ++i) h_g[i] = (float)nn_rng_normal(&g_ctx);
+    h2d(d_in, h_in, n_in);
+    h2d(d_gout, h_g, n_out);
+
+    ParamList pl;
+    param_list_init(&pl);
+    if (m->parameters) m->parameters(m, &pl);
+
+    m->forward(m, d_in, d_out, batch, &g_ctx); /* warm-up: project MP weights */
+    NN_HIP_CHECK(hipDeviceSynchronize());
+    float** snap = (float**)calloc((size_t)(pl.count > 0 ? pl.count : 1), sizeof(float*));
+    for (int k = 0; k < pl.count; ++k) {
+        snap[k] = (float*)malloc((size_t)pl.items[k].size * sizeof(float));
+        d2h(snap[k], pl.items[k].param, pl.items[k].size);
+        NN_HIP_CHECK(hipMemset(pl.items[k].grad, 0, (size_t)pl.items[k].size * sizeof(float)));
+    }
+    m->forward(m, d_in, d_out, batch, &g_ctx);
+    m->backward(m, d_in, d_out, d_gout, d_gin, batch, &g_ctx);
+    NN_HIP_CHECK(hipDeviceSynchronize());
+    d2h(h_gin, d_gin, n_in);
+    float** ana = (float**)calloc((size_t)(pl.count > 0 ? pl.count : 1), sizeof(float*));
+    for (int k = 0; k < pl.count; ++k) {
+        ana[k] = (float*)malloc((size_t)pl.items[k].size * sizeof(float));
+        d2h(ana[k], pl.items[k].grad, pl.items[k].size);
+    }
+
+    double worst = 0.0, worst_num = 0.0, worst_ana = 0.0;
+    const char* where = "input";
+    int worst_k = -1, worst_j = -1;
+    int idx[K_SAMPLES];
+
+    int n = pick_indices(n_in, idx);
+    for (int s = 0; s < n; ++s) {
+        int j = idx[s];
+        float save = h_in[j];
+        restore(&pl, snap);
+        h_in[j] = save + GC_EPS;
+        h2d(d_in, h_in, n_in);
+        double lp = loss_at(m, d_in, d_out, h_out, h_g, batch, n_out);
+        restore(&pl, snap);
+        h_in[j] = save - GC_EPS;
+        h2d(d_in, h_in, n_in);
+        double lm = loss_at(m, d_in, d_out, h_out, h_g, batch, n_out);
+        h_in[j] = save;
+        double num = (lp - lm) / (2.0 * GC_EPS);
+        double e = viol_ratio(num, h_gin[j], rtol);
+        if (e > worst) {
+            worst = e;
+            where = "input";
+            worst_k = -1;
+            worst_j = j;
+            worst_num = num;
+            worst_ana = h_gin[j];
+        }
+    }
+    h2d(d_in, h_in, n_in);
+
+    for (int k = 0; k < pl.count; ++k) {
+        int sz = pl.items[k].size;
+        n = pick_indices(sz, idx);
+        for (int s = 0; s < n; ++s) {
+            int j = idx[s];
+            float base = snap[k][j];
+            restore(&pl, snap);
+            float vp = base + GC_EPS;
+            h2d(pl.items[k].param + j, &vp, 1);
+            double lp = loss_at(m, d_in, d_out, h_out, h_g, batch, n_out);
+            restore(&pl, snap);
+            float vm = base - GC_EPS;
+            h2d(pl.items[k].param + j, &vm, 1);
+            double lm = loss_at(m, d_in, d_out, h_out, h_g, batch, n_out);
+            double num = (lp - lm) / (2.0 * GC_EPS);
+            double e = viol_ratio(num, ana[k][j], rtol);
+            if (e > worst) {
+                worst = e;
+                where = "param";
+                worst_k = k;
+                worst_j = j;
+                worst_num = num;
+                worst_ana = ana[k][j];
+            }
+        }
+    }
+    restore(&pl, snap);
+
+    int pass = worst <= 1.0;
+    if (g_verbose || !pass) {
+        printf("  [%s] %-24s worst_ratio=%.3f (%s", pass ? "PASS" : "FAIL", tag, worst, where);
+        if (worst_k >= 0) printf(" #%d", worst_k);
+        printf(")\n");
+        if (!pass) printf("         at idx %d: numeric=%+.6e analytic=%+.6e\n", worst_j, worst_num, worst_ana);
+        fflush(stdout);
+    }
+    for (int k = 0; k < pl.count; ++k) {
+        free(snap[k]);
+        free(ana[k]);
+    }
+    free(snap);
+    free(ana);
+    param_list_free(&pl);
+    m->free(m);
+    free(h_in);
+    free(h_out);
+    free(h_g);
+    free(h_gin);
+    (void)hipFree(d_in);
+    (void)hipFree(d_out);
+    (void)hipFree(d_gout);
+    (void)hipFree(d_gin);
+    return pass ? 0 : 1;
+}
+
+/* Returns the number of failing modules.  Module list: the reference's
+ * gradcheck configs on the fused-kernel path (gradcheck.c:290-306), plus the
+ * fused GroupNorm+activation module and GroupNorm shapes that take the
+ * register-resident kernels. */
+int nn_gradcheck_run(int verbose)
+{
+    g_verbose = verbose;
+    nn_context_init(&g_ctx, 42ull, (hipStream_t)0);
+    const int B = 2;
+    int fails = 0;
+    fails += check_module("mp_linear", mp_linear_create(&g_ctx, 12, 8, 1.0f), B, 2e-2);
+    fails += check_module("act_silu", activation_create(8, ACT_SILU), B, 2e-2);
+    fails += check_module("act_gelu", activation_create(8, ACT_GELU), B, 2e-2);
+    fails += check_module("act_tanh", activation_create(8, ACT_TANH), B, 2e-2);
+    fails += check_module("act_mp_silu", activation_create(8, ACT_MP_SILU), B, 2e-2);
+    fails += check_module("act_relu", activation_create(8, ACT_RELU), B, 2e-2);
+    fails += check_module("layernorm", layernorm_create(16, B), B, 2e-2);
+    fails += check_module("layernorm_c256", layernorm_create(256, B), B, 2e-2);
+    fails += check_module("groupnorm", spatial_groupnorm_create(8, 4, 6, 6, B), B, 2e-2);
+    fails += check_module("groupnorm_c32_g8", spatial_groupnorm_create(32, 8, 8, 8, B), B, 2e-2);
+    fails += check_module("groupnorm_silu", spatial_groupnorm_act_create(8, 4, 6, 6, B, ACT_SILU), B, 2e-2);
+    fails += check_module("groupnorm_silu_c32", spatial_groupnorm_act_create(32, 8, 8, 8, B, ACT_SILU), B, 2e-2);
+    fails += check_module("conv3x3", conv2d_create(&g_ctx, 3, 4, 3, 1, 1, 6, 6, B, 0, 1.0f), B, 2e-2);
+    fails += check_module("conv3x3_mp", conv2d_create(&g_ctx, 3, 4, 3, 1, 1, 6, 6, B, 1, 1.0f), B, 2e-2);
+    fails += check_module("conv1x1_mp", conv2d_create(&g_ctx, 4, 6, 1, 1, 0, 5, 5, B, 1, 1.0f), B, 2e-2);
+    fails += check_module("conv3x3_s2", conv2d_create(&g_ctx, 4, 4, 3, 2, 1, 7, 7, B, 0, 1.0f), B, 2e-2);
+    nn_context_destroy(&g_ctx);
+    printf("%s (%d failing module%s)\n", fails ? "GRADCHECK FAILED" : "ALL GRADIENTS OK", fails,
+        fails == 1 ? "" : "s");
+    fflush(stdout);
+    return fails;
+}

@@ -1,0 +1,21 @@
+"""Finite-difference gradcheck of the host modules (the reference's own test
+method, reference tests/gradcheck.c), run through tests/_build/libgradcheck.so."""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+LIB = Path(__file__).resolve().parent / "_build" / "libgradcheck.so"
+
+
+def test_module_gradcheck(L):
+    assert LIB.exists(), f"{LIB} missing: run __graft_entry__.build()"
+    gc = ctypes.CDLL(str(LIB))
+    gc.nn_gradcheck_run.restype = ctypes.c_int
+    gc.nn_gradcheck_run.argtypes = [ctypes.c_int]
+    fails = gc.nn_gradcheck_run(1)
+    assert fails == 0, f"{fails} module(s) failed the gradcheck"
