@@ -39,6 +39,59 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+def cfg5_tensor_sizes(channels=(64, 128, 256, 448, 512), emb_dim=512, c_in=3, c_out=3, res_blocks=2,
+                      floor=64):
+    """Parameter-tensor sizes of BASELINE cfg5's DDPM-UNet-like list, in the
+    reference's ParamList order: the time-embedding MLP (src/diffusion/ddpm.c:
+    103-108, 77-81), then ddpm_unet_parameters (src/ddpm_unet.c:239-255) with
+    conv_residual's gn1, conv1, time_proj, gn2, conv2 (src/conv_residual.c:
+    68-76), conv weight then bias (src/conv2d.c:68-76), the plain attention's
+    Wq..Wo then bq..bo (src/attention.c:199-216).  `res_blocks` blocks per
+    level on each side; sizes floored at `floor`.  Default: 212 tensors,
+    35,111,104 elements."""
+    out = []
+
+    def add(n):
+        out.append(max(n, floor))
+
+    def conv(ci, co, k):
+        add(k * k * ci * co)
+        add(co)
+
+    def linear(i, o):
+        add(i * o)
+        add(o)
+
+    def res_block(c):
+        add(c), add(c)
+        conv(c, c, 3)
+        linear(emb_dim, c)
+        add(c), add(c)
+        conv(c, c, 3)
+
+    levels = len(channels) - 1
+    linear(emb_dim, emb_dim)
+    linear(emb_dim, emb_dim)
+    conv(c_in, channels[0], 3)
+    for i in range(levels):
+        for _ in range(res_blocks):
+            res_block(channels[i])
+        conv(channels[i], channels[i + 1], 1)
+    cb = channels[levels]
+    res_block(cb)
+    for _ in range(4):
+        add(cb * cb)
+    for _ in range(4):
+        add(cb)
+    res_block(cb)
+    for i in reversed(range(levels)):
+        conv(channels[i + 1] + channels[i], channels[i], 1)
+        for _ in range(res_blocks):
+            res_block(channels[i])
+    conv(channels[0], c_out, 3)
+    return out
+
+
 def make_inputs(B, HW, C, seed):
     rng = np.random.default_rng(seed)
     x = rng.standard_normal((B, HW, C), dtype=np.float32)

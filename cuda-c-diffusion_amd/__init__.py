@@ -115,10 +115,13 @@ def header_functions() -> list[str]:
     for h in sorted(INCLUDE_DIR.glob("*.h")):
         text = h.read_text()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-        text = re.sub(r"#define[^\n]*(\\\n[^\n]*)*", "", text)
+        text = text.replace("\\\n", " ")  # join macro continuation lines
+        text = re.sub(r"^\s*#[^\n]*", "", text, flags=re.M)
         for m in re.finditer(r"\b([A-Za-z_][A-Za-z0-9_]*)\s*\(([^;{}]*)\)\s*;", text):
             name = m.group(1)
             if name in ("if", "while", "for", "return", "sizeof"):
+                continue
+            if m.group(2).lstrip().startswith("*"):  # function-pointer member: void (*f)(...)
                 continue
             names.append(name)
     return names

@@ -1,0 +1,114 @@
+"""The drop-in boundary, checked without a GPU: the library loads, exports every
+function include/*.h declares, and refuses impossible arguments on the host
+(reference launchers: src/nn.h:348-466) before any device work is queued."""
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def _exported(lib_path: Path) -> set[str]:
+    out = subprocess.run(["nm", "-D", "--defined-only", str(lib_path)], capture_output=True, text=True,
+                         check=True).stdout
+    return {line.split()[-1] for line in out.splitlines() if line.strip()}
+
+
+def test_library_exports_every_declared_function(nn):
+    declared = set(nn.header_functions())
+    assert len(declared) > 60, sorted(declared)
+    exported = _exported(nn.LIB_PATH)
+    missing = sorted(declared - exported)
+    assert not missing, f"declared in include/*.h but not exported: {missing}"
+
+
+def test_reference_launcher_set_is_declared(nn):
+    """Every on-path launcher of the reference's extern "C" block (src/nn.h:348-466)."""
+    ref_names = {
+        "launch_add_bias", "launch_bias_grad", "launch_sgd_step", "launch_activation_forward",
+        "launch_activation_backward", "launch_adam_step", "launch_weight_normalize",
+        "launch_weight_normalize_backward", "launch_scale_by_scalar", "launch_mp_sum", "launch_weighted_sum",
+        "launch_mp_cat", "launch_mp_channel_cat", "launch_mp_channel_split", "launch_mp_fourier",
+        "launch_sinusoidal", "launch_layernorm_forward", "launch_layernorm_backward",
+        "launch_groupnorm_forward", "launch_groupnorm_backward", "launch_im2col", "launch_col2im",
+    }
+    assert ref_names <= set(nn.header_functions())
+
+
+def test_launchers_keep_reference_argument_order(nn):
+    """Argument lists of the reference-named launchers: same count and kinds
+    (pointer / int / float), with the stream last."""
+    text = (ROOT / "include" / "nn_hip.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    sig = {m.group(1): [a.strip() for a in m.group(2).split(",")]
+           for m in re.finditer(r"void\s+(launch_\w+)\s*\(([^;]*)\)\s*;", text)}
+    expect = {
+        # kinds per argument: p = pointer, i = int, f = float, s = stream (reference nn.h:348-466)
+        "launch_groupnorm_forward": "ppppppiiiifs",
+        "launch_groupnorm_backward": "ppppppppiiiis",
+        "launch_layernorm_forward": "ppppppiifs",
+        "launch_layernorm_backward": "ppppppppiis",
+        "launch_activation_forward": "ppiis",
+        "launch_activation_backward": "pppiis",
+        "launch_adam_step": "ppppffffffis",
+        "launch_weight_normalize": "piifs",
+        "launch_weight_normalize_backward": "ppppiis",
+        "launch_weighted_sum": "pppffis",
+        "launch_mp_sum": "pppfis",
+        "launch_mp_cat": "pppfiiis",
+        "launch_mp_channel_cat": "pppfiiis",
+        "launch_mp_channel_split": "pppfiiis",
+        "launch_mp_fourier": "ppppiis",
+        "launch_sinusoidal": "ppiifs",
+        "launch_im2col": "ppiiiiiiiiis",
+        "launch_col2im": "ppiiiiiiiiis",
+    }
+
+    def kind(a: str) -> str:
+        if "hipStream_t" in a:
+            return "s"
+        if "*" in a:
+            return "p"
+        if a.startswith("float"):
+            return "f"
+        return "i"  # int and the Activation enum
+
+    for name, k in expect.items():
+        got = "".join(kind(a) for a in sig[name])
+        assert got == k, (name, got, k)
+
+
+def test_host_refusals_record_an_error(nn):
+    """Shapes the kernels cannot take are refused on the host and recorded in
+    the error record (the reference would launch and read out of bounds)."""
+    L = nn.lib()
+    L.last_error()  # clear
+    dummy = ctypes.c_void_p(16)  # never dereferenced: the shape check comes first
+    cases = [
+        ("launch_groupnorm_forward", (dummy, dummy, dummy, dummy, dummy, dummy, 1, 4, 10, 4, 1e-5, None)),
+        ("launch_groupnorm_act_forward", (dummy, dummy, dummy, dummy, dummy, dummy, 1, 4, 8, 4, 1e-5, 99, None)),
+        ("launch_layernorm_forward", (dummy, dummy, dummy, dummy, dummy, dummy, 2, 0, 1e-5, None)),
+        ("launch_im2col", (dummy, dummy, 1, 4, 4, 2, 3, 1, 1, 5, 4, None)),
+        ("launch_sinusoidal", (dummy, dummy, 2, 1, 9.2, None)),
+        ("launch_weight_normalize", (dummy, -1, 4, 1e-4, None)),
+    ]
+    for name, args in cases:
+        with pytest.raises(nn.NnHipError):
+            L.call(name, *args)
+    code, _ = L.last_error()
+    assert code == 0  # the record is cleared by each read
+
+
+def test_zero_sized_calls_are_no_ops(nn):
+    L = nn.lib()
+    null = None
+    L.launch_activation_forward(null, null, 0, nn.ACT_SILU, None)
+    L.launch_weighted_sum(null, null, null, 1.0, 2.0, 0, None)
+    L.launch_mp_fourier(null, null, null, null, 0, 16, None)
+    L.launch_im2col(null, null, 0, 4, 4, 2, 3, 1, 1, 4, 4, None)
+    assert L.last_error()[0] == 0

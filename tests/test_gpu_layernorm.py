@@ -1,0 +1,83 @@
+"""LayerNorm row (reference src/kernels.cu:491-567, launchers 594-616; module
+src/layernorm.c): HIP path through the C-ABI vs the oracle.  cfg4's
+[256*16*16, 256] attention-token shape plus the fast path's edges (C not a
+multiple of 4, C above 1024, misaligned pointers, one row)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from helpers import TOL, rel_err
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(256 * 16 * 16, 256), (2, 16), (37, 48), (5, 1000), (3, 1030), (64, 4), (1, 7), (130, 2048), (1, 1)]
+
+
+def _inputs(rng, R, C):
+    x = (0.5 + rng.standard_normal((R, C))).astype(np.float32)
+    gamma = (1 + 0.1 * rng.standard_normal(C)).astype(np.float32)
+    beta = (0.1 * rng.standard_normal(C)).astype(np.float32)
+    dy = rng.standard_normal((R, C)).astype(np.float32)
+    return x, gamma, beta, dy
+
+
+def _param_floor(dy, x, mu, rs):
+    xh = (x.astype(np.float64) - mu[:, None]) * rs[:, None]
+    d = dy.astype(np.float64)
+    return np.sqrt(np.sum((d * xh) ** 2, axis=0)), np.sqrt(np.sum(d * d, axis=0))
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_layernorm_forward_backward(L, orc, rng, shape):
+    R, C = shape
+    print(f"[case] layernorm {shape}", flush=True)
+    x, gamma, beta, dy = _inputs(rng, R, C)
+    xd, yd, gd, bd = L.to_device(x), L.alloc(x.size), L.to_device(gamma), L.to_device(beta)
+    mu, rs = L.alloc(R), L.alloc(R)
+    L.launch_layernorm_forward(yd.p, mu.p, rs.p, xd.p, gd.p, bd.p, R, C, 1e-5, None)
+    L.sync()
+    y_ref, mu_ref, rs_ref = orc.layernorm_forward(x, gamma, beta, 1e-5)
+    assert rel_err(yd.download(shape=x.shape), y_ref) <= TOL
+    assert rel_err(mu.download(), mu_ref) <= TOL
+    assert rel_err(rs.download(), rs_ref) <= TOL
+
+    dyd, dxd, ggd, gbd = L.to_device(dy), L.alloc(x.size), L.alloc(C), L.alloc(C)
+    mud, rsd = L.to_device(mu_ref), L.to_device(rs_ref)
+    L.launch_layernorm_backward(dxd.p, ggd.p, gbd.p, dyd.p, xd.p, gd.p, mud.p, rsd.p, R, C, None)
+    L.sync()
+    dx_ref, gg_ref, gb_ref = orc.layernorm_backward(dy, x, gamma, mu_ref, rs_ref)
+    fg, fb = _param_floor(dy, x, mu_ref, rs_ref)
+    assert rel_err(dxd.download(shape=x.shape), dx_ref) <= TOL
+    assert rel_err(ggd.download(), gg_ref, floor=fg) <= TOL
+    assert rel_err(gbd.download(), gb_ref, floor=fb) <= TOL
+
+    # workspace variant: identical results
+    ws = L.alloc(max(1, L.nnhip_layernorm_backward_workspace(R, C)))
+    dx2, gg2, gb2 = L.alloc(x.size), L.alloc(C), L.alloc(C)
+    L.launch_layernorm_backward_ws(dx2.p, gg2.p, gb2.p, dyd.p, xd.p, gd.p, mud.p, rsd.p, R, C, ws.p, None)
+    L.sync()
+    assert np.array_equal(dx2.download(), dxd.download())
+    assert np.array_equal(gg2.download(), ggd.download())
+    assert np.array_equal(gb2.download(), gbd.download())
+
+
+def test_layernorm_misaligned(L, orc, rng):
+    R, C = 33, 64
+    x, gamma, beta, dy = _inputs(rng, R, C)
+    xd, yd = L.alloc(x.size + 1), L.alloc(x.size + 1)
+    xd.upload(np.concatenate([[0.0], x.ravel()]).astype(np.float32))
+    gd, bd, mu, rs = L.to_device(gamma), L.to_device(beta), L.alloc(R), L.alloc(R)
+    L.launch_layernorm_forward(yd.offset(1), mu.p, rs.p, xd.offset(1), gd.p, bd.p, R, C, 1e-5, None)
+    L.sync()
+    y_ref, _, _ = orc.layernorm_forward(x, gamma, beta, 1e-5)
+    assert rel_err(yd.download()[1:].reshape(R, C), y_ref) <= TOL
+
+
+def test_layernorm_empty_batch_zeroes_param_grads(L):
+    C = 16
+    gg, gb = L.to_device(np.full(C, 3.0, np.float32)), L.to_device(np.full(C, 3.0, np.float32))
+    d = L.alloc(16)
+    L.launch_layernorm_backward(d.p, gg.p, gb.p, d.p, d.p, d.p, d.p, d.p, 0, C, None)
+    L.sync()
+    assert np.all(gg.download() == 0) and np.all(gb.download() == 0)

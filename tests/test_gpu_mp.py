@@ -1,0 +1,99 @@
+"""Magnitude-preserving rows: mp_cat / mp_channel_cat / mp_channel_split
+(reference src/kernels.cu:318-328, 368-378, 1215-1232, 1251-1278) bit-exact,
+and forced weight normalisation with gain, forward and backward
+(src/kernels.cu:255-297, 330-344; callers src/mp_linear.c:12-38,
+src/conv2d.c:24-55) within 1e-5.  Shapes are BASELINE cfg2's."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from helpers import TOL, assert_bits_equal, rel_err
+
+pytestmark = pytest.mark.gpu
+
+R2 = 128 * 32 * 32  # cfg2 pixels
+
+
+@pytest.mark.parametrize("rows,Na,Nb,t", [(R2, 128, 128, 0.3), (7, 3, 5, 0.3), (1000, 64, 192, 0.5),
+                                          (33, 1, 1, 0.7)])
+def test_mp_cat_bit_exact(L, orc, rng, rows, Na, Nb, t):
+    print(f"[case] mp_cat rows={rows} Na={Na} Nb={Nb}", flush=True)
+    a = rng.standard_normal((rows, Na), dtype=np.float32)
+    b = rng.standard_normal((rows, Nb), dtype=np.float32)
+    ad, bd, od = L.to_device(a), L.to_device(b), L.alloc(rows * (Na + Nb))
+    L.launch_mp_cat(od.p, ad.p, bd.p, t, rows, Na, Nb, None)
+    L.sync()
+    ref = orc.mp_cat(a, b, t)
+    assert_bits_equal(od.download(shape=ref.shape), ref, "mp_cat")
+    # the NHWC channel form is the same placement over spatial = N*H*W pixels
+    od.fill_bytes(0)
+    L.launch_mp_channel_cat(od.p, ad.p, bd.p, t, rows, Na, Nb, None)
+    L.sync()
+    assert_bits_equal(od.download(shape=ref.shape), ref, "mp_channel_cat")
+
+
+@pytest.mark.parametrize("rows,Ca,Cb,t", [(R2, 128, 128, 0.3), (7, 3, 5, 0.3), (1000, 64, 192, 0.5)])
+def test_mp_channel_split_bit_exact(L, orc, rng, rows, Ca, Cb, t):
+    g = rng.standard_normal((rows, Ca + Cb), dtype=np.float32)
+    gd, gad, gbd = L.to_device(g), L.alloc(rows * Ca), L.alloc(rows * Cb)
+    L.launch_mp_channel_split(gad.p, gbd.p, gd.p, t, rows, Ca, Cb, None)
+    L.sync()
+    ga, gb = orc.mp_split(g, Ca, Cb, t)
+    assert_bits_equal(gad.download(shape=ga.shape), ga, "grad_a")
+    assert_bits_equal(gbd.download(shape=gb.shape), gb, "grad_b")
+
+
+@pytest.mark.parametrize("n_in,n_out", [(1152, 128), (12, 8), (27, 4), (4, 6), (1, 1), (300, 1000)])
+def test_weight_normalize_forward(L, orc, rng, n_in, n_out):
+    W = rng.standard_normal((n_in, n_out)).astype(np.float32)
+    Wd = L.to_device(W)
+    L.launch_weight_normalize(Wd.p, n_in, n_out, 1e-4, None)
+    L.sync()
+    assert rel_err(Wd.download(shape=W.shape), orc.weight_normalize(W, 1e-4)) <= TOL
+    # repeated forwards converge to |W_j|^2 = 1 - eps (the in-place forced form)
+    for _ in range(20):
+        L.launch_weight_normalize(Wd.p, n_in, n_out, 1e-4, None)
+    L.sync()
+    ss = np.sum(Wd.download(shape=W.shape).astype(np.float64) ** 2, axis=0)
+    np.testing.assert_allclose(ss, 1 - 1e-4, rtol=5e-6)
+
+
+@pytest.mark.parametrize("n_in,n_out", [(1152, 128), (12, 8), (4, 6), (300, 1000)])
+def test_weight_normalize_backward(L, orc, rng, n_in, n_out):
+    W = rng.standard_normal((n_in, n_out)).astype(np.float32)
+    Wn = orc.weight_normalize(W, 1e-4)
+    M = rng.standard_normal((n_in, n_out)).astype(np.float32)
+    gain = np.array([1.3], np.float32)
+    gWd, Wnd, gaind = L.to_device(M), L.to_device(Wn), L.to_device(gain)
+    gg = L.to_device(np.array([0.25], np.float32))  # accumulated onto, as the reference's atomicAdd
+    L.launch_weight_normalize_backward(gWd.p, Wnd.p, gaind.p, gg.p, n_in, n_out, None)
+    L.sync()
+    gW_ref, gg_ref = orc.weight_normalize_backward(M, Wn, float(gain[0]), 0.25)
+    terms = (Wn.astype(np.float64) * M)
+    dots = terms.sum(axis=0)
+    # floor for gW: its RMS; for the gain gradient: sqrt of the summed squared terms
+    assert rel_err(gWd.download(shape=M.shape), gW_ref) <= TOL
+    floor = float(np.sqrt(np.sum(terms ** 2)) + 0.25)
+    assert abs(float(gg.download()[0]) - gg_ref) / max(abs(gg_ref), floor) <= TOL
+    assert abs(gg_ref - (0.25 + dots.sum())) < 1e-3
+
+
+def test_mp_linear_weight_chain(L, orc, rng):
+    """The mp_linear sequence (src/mp_linear.c:12-38) minus the GEMM: normalise
+    in place, then the backward on the normalised weight with the gain buffer
+    zeroed by the caller."""
+    n_in, n_out = 1152, 128
+    W = rng.standard_normal((n_in, n_out)).astype(np.float32)
+    Wd = L.to_device(W)
+    L.launch_weight_normalize(Wd.p, n_in, n_out, 1e-4, None)
+    M = rng.standard_normal((n_in, n_out)).astype(np.float32)
+    gWd = L.to_device(M)
+    gain, gg = L.to_device(np.array([1.0], np.float32)), L.alloc(1)
+    gg.fill_bytes(0)
+    L.launch_weight_normalize_backward(gWd.p, Wd.p, gain.p, gg.p, n_in, n_out, None)
+    L.sync()
+    Wn_ref = orc.weight_normalize(W, 1e-4)
+    gW_ref, gg_ref = orc.weight_normalize_backward(M, Wn_ref, 1.0, 0.0)
+    assert rel_err(gWd.download(shape=M.shape), gW_ref) <= TOL
+    assert abs(float(gg.download()[0]) - gg_ref) <= TOL * max(abs(gg_ref), float(np.sqrt(n_in * n_out)))
