@@ -34,6 +34,14 @@ METRIC = "GroupNorm+SiLU fwd+bwd µs and HBM GB/s (% of 8 TB/s peak), N=256 64×
 HBM_PEAK_GBS = 8000.0
 SEED = 410293
 
+# HBM bytes per launch of the dominant (backward) kernel at the north-star
+# shape, from `rocprofv3 --pmc FETCH_SIZE` and `--pmc WRITE_SIZE` runs of this
+# bench, scaled by a plain copy's counters (FETCH x2, WRITE x1); the commands
+# and raw values are in profiles/gn_silu_fwd_bwd_n256_64x64x256.md.
+# Re-measure when the kernel changes.
+TRAFFIC_BYTES = {"gn_bwd_reg<1024, 8, 2, 3>": (2 * 1_056_987 + 1_050_046) * 1024}
+ROOFLINE_KERNEL = "gn_bwd_reg<1024, 8, 2, 3>"
+
 
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
@@ -127,6 +135,182 @@ def cpu_baseline(x, dy, gamma, beta, G, sample_b, reps=1):
     }
 
 
+
+# ---------------------------------------------------------------------------
+# --suite: every hot-path row at its BASELINE config, timed on the GPU.
+# One JSON line per row on stdout: µs per launch sequence (median of reps,
+# HIP events on the launch stream), algorithmic bytes, GB/s and the fraction
+# of the 8 TB/s HBM roofline.  Inputs are seeded synthetic data of the
+# config's shape, resident in HBM before timing.
+# ---------------------------------------------------------------------------
+class _Timer:
+    def __init__(self, L, stream):
+        self.L, self.stream = L, stream
+        self.ev = [L.dll.nnhip_event_create() for _ in range(2)]
+
+    def median_us(self, fn, reps=20, warmup=3):
+        L = self.L
+        for _ in range(warmup):
+            fn()
+        L.dll.nnhip_stream_synchronize(self.stream)
+        out = []
+        for _ in range(reps):
+            L.dll.nnhip_event_record(self.ev[0], self.stream)
+            fn()
+            L.dll.nnhip_event_record(self.ev[1], self.stream)
+            L.dll.nnhip_event_synchronize(self.ev[1])
+            out.append(1e3 * L.dll.nnhip_event_elapsed_ms(self.ev[0], self.ev[1]))
+        L.check("suite")
+        return float(np.median(out))
+
+
+def _row(name, cfg, us, algo_bytes, note=""):
+    gbs = algo_bytes / (us * 1e-6) / 1e9 if algo_bytes else None
+    rec = {"row": name, "config": cfg, "us": round(us, 2), "algorithmic_bytes": int(algo_bytes),
+           "GB_s": round(gbs, 1) if gbs else None, "hbm_frac": round(gbs / HBM_PEAK_GBS, 4) if gbs else None}
+    if note:
+        rec["note"] = note
+    print(json.dumps(rec), flush=True)
+    log(f"[suite] {name:34s} {us:9.2f} us  " + (f"{gbs:7.0f} GB/s ({gbs / HBM_PEAK_GBS:.3f})" if gbs else ""))
+
+
+def run_suite(L, nn, reps):
+    rng = np.random.default_rng(SEED)
+    stream = L.dll.nnhip_stream_create()
+    T = _Timer(L, stream)
+    f32 = np.float32
+
+    def dev(a):
+        return L.to_device(np.ascontiguousarray(a, dtype=f32))
+
+    # cfg1: GN(32)+SiLU [8,32,32,128]
+    B, HW, C, G = 8, 1024, 128, 32
+    x, dy = dev(rng.standard_normal(B * HW * C)), dev(rng.standard_normal(B * HW * C))
+    g, bt = dev(1 + 0.1 * rng.standard_normal(C)), dev(0.1 * rng.standard_normal(C))
+    y, dx, mu, rs, gg, gb = L.alloc(B * HW * C), L.alloc(B * HW * C), L.alloc(B * G), L.alloc(B * G), L.alloc(C), \
+        L.alloc(C)
+    ws = L.alloc(L.nnhip_groupnorm_backward_workspace(B, HW, C, G))
+
+    def gn1():
+        L.launch_groupnorm_act_forward(y.p, mu.p, rs.p, x.p, g.p, bt.p, B, HW, C, G, 1e-5, 3, stream)
+        L.launch_groupnorm_act_backward_ws(dx.p, gg.p, gb.p, dy.p, x.p, g.p, bt.p, mu.p, rs.p, B, HW, C, G, 3,
+                                           ws.p, stream)
+    _row("gn_silu_fwd_bwd", "cfg1 [8,32,32,128] G32", T.median_us(gn1, reps), 20 * B * HW * C,
+         "cache-resident: GB/s are not an HBM roofline claim")
+    del x, dy, y, dx
+
+    # cfg2: EDM MP ops
+    R, Cc = 128 * 32 * 32, 128
+    a, b_ = dev(rng.standard_normal(R * Cc)), dev(rng.standard_normal(R * Cc))
+    o = L.alloc(R * Cc)
+    _row("mp_sum", "cfg2 [128,32,32,128] t=0.3",
+         T.median_us(lambda: L.launch_mp_sum(o.p, a.p, b_.p, 0.3, R * Cc, stream), reps), 12 * R * Cc)
+    o2 = L.alloc(R * 2 * Cc)
+    _row("mp_cat", "cfg2 -> [128,32,32,256]",
+         T.median_us(lambda: L.launch_mp_channel_cat(o2.p, a.p, b_.p, 0.3, R, Cc, Cc, stream), reps), 16 * R * Cc)
+    _row("mp_channel_split", "cfg2 [128,32,32,256] -> 2x128",
+         T.median_us(lambda: L.launch_mp_channel_split(a.p, b_.p, o2.p, 0.3, R, Cc, Cc, stream), reps),
+         16 * R * Cc)
+    del o2
+    Kg, Co = 1152, 128
+    W = dev(rng.standard_normal(Kg * Co))
+    _row("weight_normalize", "cfg2 W[1152,128] eps 1e-4",
+         T.median_us(lambda: L.launch_weight_normalize(W.p, Kg, Co, 1e-4, stream), reps), 8 * Kg * Co,
+         "latency-bound")
+    M, gain, ggn = dev(rng.standard_normal(Kg * Co)), dev(np.ones(1)), L.alloc(1)
+    _row("weight_normalize_backward", "cfg2 W[1152,128]",
+         T.median_us(lambda: L.launch_weight_normalize_backward(M.p, W.p, gain.p, ggn.p, Kg, Co, stream), reps),
+         12 * Kg * Co, "latency-bound")
+    sig = np.exp(-1.2 + 1.2 * rng.standard_normal(128)).clip(0.002, 80)
+    xs, fr, ph = dev(np.log(sig) / 4), dev(rng.standard_normal(256)), dev(rng.uniform(0, 1, 256))
+    emb = L.alloc(128 * 256)
+    _row("mp_fourier", "cfg2 [128 x 256]",
+         T.median_us(lambda: L.launch_mp_fourier(emb.p, xs.p, fr.p, ph.p, 128, 256, stream), reps),
+         4 * (128 + 512 + 128 * 256), "latency-bound")
+    act_a, act_o = a, o
+    _row("mp_silu_fwd", "cfg2 [128,32,32,128]",
+         T.median_us(lambda: L.launch_activation_forward(act_o.p, act_a.p, R * Cc, 5, stream), reps), 8 * R * Cc)
+    _row("scale_by_scalar", "cfg2 GEMM out [131072,128]",
+         T.median_us(lambda: L.launch_scale_by_scalar(act_o.p, gain.p, R * Cc, stream), reps), 8 * R * Cc)
+    del a, b_, o
+
+    # cfg3: im2col / col2im 3x3 s1 p1, N=128, 32x32x128
+    Bn, H, Wd, Ci, K = 128, 32, 32, 128, 3
+    ncol = Bn * H * Wd * K * K * Ci
+    im = dev(rng.uniform(-1, 1, Bn * H * Wd * Ci))
+    col = L.alloc(ncol)
+    _row("im2col", "cfg3 [128,32,32,128] 3x3 s1 p1",
+         T.median_us(lambda: L.launch_im2col(col.p, im.p, Bn, H, Wd, Ci, K, 1, 1, H, Wd, stream), reps),
+         4 * (ncol + Bn * H * Wd * Ci))
+    _row("col2im_set", "cfg3 (gather, no memset)",
+         T.median_us(lambda: L.launch_col2im_set(im.p, col.p, Bn, H, Wd, Ci, K, 1, 1, H, Wd, stream), reps),
+         4 * (ncol + Bn * H * Wd * Ci))
+    _row("col2im", "cfg3 (reference pair: memset + accumulate)",
+         T.median_us(lambda: (L.dll.nnhip_memset_async(im.p, 0, 4 * Bn * H * Wd * Ci, stream),
+                              L.launch_col2im(im.p, col.p, Bn, H, Wd, Ci, K, 1, 1, H, Wd, stream)), reps),
+         4 * (ncol + Bn * H * Wd * Ci))
+    del col, im
+
+    # cfg4: sinusoidal, LayerNorm, SiLU over the DDPM stack
+    t = dev(rng.integers(0, 1000, 256))
+    semb = L.alloc(256 * 256)
+    lmp = float(f32(np.log(f32(10000.0))))
+    _row("sinusoidal", "cfg4 [256 x 256]",
+         T.median_us(lambda: L.launch_sinusoidal(semb.p, t.p, 256, 256, lmp, stream), reps), 4 * (256 + 65536),
+         "latency-bound")
+    Rl, Cl = 65536, 256
+    xl, dyl = dev(rng.standard_normal(Rl * Cl)), dev(rng.standard_normal(Rl * Cl))
+    yl, dxl = L.alloc(Rl * Cl), L.alloc(Rl * Cl)
+    gl, bl = dev(1 + 0.1 * rng.standard_normal(Cl)), dev(0.1 * rng.standard_normal(Cl))
+    mul, rsl, ggl, gbl = L.alloc(Rl), L.alloc(Rl), L.alloc(Cl), L.alloc(Cl)
+    wsl = L.alloc(L.nnhip_layernorm_backward_workspace(Rl, Cl))
+    _row("layernorm_fwd", "cfg4 [65536, 256]",
+         T.median_us(lambda: L.launch_layernorm_forward(yl.p, mul.p, rsl.p, xl.p, gl.p, bl.p, Rl, Cl, 1e-5, stream),
+                     reps), 8 * Rl * Cl)
+    _row("layernorm_bwd", "cfg4 [65536, 256]",
+         T.median_us(lambda: L.launch_layernorm_backward_ws(dxl.p, ggl.p, gbl.p, dyl.p, xl.p, gl.p, mul.p, rsl.p, Rl,
+                                                            Cl, wsl.p, stream), reps), 12 * Rl * Cl)
+    del xl, dyl, yl, dxl
+    n4 = 256 * 64 * 64 * 256
+    xa, ga = dev(rng.standard_normal(n4, dtype=f32)), L.alloc(n4)
+    ya = L.alloc(n4)
+    _row("silu_fwd", "cfg4 [256,64,64,256]",
+         T.median_us(lambda: L.launch_activation_forward(ya.p, xa.p, n4, 3, stream), max(5, reps // 4)), 8 * n4)
+    _row("silu_bwd", "cfg4 [256,64,64,256]",
+         T.median_us(lambda: L.launch_activation_backward(ga.p, ya.p, xa.p, n4, 3, stream), max(5, reps // 4)),
+         12 * n4)
+    del xa, ga, ya
+
+    # cfg5: fused Adam + EMA over the DDPM-UNet-like list
+    sizes = cfg5_tensor_sizes()
+    total = sum(sizes)
+    bufs = {k: L.alloc(total + 4 * len(sizes)) for k in ("p", "m", "v", "g", "s")}
+    bufs["p"].upload((0.02 * rng.standard_normal(total)).astype(f32))
+    bufs["g"].upload((1e-3 * rng.standard_normal(total)).astype(f32))
+    for k in ("m", "v"):
+        bufs[k].fill_bytes(0)
+    slots, off = [], 0
+    for n in sizes:
+        slots.append({k2: bufs[k1].offset(off) for k1, k2 in (("p", "p"), ("m", "m"), ("v", "v"), ("g", "g"),
+                                                              ("s", "shadow"))} | {"n": n})
+        off += (n + 3) // 4 * 4  # keep every tensor 16-byte aligned
+    plan = nn.make_plan(L, slots)
+    w1 = float(f32(1) - f32(0.9999))
+    _row("adam_ema_fused", f"cfg5 {len(sizes)} tensors / {total} params",
+         T.median_us(lambda: L.launch_adam_ema_step(plan, 1e-4, 0.9, 0.999, 1e-8, 0.1, 0.001, 0.9999, w1, stream),
+                     reps), 36 * total)
+
+    def per_tensor():
+        for s_ in slots:
+            L.launch_adam_step(s_["p"], s_["m"], s_["v"], s_["g"], 1e-4, 0.9, 0.999, 1e-8, 0.1, 0.001, s_["n"],
+                               stream)
+            L.launch_weighted_sum(s_["shadow"], s_["shadow"], s_["p"], 0.9999, w1, s_["n"], stream)
+    _row("adam_ema_per_tensor", f"cfg5 reference launch pattern ({2 * len(sizes)} launches)",
+         T.median_us(per_tensor, max(5, reps // 4)), 40 * total, "host launch loop included")
+    L.dll.nnhip_multi_tensor_plan_destroy(plan)
+    L.dll.nnhip_stream_destroy(stream)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -135,6 +319,8 @@ def main() -> int:
     ap.add_argument("--batch", type=int, default=256)
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     ap.add_argument("--cpu-sample", type=int, default=16, help="batch samples timed on the CPU")
+    ap.add_argument("--suite", action="store_true",
+                    help="time every hot-path row at its BASELINE config (one JSON line per row) instead")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one GPU "
@@ -150,6 +336,10 @@ def main() -> int:
         print("bench.py: no HIP device", file=sys.stderr)
         return 1
     info = L.device_info()
+    if args.suite:
+        log(f"[suite] device {info}")
+        run_suite(L, nn, max(5, args.steps))
+        return 0
     B, H, W, C, G = args.batch, 64, 64, 256, 32
     HW = H * W
     n = B * HW * C
@@ -245,13 +435,13 @@ def main() -> int:
                    "layout": "NHWC", "algorithmic_bytes_per_step": int(algo_bytes),
                    "device": info["arch"]},
         "roofline": {
-            "kernel": "gn_bwd_reg (launch_groupnorm_act_backward_ws incl. the dgamma/dbeta reduce)",
+            "kernel": ROOFLINE_KERNEL + " + gn_param_reduce (launch_groupnorm_act_backward_ws)",
             "bound": "hbm",
             "achieved": round(bwd_gbs, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(bwd_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": TRAFFIC_BYTES.get(ROOFLINE_KERNEL),
             "algorithmic_bytes_per_launch": int(bwd_bytes),
             "avg_launch_us": round(bwd_us, 2),
         },

@@ -148,19 +148,24 @@ __global__ __launch_bounds__(kGenTpb) void gn_param_partial_generic(float* __res
     }
 }
 
-// ggamma[c] = sum_b part_g[b*C+c] (and gbeta), fixed order: wave w sums
-// b = w, w+4, ... ascending, then the 4 wave sums are added in wave order.
-__global__ __launch_bounds__(kGenTpb) void gn_param_reduce(float* __restrict__ ggamma,
+// ggamma[c] = sum_b part_g[b*C+c] (and gbeta), fixed order: wave w of the
+// 16 sums b = w, w+16, ... ascending, then the 16 wave sums are added in wave
+// order.  One 1024-thread workgroup per 64 channels keeps the serial chain at
+// B/16 loads.
+constexpr int kRedTpb = 1024;
+constexpr int kRedNw = kRedTpb / kWave;
+
+__global__ __launch_bounds__(kRedTpb) void gn_param_reduce(float* __restrict__ ggamma,
     float* __restrict__ gbeta, const float* __restrict__ part_g,
     const float* __restrict__ part_b, int B, int C) {
-    __shared__ float lg[kGenNw][kWave];
-    __shared__ float lb[kGenNw][kWave];
+    __shared__ float lg[kRedNw][kWave];
+    __shared__ float lb[kRedNw][kWave];
     const int lane = threadIdx.x & (kWave - 1);
     const int wid = threadIdx.x / kWave;
     const int c = blockIdx.x * kWave + lane;
     float sg = 0.0f, sb = 0.0f;
     if (c < C) {
-        for (int b = wid; b < B; b += kGenNw) {
+        for (int b = wid; b < B; b += kRedNw) {
             sg += part_g[(size_t)b * C + c];
             sb += part_b[(size_t)b * C + c];
         }
@@ -171,7 +176,7 @@ __global__ __launch_bounds__(kGenTpb) void gn_param_reduce(float* __restrict__ g
     if (wid == 0 && c < C) {
         float ag = lg[0][lane], ab = lb[0][lane];
 #pragma unroll
-        for (int w = 1; w < kGenNw; ++w) {
+        for (int w = 1; w < kRedNw; ++w) {
             ag += lg[w][lane];
             ab += lb[w][lane];
         }
@@ -276,7 +281,7 @@ void gn_backward_impl(const char* what, float* dx, float* ggamma, float* gbeta, 
             gn_param_partial_generic<A><<<dim3((unsigned)((C + kWave - 1) / kWave), (unsigned)B),
                 dim3(kGenTpb), 0, s>>>(part_g, part_b, dy, x, gamma, beta, mu, rstd, G, HW, C, cpg));
     }
-    gn_param_reduce<<<dim3((unsigned)((C + kWave - 1) / kWave)), dim3(kGenTpb), 0, s>>>(ggamma,
+    gn_param_reduce<<<dim3((unsigned)((C + kWave - 1) / kWave)), dim3(kRedTpb), 0, s>>>(ggamma,
         gbeta, part_g, part_b, B, C);
     if (!ws) nnk_scratch_release(scratch, s);
     nnk_after_launch(what, s);
