@@ -2,7 +2,7 @@
 """North-star benchmark: GroupNorm(32)+SiLU forward+backward, NHWC fp32,
 N=256, H=W=64, C=256 (metric quoted on it).
 
-A step is one fused forward (launch_groupnorm_act_forward) plus one fused
+A step is one fused forward (launch_groupnorm_act_forward_ws) plus one fused
 backward (launch_groupnorm_act_backward_ws: dx and dgamma/dbeta) over the
 whole batch, inputs resident in HBM.  value = algorithmic bytes per step /
 time per step, algorithmic bytes = 20 B/elem (fwd: read x, write y; bwd: read
@@ -352,13 +352,15 @@ def main() -> int:
     mu, rs = L.alloc(B * G), L.alloc(B * G)
     gg, gb = L.alloc(C), L.alloc(C)
     ws = L.alloc(L.nnhip_groupnorm_backward_workspace(B, HW, C, G))
+    fws = L.alloc(max(1, L.nnhip_groupnorm_forward_workspace(B, HW, C, G)))
     stream = L.dll.nnhip_stream_create()
     if not stream:
         raise RuntimeError("stream creation failed")
     act = nn.ACT_SILU
 
     def fwd():
-        L.launch_groupnorm_act_forward(yd.p, mu.p, rs.p, xd.p, gd.p, bd.p, B, HW, C, G, 1e-5, act, stream)
+        L.launch_groupnorm_act_forward_ws(yd.p, mu.p, rs.p, xd.p, gd.p, bd.p, B, HW, C, G, 1e-5, act, fws.p,
+                                          stream)
 
     def bwd():
         L.launch_groupnorm_act_backward_ws(dxd.p, gg.p, gb.p, dyd.p, xd.p, gd.p, bd.p, mu.p, rs.p, B, HW, C, G,
@@ -396,6 +398,9 @@ def main() -> int:
         fwd_ms.append(L.dll.nnhip_event_elapsed_ms(ev[0], ev[1]))
         bwd_ms.append(L.dll.nnhip_event_elapsed_ms(ev[1], ev[2]))
     L.check("bench")
+    for name, w in (("forward", fws), ("backward", ws)):
+        if L.nnhip_groupnorm_workspace_status(w.p) != 0:
+            raise RuntimeError(f"bench: a statistics wait of the {name} kernel ran out of polls")
     fwd_us = 1e3 * float(np.mean(fwd_ms))
     bwd_us = 1e3 * float(np.mean(bwd_ms))
 

@@ -91,7 +91,10 @@ _SIGS = {
     "launch_col2im": (None, [P, P, I, I, I, I, I, I, I, I, I, P], True),
     "launch_groupnorm_act_forward": (None, [P, P, P, P, P, P, I, I, I, I, F, I, P], True),
     "launch_groupnorm_act_backward": (None, [P, P, P, P, P, P, P, P, P, I, I, I, I, I, P], True),
+    "nnhip_groupnorm_forward_workspace": (SZ, [I, I, I, I], False),
     "nnhip_groupnorm_backward_workspace": (SZ, [I, I, I, I], False),
+    "nnhip_groupnorm_workspace_status": (I, [P], False),
+    "launch_groupnorm_act_forward_ws": (None, [P, P, P, P, P, P, I, I, I, I, F, I, P, P], True),
     "nnhip_layernorm_backward_workspace": (SZ, [I, I], False),
     "launch_groupnorm_act_backward_ws": (None, [P, P, P, P, P, P, P, P, P, I, I, I, I, I, P, P], True),
     "launch_layernorm_backward_ws": (None, [P, P, P, P, P, P, P, P, I, I, P, P], True),

@@ -1,0 +1,612 @@
+// gn_stream.h -- streaming NHWC GroupNorm (+ fused activation) for large
+// per-sample groups: the HBM-bound path of the GroupNorm launchers.
+//
+// Reference maths: src/kernels.cu:622-717 (forward statistics, backward-x,
+// backward-param), composed with the activation of src/kernels.cu:21-68 as the
+// DDPM block does (src/conv_residual.c:28-29, 51-52).
+//
+// Why a streaming design.  A workgroup that holds a whole (sample, group) reads
+// it as cpg-float columns of every pixel row (32 bytes per 1 KB row at the
+// north-star shape) and runs load -> reduce -> store in lock-step phases; both
+// cost bandwidth on gfx950.  Here every wave instruction reads whole 128-byte
+// lines of contiguous pixel-row segments, and the group statistics of a sample
+// are combined across workgroups without anyone blocking on them:
+//
+//   tile       = TP pixel rows x CW4 float4 columns (a column block) of one
+//                sample; it covers GT = CW4 / (cpg/4) whole groups.
+//   grid       = P persistent workgroups (cooperative launch: all resident),
+//                P a multiple of the tiles per sample, so workgroup w always
+//                owns the same (column block, pixel tile) position and walks
+//                the samples; tile i = round * P + w.
+//   round r    : prefetch tile i+P into registers;
+//                phase A on tile i (registers): per-group partial statistics
+//                -> one epoch-tagged 64-bit record per (tile, group, value);
+//                phase B on tile i-P (parked in LDS by the previous round):
+//                read the T records of each of its groups, merge them in a
+//                fixed order, normalise / form dx, store;
+//                park tile i in LDS.
+//
+// Records carry the launch epoch in their upper 32 bits and are written and
+// read with agent-scope atomic 64-bit accesses, so a reader accepts exactly
+// this launch's values and needs no fence or counter.  Every wait is bounded:
+// past `spin_limit` polls the workgroup flags an error in the workspace and
+// stops waiting (the kernel always terminates).  Deadlock freedom: waits go
+// only to tiles of earlier rounds or of the current round's phase A, which no
+// workgroup skips, and cooperative launch makes all P workgroups resident.
+//
+// Forward statistics are Chan et al.'s parallel mean/M2 merges of two-pass
+// per-thread values (more accurate than the reference's E[x^2]-mu^2).  The
+// backward sums S1 = sum g, S2 = sum g*xhat (g = dy*act'(h)*gamma) per group and
+// accumulates the dgamma/dbeta partials per lane across the workgroup's tiles;
+// a final fixed-order reduce over workgroups gives dgamma/dbeta.
+#pragma once
+
+#include "nnk_common.h"
+
+namespace nnk {
+namespace gns {
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t sample_rsrc(const float* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, (int)bytes, 0x00020000);
+}
+
+// 128-bit buffer load; the whole-vector bit cast keeps all four lanes (taking
+// components of the integer vector one by one lets this hipcc shrink the load).
+__device__ __forceinline__ float4 bload(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    const f32x4 f = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
+    return make_float4(f.x, f.y, f.z, f.w);
+}
+
+__device__ __forceinline__ unsigned long long tagged(unsigned long long tag, float v) {
+    return tag | (unsigned long long)__builtin_bit_cast(unsigned, v);
+}
+__device__ __forceinline__ void rec_store(unsigned long long* p, unsigned long long v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned long long rec_load(const unsigned long long* p) {
+    return __hip_atomic_load(const_cast<unsigned long long*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Poll one record until it carries `epoch`; bounded.
+__device__ __forceinline__ float rec_wait(const unsigned long long* p, unsigned long long r, unsigned epoch,
+    unsigned spin_limit, unsigned* err) {
+    unsigned n = 0;
+    while ((unsigned)(r >> 32) != epoch) {
+        if (++n > spin_limit) {
+            atomicOr(err, 1u);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+        r = rec_load(p);
+    }
+    return __builtin_bit_cast(float, (unsigned)r);
+}
+
+// Chan merge of (na, ma, qa) with (nb, mb, qb).
+__device__ __forceinline__ void chan_merge(float& n, float& m, float& q, float nb, float mb, float qb) {
+    const float nn = n + nb;
+    const float d = mb - m;
+    m = m + d * (nb / nn);
+    q = q + qb + d * d * (n * nb / nn);
+    n = nn;
+}
+// Merge of two equal-count partials (count c each).
+__device__ __forceinline__ void chan_merge_eq(float& m, float& q, float mo, float qo, float c) {
+    const float d = mo - m;
+    m = 0.5f * (m + mo);
+    q = q + qo + d * d * (0.5f * c);
+}
+
+// ---------------------------------------------------------------------------
+// Geometry shared by the forward and backward kernels.
+// ---------------------------------------------------------------------------
+template <int TPB_, int TP_, int CW4_, int CPG4_>
+struct Geom {
+    static constexpr int TPB = TPB_;            // threads per workgroup
+    static constexpr int NW = TPB / kWave;      // waves
+    static constexpr int TP = TP_;              // pixel rows per tile
+    static constexpr int CW4 = CW4_;            // float4 columns per tile row
+    static constexpr int CPG4 = CPG4_;          // float4 per group
+    static constexpr int RW = kWave / CW4;      // tile rows per wave instruction
+    static constexpr int RSTEP = NW * RW;       // tile rows per workgroup instruction
+    static constexpr int NV = TP / RSTEP;       // float4 per thread per tensor
+    static constexpr int GT = CW4 / CPG4;       // groups per tile
+    static_assert(kWave % CW4 == 0 && CW4 % CPG4 == 0, "tile columns");
+    static_assert(TP % RSTEP == 0 && NV >= 1, "tile rows");
+    static_assert(GT <= kWave, "groups per tile");
+};
+
+// Runtime shape of a launch.
+struct Shape {
+    int B, HW, C, G;   // batch, pixels, channels, groups
+    int T;             // pixel tiles per sample = HW / TP
+    int NCB;           // column blocks per row = C / (4 * CW4)
+    int ntiles;        // B * NCB * T
+    uint32_t sample_bytes;
+    float inv_n;       // 1 / (HW * cpg)
+};
+
+// Workspace layout (device): [err u32 (padded to 256 B)] [records u64] [channel partials f32].
+struct Work {
+    unsigned* err;
+    unsigned long long* rec;   // ntiles * GT * 2
+    float* cpart;              // bwd: P * 2 * (4 * CW4)
+};
+
+// Lanes that share this lane's group inside a wave: xor over the column bits
+// inside the group and over the row bits of the wave.
+template <class Gm, class F>
+__device__ __forceinline__ void for_group_xor(F f) {
+#pragma unroll
+    for (int o = 1; o < Gm::CPG4; o <<= 1) f(o);
+#pragma unroll
+    for (int o = Gm::CW4; o < kWave; o <<= 1) f(o);
+}
+
+// ---------------------------------------------------------------------------
+// Forward.
+// ---------------------------------------------------------------------------
+template <class Gm, int ACT, int RPL>
+__global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float* __restrict__ mu_out,
+    float* __restrict__ rstd_out, const float* __restrict__ x, const float* __restrict__ gamma,
+    const float* __restrict__ beta, Shape sh, Work wk, float eps, unsigned epoch, unsigned spin_limit) {
+#pragma clang fp contract(fast)
+    constexpr int NW = Gm::NW, NV = Gm::NV, GT = Gm::GT, TPB = Gm::TPB, CW4 = Gm::CW4;
+    extern __shared__ float4 parked[];          // NV * TPB float4: the tile awaiting phase B
+    // Double-buffered by loop parity pb: consecutive phase A's (and phase B's)
+    // may run with no barrier between them (first and last rounds), so a
+    // buffer is rewritten only two phases later, past the other phase's barrier.
+    __shared__ float wred[2][NW][GT][2];
+    __shared__ float stat[2][GT][2];
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
+    const int col = lane % CW4, row0 = wid * Gm::RW + lane / CW4;
+    const int gl = col / Gm::CPG4;              // group of this lane within the tile
+    const int P = gridDim.x, w = blockIdx.x;
+    const int T = sh.T, NCB = sh.NCB;
+    const int cb = (w / T) % NCB;               // fixed column block of this workgroup
+    const int t = w % T;                        // fixed pixel tile of this workgroup
+    const int c0 = cb * CW4 * 4 + col * 4;      // first channel of this lane
+    const uint32_t voff = (uint32_t)(row0 * sh.C + c0) * 4u;
+    const uint32_t row_bytes = (uint32_t)sh.C * 4u;
+    const float4 gm = ld4(gamma + c0), bt = ld4(beta + c0);
+    const float nthr = (float)(NV * 4);
+    const unsigned long long tag = (unsigned long long)epoch << 32;
+    // merge role in phase B: LPG = T / RPL lanes per group (a power of two,
+    // at most TPB / GT); lane rj merges records rj, rj + LPG, ... (RPL of them)
+    const int LPG = T / RPL;
+    const int rg = tid / LPG, rj = tid % LPG;
+    const bool merger = rg < GT;
+
+    auto sample_of = [&](int tile) { return tile / (NCB * T); };
+    auto load_tile = [&](float4 (&v)[NV], int b) {
+        const __amdgpu_buffer_rsrc_t r = sample_rsrc(x + (size_t)b * sh.HW * sh.C, sh.sample_bytes);
+        const uint32_t base = (uint32_t)(t * Gm::TP) * row_bytes;
+#pragma unroll
+        for (int k = 0; k < NV; ++k) v[k] = bload(r, voff, base + (uint32_t)(k * Gm::RSTEP) * row_bytes);
+    };
+    auto phase_a = [&](float4 (&v)[NV], int tile, int pb) {
+        float s = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NV; ++k) s += (v[k].x + v[k].y) + (v[k].z + v[k].w);
+        float m = s / nthr, q = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            const float a = v[k].x - m, bb = v[k].y - m, c = v[k].z - m, d = v[k].w - m;
+            q += (a * a + bb * bb) + (c * c + d * d);
+        }
+        float cnt = nthr;
+        for_group_xor<Gm>([&](int o) {
+            chan_merge_eq(m, q, __shfl_xor(m, o, kWave), __shfl_xor(q, o, kWave), cnt);
+            cnt *= 2.0f;
+        });
+        if (lane % CW4 % Gm::CPG4 == 0 && lane < CW4) {
+            wred[pb][wid][gl][0] = m;
+            wred[pb][wid][gl][1] = q;
+        }
+        __syncthreads();
+        if (tid < GT) {
+            float mm[NW], qq[NW];
+#pragma unroll
+            for (int i = 0; i < NW; ++i) {
+                mm[i] = wred[pb][i][tid][0];
+                qq[i] = wred[pb][i][tid][1];
+            }
+#pragma unroll
+            for (int half = NW / 2; half >= 1; half >>= 1) {
+#pragma unroll
+                for (int i = 0; i < half; ++i) chan_merge_eq(mm[i], qq[i], mm[i + half], qq[i + half], cnt);
+                cnt *= 2.0f;
+            }
+            unsigned long long* r = wk.rec + ((size_t)tile * GT + tid) * 2;
+            rec_store(r, tagged(tag, mm[0]));
+            rec_store(r + 1, tagged(tag, qq[0]));
+        }
+    };
+    auto phase_b = [&](int tile, const unsigned long long (&r0)[RPL], const unsigned long long (&r1)[RPL], int pb) {
+        const int b = sample_of(tile);
+        if (merger) {
+            // lane rj merges records rj, rj+LPG, ... of group rg in tile order, then a fixed xor tree
+            const float ntile = (float)(Gm::TP * Gm::CPG4 * 4);
+            float n = 0.0f, m = 0.0f, q = 0.0f;
+            const size_t unit = (size_t)b * NCB + cb;
+#pragma unroll
+            for (int u = 0; u < RPL; ++u) {
+                const unsigned long long* p = wk.rec + (((unit * T) + rj + u * LPG) * GT + rg) * 2;
+                const float mj = rec_wait(p, r0[u], epoch, spin_limit, wk.err);
+                const float qj = rec_wait(p + 1, r1[u], epoch, spin_limit, wk.err);
+                if (u == 0) {
+                    n = ntile;
+                    m = mj;
+                    q = qj;
+                } else {
+                    chan_merge(n, m, q, ntile, mj, qj);
+                }
+            }
+            for (int o = 1; o < LPG; o <<= 1) {
+                chan_merge_eq(m, q, __shfl_xor(m, o, kWave), __shfl_xor(q, o, kWave), n);
+                n *= 2.0f;
+            }
+            if (rj == 0) {
+                stat[pb][rg][0] = m;
+                stat[pb][rg][1] = rsqrtf(q / n + eps);
+            }
+        }
+        __syncthreads();
+        const float mean = stat[pb][gl][0], rs = stat[pb][gl][1];
+        if (t == 0 && tid < GT) {
+            mu_out[b * sh.G + cb * GT + tid] = stat[pb][tid][0];
+            rstd_out[b * sh.G + cb * GT + tid] = stat[pb][tid][1];
+        }
+        float* ys = y + (size_t)b * sh.HW * sh.C + (size_t)(t * Gm::TP + row0) * sh.C + c0;
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            const float4 v = parked[k * TPB + tid];
+            float4 o;
+            o.x = act_fwd<ACT>(gm.x * ((v.x - mean) * rs) + bt.x);
+            o.y = act_fwd<ACT>(gm.y * ((v.y - mean) * rs) + bt.y);
+            o.z = act_fwd<ACT>(gm.z * ((v.z - mean) * rs) + bt.z);
+            o.w = act_fwd<ACT>(gm.w * ((v.w - mean) * rs) + bt.w);
+            st4(ys + (size_t)(k * Gm::RSTEP) * sh.C, o);
+        }
+    };
+    auto records_prefetch = [&](int tile, unsigned long long (&r0)[RPL], unsigned long long (&r1)[RPL]) {
+        if (!merger) return;
+        const int b = sample_of(tile);
+        const size_t unit = (size_t)b * NCB + cb;
+#pragma unroll
+        for (int u = 0; u < RPL; ++u) {
+            const unsigned long long* p = wk.rec + (((unit * T) + rj + u * LPG) * GT + rg) * 2;
+            r0[u] = rec_load(p);
+            r1[u] = rec_load(p + 1);
+        }
+    };
+    auto park = [&](float4 (&v)[NV]) {
+#pragma unroll
+        for (int k = 0; k < NV; ++k) parked[k * TPB + tid] = v[k];
+    };
+
+    // tile i = round * P + w; its sample = i / (NCB * T)
+    float4 ra[NV], rb[NV];
+    int tA = w, tB = -1;
+    const int nt = sh.ntiles;
+    if (tA < nt) load_tile(ra, sample_of(tA));
+    for (;;) {
+        unsigned long long r0[RPL], r1[RPL];
+        int tN = tA < nt ? tA + P : nt;
+        if (tN < nt) load_tile(rb, sample_of(tN));
+        if (tB >= 0) records_prefetch(tB, r0, r1);
+        if (tA < nt) phase_a(ra, tA, 0);
+        if (tB >= 0) phase_b(tB, r0, r1, 0);
+        if (tA < nt) {
+            park(ra);
+            tB = tA;
+        } else {
+            tB = -1;
+        }
+        tA = tN;
+        if (tA >= nt && tB < 0) break;
+        tN = tA < nt ? tA + P : nt;
+        if (tN < nt) load_tile(ra, sample_of(tN));
+        if (tB >= 0) records_prefetch(tB, r0, r1);
+        if (tA < nt) phase_a(rb, tA, 1);
+        if (tB >= 0) phase_b(tB, r0, r1, 1);
+        if (tA < nt) {
+            park(rb);
+            tB = tA;
+        } else {
+            tB = -1;
+        }
+        tA = tN;
+        if (tA >= nt && tB < 0) break;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Backward.  dy is the gradient of act(GN(x)); the pre-activation is
+// recomputed from x, mu, rstd, gamma, beta.  Parks xhat and g = d*gamma.
+// ---------------------------------------------------------------------------
+template <class Gm, int ACT, int RPL>
+__global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, const float* __restrict__ dy,
+    const float* __restrict__ x, const float* __restrict__ gamma, const float* __restrict__ beta,
+    const float* __restrict__ mu, const float* __restrict__ rstd, Shape sh, Work wk, unsigned epoch,
+    unsigned spin_limit) {
+#pragma clang fp contract(fast)
+    constexpr int NW = Gm::NW, NV = Gm::NV, GT = Gm::GT, TPB = Gm::TPB, CW4 = Gm::CW4;
+    extern __shared__ float4 parked[];          // 2 * NV * TPB float4: xhat then g of the tile awaiting phase B
+    // Double-buffered by loop parity pb: consecutive phase A's (and phase B's)
+    // may run with no barrier between them (first and last rounds), so a
+    // buffer is rewritten only two phases later, past the other phase's barrier.
+    __shared__ float wred[2][NW][GT][2];
+    __shared__ float stat[2][GT][2];
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
+    const int col = lane % CW4, row0 = wid * Gm::RW + lane / CW4;
+    const int gl = col / Gm::CPG4;
+    const int P = gridDim.x, w = blockIdx.x;
+    const int T = sh.T, NCB = sh.NCB;
+    const int cb = (w / T) % NCB;
+    const int t = w % T;
+    const int c0 = cb * CW4 * 4 + col * 4;
+    const int gglob = cb * GT + gl;             // global group index of this lane
+    const uint32_t voff = (uint32_t)(row0 * sh.C + c0) * 4u;
+    const uint32_t row_bytes = (uint32_t)sh.C * 4u;
+    const float4 gm = ld4(gamma + c0);
+    float4 bt = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if constexpr (ACT != ACT_IDENTITY) bt = ld4(beta + c0);
+    const unsigned long long tag = (unsigned long long)epoch << 32;
+    const int LPG = T / RPL;
+    const int rg = tid / LPG, rj = tid % LPG;
+    const bool merger = rg < GT;
+    float4 cg = make_float4(0.0f, 0.0f, 0.0f, 0.0f), cbs = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+
+    auto sample_of = [&](int tile) { return tile / (NCB * T); };
+    auto load_tile = [&](float4 (&xv)[NV], float4 (&gv)[NV], int b) {
+        const size_t so = (size_t)b * sh.HW * sh.C;
+        const __amdgpu_buffer_rsrc_t rx = sample_rsrc(x + so, sh.sample_bytes);
+        const __amdgpu_buffer_rsrc_t rd = sample_rsrc(dy + so, sh.sample_bytes);
+        const uint32_t base = (uint32_t)(t * Gm::TP) * row_bytes;
+#pragma unroll
+        for (int k = 0; k < NV; ++k) xv[k] = bload(rx, voff, base + (uint32_t)(k * Gm::RSTEP) * row_bytes);
+#pragma unroll
+        for (int k = 0; k < NV; ++k) gv[k] = bload(rd, voff, base + (uint32_t)(k * Gm::RSTEP) * row_bytes);
+    };
+    // phase A: xv -> xhat, gv -> g in place; per-group S1 = sum g, S2 = sum g*xhat -> records
+    auto phase_a = [&](float4 (&xv)[NV], float4 (&gv)[NV], int tile, float mean, float rs, int pb) {
+        float s1 = 0.0f, s2 = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            float4 xh, d;
+            xh.x = (xv[k].x - mean) * rs;
+            xh.y = (xv[k].y - mean) * rs;
+            xh.z = (xv[k].z - mean) * rs;
+            xh.w = (xv[k].w - mean) * rs;
+            d = gv[k];
+            if constexpr (ACT != ACT_IDENTITY) {
+                d.x = d.x * act_grad<ACT>(gm.x * xh.x + bt.x);
+                d.y = d.y * act_grad<ACT>(gm.y * xh.y + bt.y);
+                d.z = d.z * act_grad<ACT>(gm.z * xh.z + bt.z);
+                d.w = d.w * act_grad<ACT>(gm.w * xh.w + bt.w);
+            }
+            cg.x += d.x * xh.x;
+            cg.y += d.y * xh.y;
+            cg.z += d.z * xh.z;
+            cg.w += d.w * xh.w;
+            cbs.x += d.x;
+            cbs.y += d.y;
+            cbs.z += d.z;
+            cbs.w += d.w;
+            float4 g;
+            g.x = d.x * gm.x;
+            g.y = d.y * gm.y;
+            g.z = d.z * gm.z;
+            g.w = d.w * gm.w;
+            s1 += (g.x + g.y) + (g.z + g.w);
+            s2 += (g.x * xh.x + g.y * xh.y) + (g.z * xh.z + g.w * xh.w);
+            xv[k] = xh;
+            gv[k] = g;
+        }
+        for_group_xor<Gm>([&](int o) {
+            s1 += __shfl_xor(s1, o, kWave);
+            s2 += __shfl_xor(s2, o, kWave);
+        });
+        if (lane % CW4 % Gm::CPG4 == 0 && lane < CW4) {
+            wred[pb][wid][gl][0] = s1;
+            wred[pb][wid][gl][1] = s2;
+        }
+        __syncthreads();
+        if (tid < GT) {
+            float a = wred[pb][0][tid][0], c = wred[pb][0][tid][1];
+#pragma unroll
+            for (int i = 1; i < NW; ++i) {
+                a += wred[pb][i][tid][0];
+                c += wred[pb][i][tid][1];
+            }
+            unsigned long long* r = wk.rec + ((size_t)tile * GT + tid) * 2;
+            rec_store(r, tagged(tag, a));
+            rec_store(r + 1, tagged(tag, c));
+        }
+    };
+    auto records_prefetch = [&](int tile, unsigned long long (&r0)[RPL], unsigned long long (&r1)[RPL]) {
+        if (!merger) return;
+        const size_t unit = (size_t)sample_of(tile) * NCB + cb;
+#pragma unroll
+        for (int u = 0; u < RPL; ++u) {
+            const unsigned long long* p = wk.rec + (((unit * T) + rj + u * LPG) * GT + rg) * 2;
+            r0[u] = rec_load(p);
+            r1[u] = rec_load(p + 1);
+        }
+    };
+    auto phase_b = [&](int tile, const unsigned long long (&r0)[RPL], const unsigned long long (&r1)[RPL],
+                       float rs, int pb) {
+        const int b = sample_of(tile);
+        if (merger) {
+            const size_t unit = (size_t)b * NCB + cb;
+            float a = 0.0f, c = 0.0f;
+#pragma unroll
+            for (int u = 0; u < RPL; ++u) {
+                const unsigned long long* p = wk.rec + (((unit * T) + rj + u * LPG) * GT + rg) * 2;
+                a += rec_wait(p, r0[u], epoch, spin_limit, wk.err);
+                c += rec_wait(p + 1, r1[u], epoch, spin_limit, wk.err);
+            }
+            for (int o = 1; o < LPG; o <<= 1) {
+                a += __shfl_xor(a, o, kWave);
+                c += __shfl_xor(c, o, kWave);
+            }
+            if (rj == 0) {
+                stat[pb][rg][0] = a * sh.inv_n;
+                stat[pb][rg][1] = c * sh.inv_n;
+            }
+        }
+        __syncthreads();
+        const float m1 = stat[pb][gl][0], m2 = stat[pb][gl][1];
+        float* dxs = dx + (size_t)b * sh.HW * sh.C + (size_t)(t * Gm::TP + row0) * sh.C + c0;
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            const float4 xh = parked[k * TPB + tid];
+            const float4 g = parked[(NV + k) * TPB + tid];
+            float4 o;
+            o.x = rs * ((g.x - m1) - xh.x * m2);
+            o.y = rs * ((g.y - m1) - xh.y * m2);
+            o.z = rs * ((g.z - m1) - xh.z * m2);
+            o.w = rs * ((g.w - m1) - xh.w * m2);
+            st4(dxs + (size_t)(k * Gm::RSTEP) * sh.C, o);
+        }
+    };
+
+    auto park = [&](const float4 (&xh)[NV], const float4 (&g)[NV]) {
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            parked[k * TPB + tid] = xh[k];
+            parked[(NV + k) * TPB + tid] = g[k];
+        }
+    };
+
+    float4 xa[NV], ga[NV], xb[NV], gb[NV];
+    int tA = w, tB = -1;
+    float rsB = 0.0f;
+    const int nt = sh.ntiles;
+    float meanA = 0.0f, rsA = 0.0f;
+    if (tA < nt) {
+        const int b = sample_of(tA);
+        load_tile(xa, ga, b);
+        meanA = mu[b * sh.G + gglob];
+        rsA = rstd[b * sh.G + gglob];
+    }
+    for (;;) {
+        unsigned long long r0[RPL], r1[RPL];
+        int tN = tA < nt ? tA + P : nt;
+        float meanN = 0.0f, rsN = 0.0f;
+        if (tN < nt) {
+            const int b = sample_of(tN);
+            load_tile(xb, gb, b);
+            meanN = mu[b * sh.G + gglob];
+            rsN = rstd[b * sh.G + gglob];
+        }
+        if (tB >= 0) records_prefetch(tB, r0, r1);
+        if (tA < nt) phase_a(xa, ga, tA, meanA, rsA, 0);
+        if (tB >= 0) phase_b(tB, r0, r1, rsB, 0);
+        if (tA < nt) {
+            park(xa, ga);
+            tB = tA;
+            rsB = rsA;
+        } else {
+            tB = -1;
+        }
+        tA = tN;
+        meanA = meanN;
+        rsA = rsN;
+        if (tA >= nt && tB < 0) break;
+        tN = tA < nt ? tA + P : nt;
+        meanN = 0.0f;
+        rsN = 0.0f;
+        if (tN < nt) {
+            const int b = sample_of(tN);
+            load_tile(xa, ga, b);
+            meanN = mu[b * sh.G + gglob];
+            rsN = rstd[b * sh.G + gglob];
+        }
+        if (tB >= 0) records_prefetch(tB, r0, r1);
+        if (tA < nt) phase_a(xb, gb, tA, meanA, rsA, 1);
+        if (tB >= 0) phase_b(tB, r0, r1, rsB, 1);
+        if (tA < nt) {
+            park(xb, gb);
+            tB = tA;
+            rsB = rsA;
+        } else {
+            tB = -1;
+        }
+        tA = tN;
+        meanA = meanN;
+        rsA = rsN;
+        if (tA >= nt && tB < 0) break;
+    }
+
+    // dgamma/dbeta partials of this workgroup: lanes with equal column own the
+    // same 4 channels; sum over the wave's rows, then over the waves in order.
+    // The parked region is free now and holds the per-wave sums.
+    static_assert(NW * CW4 * 8 <= 2 * NV * TPB * 4, "channel partials fit the parked region");
+    float(*cred)[CW4][8] = reinterpret_cast<float(*)[CW4][8]>(parked);
+    __syncthreads();  // every thread has finished its last phase B read of the parked tile
+    float c8[8] = {cg.x, cg.y, cg.z, cg.w, cbs.x, cbs.y, cbs.z, cbs.w};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+#pragma unroll
+        for (int o = CW4; o < kWave; o <<= 1) c8[j] += __shfl_xor(c8[j], o, kWave);
+    }
+    if (lane < CW4) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) cred[wid][lane][j] = c8[j];
+    }
+    __syncthreads();
+    for (int i = tid; i < CW4 * 8; i += TPB) {
+        const int cl = i / 8, j = i % 8;
+        float acc = cred[0][cl][j];
+#pragma unroll
+        for (int ww = 1; ww < NW; ++ww) acc += cred[ww][cl][j];
+        // cpart[w][j>>2][channel within block]
+        wk.cpart[((size_t)w * 2 + (j >> 2)) * (CW4 * 4) + cl * 4 + (j & 3)] = acc;
+    }
+}
+
+}  // namespace gns
+}  // namespace nnk
+
+// ---------------------------------------------------------------------------
+// Host side (k_gns_fwd.hip / k_gns_bwd.hip).
+// ---------------------------------------------------------------------------
+// Streaming geometry: 1024 threads, half-row tiles of 32 float4 (128
+// channels); forward tiles of 256 pixel rows, backward of 128.
+namespace nnk {
+namespace gns {
+constexpr int kTpb = 1024;
+constexpr int kCw4 = 32;
+constexpr int kFwdTp = 256;
+constexpr int kBwdTp = 128;
+constexpr int kMaxGrid = 1024;        // persistent workgroups at most
+constexpr unsigned kSpinLimit = 1u << 16;
+
+struct Plan {
+    bool ok;
+    int cpg4, rpl;
+    Shape sh;
+    size_t ws_floats;   // workspace needed (err + records [+ channel partials])
+    size_t rec_offset;  // in bytes from the workspace start
+    size_t cpart_offset;
+};
+
+// Applicability and sizes; `bwd` selects the backward geometry.
+Plan make_plan(bool bwd, int B, int HW, int C, int G);
+unsigned next_epoch();
+}  // namespace gns
+}  // namespace nnk
+
+// Launch the streaming kernels when the shape fits and the device can hold
+// the persistent grid; return false (nothing launched) otherwise.  `ws` is a
+// device workspace of at least plan.ws_floats floats whose records region
+// never holds this launch's epoch (zero-filled once, or cleared by the caller).
+bool nnk_gns_forward(int act, float* y, float* mu, float* rstd, const float* x, const float* gamma,
+    const float* beta, int B, int HW, int C, int G, float eps, float* ws, hipStream_t s);
+bool nnk_gns_backward(int act, float* dx, float* ggamma, float* gbeta, const float* dy, const float* x,
+    const float* gamma, const float* beta, const float* mu, const float* rstd, int B, int HW, int C, int G,
+    float* ws, hipStream_t s);

@@ -1,0 +1,157 @@
+// k_gns.hip -- host side shared by the streaming GroupNorm launchers
+// (k_gns_fwd.hip, k_gns_bwd.hip): shape plan, launch epochs, and the
+// deterministic dgamma/dbeta reduction over the persistent workgroups.
+#include <atomic>
+
+#include "gn_stream.h"
+
+namespace nnk {
+namespace gns {
+
+static bool is_pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
+
+Plan make_plan(bool bwd, int B, int HW, int C, int G) {
+    Plan p{};
+    p.ok = false;
+    if (B <= 0 || HW <= 0 || C <= 0 || G <= 0 || C % G != 0) return p;
+    const int cpg = C / G;
+    if (cpg % 4 != 0) return p;
+    const int cpg4 = cpg / 4;
+    if (cpg4 != 1 && cpg4 != 2 && cpg4 != 4) return p;
+    if (C % (4 * kCw4) != 0) return p;
+    const int TP = bwd ? kBwdTp : kFwdTp;
+    if (HW % TP != 0) return p;
+    const int T = HW / TP;
+    if (!is_pow2(T)) return p;
+    const int GT = kCw4 / cpg4;
+    const int lpg_max = kTpb / GT;
+    int rpl = 0;
+    if (T <= lpg_max) rpl = 1;
+    else if (T <= 2 * lpg_max) rpl = 2;
+    else return p;
+    if ((long long)HW * C * 4 >= (1LL << 31)) return p;
+    const int NCB = C / (4 * kCw4);
+    if ((long long)NCB * T > kMaxGrid) return p;
+    if ((long long)B * NCB * T >= (1LL << 31) / (2 * GT)) return p;
+    p.cpg4 = cpg4;
+    p.rpl = rpl;
+    p.sh.B = B;
+    p.sh.HW = HW;
+    p.sh.C = C;
+    p.sh.G = G;
+    p.sh.T = T;
+    p.sh.NCB = NCB;
+    p.sh.ntiles = B * NCB * T;
+    p.sh.sample_bytes = (uint32_t)((long long)HW * C * 4);
+    p.sh.inv_n = 1.0f / (float)((long long)HW * cpg);
+    p.rec_offset = 256;
+    const size_t rec_bytes = (size_t)p.sh.ntiles * GT * 2 * sizeof(unsigned long long);
+    p.cpart_offset = p.rec_offset + rec_bytes;
+    const size_t cpart_bytes = bwd ? (size_t)kMaxGrid * 2 * (4 * kCw4) * sizeof(float) : 0;
+    p.ws_floats = (p.cpart_offset + cpart_bytes + sizeof(float) - 1) / sizeof(float);
+    p.ok = true;
+    return p;
+}
+
+unsigned next_epoch() {
+    static std::atomic<unsigned> epoch{0};
+    unsigned e = ++epoch;
+    if (e == 0) e = ++epoch;  // 0 is the value of a zero-filled workspace
+    return e;
+}
+
+}  // namespace gns
+}  // namespace nnk
+
+namespace {
+
+// Zero a workspace drawn from the stream-ordered pool before its first use.
+__global__ void gns_clear(unsigned* p, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        p[i] = 0u;
+}
+
+// dgamma/dbeta over the workgroups that own each column block: wave w sums
+// owners m = w, w + 16, ... (ascending), then the 16 wave sums are added in
+// wave order.  Grid: ceil(C / 64) workgroups of 1024 threads.
+__global__ __launch_bounds__(1024) void gns_param_reduce_k(float* __restrict__ ggamma,
+    float* __restrict__ gbeta, const float* __restrict__ cpart, int P, int T, int NCB, int C) {
+    constexpr int kCwc = 4 * nnk::gns::kCw4;
+    __shared__ float lg[16][64];
+    __shared__ float lb[16][64];
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int c = blockIdx.x * 64 + lane;
+    float sg = 0.0f, sb = 0.0f;
+    if (c < C) {
+        const int cb = c / kCwc, cl = c % kCwc;
+        const int owners = P / NCB;
+        for (int m = wid; m < owners; m += 16) {
+            const int w = ((m / T) * NCB + cb) * T + (m % T);
+            sg += cpart[((size_t)w * 2) * kCwc + cl];
+            sb += cpart[((size_t)w * 2 + 1) * kCwc + cl];
+        }
+    }
+    lg[wid][lane] = sg;
+    lb[wid][lane] = sb;
+    __syncthreads();
+    if (wid == 0 && c < C) {
+        float ag = lg[0][lane], ab = lb[0][lane];
+#pragma unroll
+        for (int w = 1; w < 16; ++w) {
+            ag += lg[w][lane];
+            ab += lb[w][lane];
+        }
+        ggamma[c] = ag;
+        gbeta[c] = ab;
+    }
+}
+
+}  // namespace
+
+void nnk_gns_clear_workspace(float* ws, size_t n_floats, hipStream_t s) {
+    if (n_floats == 0) return;
+    const size_t blocks = (n_floats + 255) / 256 < 4096 ? (n_floats + 255) / 256 : 4096;
+    gns_clear<<<dim3((unsigned)blocks), dim3(256), 0, s>>>(reinterpret_cast<unsigned*>(ws), n_floats);
+}
+
+void nnk_gns_param_reduce(float* ggamma, float* gbeta, const float* cpart, int P, int T, int NCB, int C,
+    hipStream_t s) {
+    gns_param_reduce_k<<<dim3((unsigned)((C + 63) / 64)), dim3(1024), 0, s>>>(ggamma, gbeta, cpart, P, T, NCB, C);
+}
+
+// Persistent grid size for a kernel: resident workgroups of the device
+// (cached per device and kernel), capped and rounded down to whole units.
+int nnk_gns_grid(const void* fn, int key, size_t lds, int unit) {
+    constexpr int kDev = 16, kKeys = 128;
+    static int occ_cache[kDev][kKeys];
+    static int cu_cache[kDev];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kDev || key < 0 || key >= kKeys) return 0;
+    if (occ_cache[dev][key] == 0) {
+        if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
+            (void)hipGetLastError();
+            occ_cache[dev][key] = -1;
+            return 0;
+        }
+        int occ = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, nnk::gns::kTpb, lds) != hipSuccess || occ <= 0) {
+            (void)hipGetLastError();
+            occ_cache[dev][key] = -1;
+            return 0;
+        }
+        occ_cache[dev][key] = occ;
+    }
+    if (occ_cache[dev][key] < 0) return 0;
+    if (cu_cache[dev] == 0) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) {
+            (void)hipGetLastError();
+            return 0;
+        }
+        cu_cache[dev] = cus;
+    }
+    long long P = (long long)occ_cache[dev][key] * cu_cache[dev];
+    if (P > nnk::gns::kMaxGrid) P = nnk::gns::kMaxGrid;
+    P = P / unit * unit;
+    return (int)P;
+}

@@ -1,0 +1,67 @@
+// k_gns_bwd.hip -- instantiations and launch of the streaming GroupNorm
+// backward (gn_stream.h) and its dgamma/dbeta reduction.
+#include "gn_stream.h"
+
+int nnk_gns_grid(const void* fn, int key, size_t lds, int unit);
+void nnk_gns_param_reduce(float* ggamma, float* gbeta, const float* cpart, int P, int T, int NCB, int C,
+    hipStream_t s);
+
+namespace {
+
+using namespace nnk;
+using namespace nnk::gns;
+
+template <int ACT, int CPG4, int RPL>
+bool launch(const Plan& p, float* dx, float* ggamma, float* gbeta, const float* dy, const float* x,
+    const float* gamma, const float* beta, const float* mu, const float* rstd, float* ws, hipStream_t s) {
+    using Gm = Geom<kTpb, kBwdTp, kCw4, CPG4>;
+    const void* fn = reinterpret_cast<const void*>(&gns_bwd<Gm, ACT, RPL>);
+    const size_t lds = (size_t)2 * Gm::NV * kTpb * sizeof(float4);
+    const int key = 64 + (ACT * 3 + (CPG4 == 1 ? 0 : CPG4 == 2 ? 1 : 2)) * 2 + (RPL - 1);
+    const int P = nnk_gns_grid(fn, key, lds, p.sh.T * p.sh.NCB);
+    if (P <= 0) return false;
+    Shape sh = p.sh;
+    Work wk;
+    wk.err = reinterpret_cast<unsigned*>(ws);
+    wk.rec = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(ws) + p.rec_offset);
+    wk.cpart = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + p.cpart_offset);
+    unsigned epoch = next_epoch();
+    unsigned limit = kSpinLimit;
+    void* args[] = {&dx, const_cast<float**>(&dy), const_cast<float**>(&x), const_cast<float**>(&gamma),
+        const_cast<float**>(&beta), const_cast<float**>(&mu), const_cast<float**>(&rstd), &sh, &wk, &epoch,
+        &limit};
+    if (hipLaunchCooperativeKernel(fn, dim3((unsigned)P), dim3(kTpb), args, (unsigned)lds, s) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    nnk_gns_param_reduce(ggamma, gbeta, wk.cpart, P, sh.T, sh.NCB, sh.C, s);
+    return true;
+}
+
+template <int ACT>
+bool by_shape(const Plan& p, float* dx, float* ggamma, float* gbeta, const float* dy, const float* x,
+    const float* gamma, const float* beta, const float* mu, const float* rstd, float* ws, hipStream_t s) {
+#define NNK_GNS_BWD_CASE(CPG4, RPL)                                                                          \
+    if (p.cpg4 == CPG4 && p.rpl == RPL)                                                                      \
+        return launch<ACT, CPG4, RPL>(p, dx, ggamma, gbeta, dy, x, gamma, beta, mu, rstd, ws, s);
+    NNK_GNS_BWD_CASE(1, 1)
+    NNK_GNS_BWD_CASE(1, 2)
+    NNK_GNS_BWD_CASE(2, 1)
+    NNK_GNS_BWD_CASE(2, 2)
+    NNK_GNS_BWD_CASE(4, 1)
+    NNK_GNS_BWD_CASE(4, 2)
+#undef NNK_GNS_BWD_CASE
+    return false;
+}
+
+}  // namespace
+
+bool nnk_gns_backward(int act, float* dx, float* ggamma, float* gbeta, const float* dy, const float* x,
+    const float* gamma, const float* beta, const float* mu, const float* rstd, int B, int HW, int C, int G,
+    float* ws, hipStream_t s) {
+    const Plan p = make_plan(true, B, HW, C, G);
+    if (!p.ok || !ws) return false;
+    bool launched = false;
+    NNK_ACT_DISPATCH(act, A, launched = by_shape<A>(p, dx, ggamma, gbeta, dy, x, gamma, beta, mu, rstd, ws, s));
+    return launched;
+}

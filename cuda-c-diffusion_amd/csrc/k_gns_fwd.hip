@@ -1,0 +1,61 @@
+// k_gns_fwd.hip -- instantiations and launch of the streaming GroupNorm
+// forward (gn_stream.h).
+#include "gn_stream.h"
+
+int nnk_gns_grid(const void* fn, int key, size_t lds, int unit);
+
+namespace {
+
+using namespace nnk;
+using namespace nnk::gns;
+
+template <int ACT, int CPG4, int RPL>
+bool launch(const Plan& p, float* y, float* mu, float* rstd, const float* x, const float* gamma,
+    const float* beta, float eps, float* ws, hipStream_t s) {
+    using Gm = Geom<kTpb, kFwdTp, kCw4, CPG4>;
+    const void* fn = reinterpret_cast<const void*>(&gns_fwd<Gm, ACT, RPL>);
+    const size_t lds = (size_t)Gm::NV * kTpb * sizeof(float4);
+    const int key = (ACT * 3 + (CPG4 == 1 ? 0 : CPG4 == 2 ? 1 : 2)) * 2 + (RPL - 1);
+    const int P = nnk_gns_grid(fn, key, lds, p.sh.T * p.sh.NCB);
+    if (P <= 0) return false;
+    Shape sh = p.sh;
+    Work wk;
+    wk.err = reinterpret_cast<unsigned*>(ws);
+    wk.rec = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(ws) + p.rec_offset);
+    wk.cpart = nullptr;
+    unsigned epoch = next_epoch();
+    unsigned limit = kSpinLimit;
+    void* args[] = {&y, &mu, &rstd, const_cast<float**>(&x), const_cast<float**>(&gamma),
+        const_cast<float**>(&beta), &sh, &wk, &eps, &epoch, &limit};
+    if (hipLaunchCooperativeKernel(fn, dim3((unsigned)P), dim3(kTpb), args, (unsigned)lds, s) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return true;
+}
+
+template <int ACT>
+bool by_shape(const Plan& p, float* y, float* mu, float* rstd, const float* x, const float* gamma,
+    const float* beta, float eps, float* ws, hipStream_t s) {
+#define NNK_GNS_FWD_CASE(CPG4, RPL)                                                     \
+    if (p.cpg4 == CPG4 && p.rpl == RPL) return launch<ACT, CPG4, RPL>(p, y, mu, rstd, x, gamma, beta, eps, ws, s);
+    NNK_GNS_FWD_CASE(1, 1)
+    NNK_GNS_FWD_CASE(1, 2)
+    NNK_GNS_FWD_CASE(2, 1)
+    NNK_GNS_FWD_CASE(2, 2)
+    NNK_GNS_FWD_CASE(4, 1)
+    NNK_GNS_FWD_CASE(4, 2)
+#undef NNK_GNS_FWD_CASE
+    return false;
+}
+
+}  // namespace
+
+bool nnk_gns_forward(int act, float* y, float* mu, float* rstd, const float* x, const float* gamma,
+    const float* beta, int B, int HW, int C, int G, float eps, float* ws, hipStream_t s) {
+    const Plan p = make_plan(false, B, HW, C, G);
+    if (!p.ok || !ws) return false;
+    bool launched = false;
+    NNK_ACT_DISPATCH(act, A, launched = by_shape<A>(p, y, mu, rstd, x, gamma, beta, eps, ws, s));
+    return launched;
+}

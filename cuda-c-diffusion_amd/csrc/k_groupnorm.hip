@@ -7,7 +7,13 @@
 //   * generic (below): any cpg / size / alignment.  Streams the group twice
 //     (statistics, then output) and computes the dgamma/dbeta partials in a
 //     separate coalesced kernel.  Same maths, same reduction discipline.
+#include <stdlib.h>
+#include <string.h>
+
 #include "gn_kernels.h"
+#include "gn_stream.h"
+
+void nnk_gns_clear_workspace(float* ws, size_t n_floats, hipStream_t s);
 
 namespace {
 
@@ -223,17 +229,68 @@ bool shape_ok(const char* what, int B, int HW, int C, int G) {
     return true;
 }
 
+// Path policy: NNHIP_GN_PATH=stream uses the streaming kernels whenever the
+// shape fits them, =reg never; unset (auto) uses them for tensors of at least
+// kStreamMinElems elements, below which the register-resident kernels win,
+// and for any size the register-resident kernels cannot take (their
+// alternative is the two-pass generic kernel).
+enum class GnPath { kAuto, kStream, kReg };
+constexpr long long kStreamMinElems = 1LL << 22;
+
+GnPath gn_path() {  // read per launch, so a process can switch paths
+    const char* e = getenv("NNHIP_GN_PATH");
+    if (e && strcmp(e, "stream") == 0) return GnPath::kStream;
+    if (e && strcmp(e, "reg") == 0) return GnPath::kReg;
+    return GnPath::kAuto;
+}
+
+bool want_stream(bool bwd, int B, int HW, int C, int G, bool reg_ok) {
+    const GnPath path = gn_path();
+    if (path == GnPath::kReg) return false;
+    if (!nnk::gns::make_plan(bwd, B, HW, C, G).ok) return false;
+    return path == GnPath::kStream || !reg_ok || (long long)B * HW * C >= kStreamMinElems;
+}
+
+// Streaming launch on the caller's workspace or on one drawn from the
+// stream-ordered pool.  The region is zeroed first: the kernels accept a
+// statistics record only when it carries the launch's (non-zero) epoch, and
+// clearing guarantees that nothing left in the memory by earlier calls (of
+// other shapes or paths) can carry it.
+template <class F>
+bool try_stream(bool bwd, int B, int HW, int C, int G, bool reg_ok, float* ws, hipStream_t s, const char* what,
+    F launch) {
+    if (!want_stream(bwd, B, HW, C, G, reg_ok)) return false;
+    const nnk::gns::Plan p = nnk::gns::make_plan(bwd, B, HW, C, G);
+    float* w = ws;
+    if (!w) {
+        w = nnk_scratch_acquire(p.ws_floats, s, what);
+        if (!w) return false;
+    }
+    nnk_gns_clear_workspace(w, p.ws_floats, s);
+    const bool ok = launch(w);
+    if (!ws) nnk_scratch_release(w, s);
+    return ok;
+}
+
 void gn_forward_impl(const char* what, float* y, float* mu, float* rstd, const float* x,
     const float* gamma, const float* beta, int B, int HW, int C, int G, float eps, int act,
-    hipStream_t s) {
+    float* ws, hipStream_t s) {
     if (!shape_ok(what, B, HW, C, G)) return;
     NNK_REQUIRE(valid_act(act), what, "%s: unknown activation %d", what, act);
     if (B == 0) return;
     NNK_REQUIRE(y && mu && rstd && x && gamma && beta, what, "%s: null pointer", what);
+    NNK_REQUIRE(ws == nullptr || aligned16(ws), what, "%s: workspace must be 16-byte aligned", what);
     const int cpg = C / G;
     int cfg = -1;
     const int v4pp = reg_v4pp(cpg, HW, x, y, gamma, beta, cfg);
     bool launched = false;
+    const bool stream_aligned = aligned16(x) && aligned16(y) && aligned16(gamma) && aligned16(beta);
+    if (stream_aligned && try_stream(false, B, HW, C, G, v4pp != 0, ws, s, what, [&](float* w) {
+            return nnk_gns_forward(act, y, mu, rstd, x, gamma, beta, B, HW, C, G, eps, w, s);
+        })) {
+        nnk_after_launch(what, s);
+        return;
+    }
     if (v4pp) launched = nnk_gn_fwd_reg_dispatch(cfg, v4pp, act, y, mu, rstd, x, gamma, beta, B, G, HW, C, eps, s);
     if (!launched) {
         const FastDiv dv((uint32_t)cpg);
@@ -258,6 +315,21 @@ void gn_backward_impl(const char* what, float* dx, float* ggamma, float* gbeta, 
     NNK_REQUIRE(dx && dy && x && gamma && mu && rstd, what, "%s: null pointer", what);
     NNK_REQUIRE(act == ACT_IDENTITY || beta, what, "%s: beta is required with an activation", what);
     NNK_REQUIRE(ws == nullptr || aligned16(ws), what, "%s: workspace must be 16-byte aligned", what);
+    {
+        const bool stream_aligned = aligned16(x) && aligned16(dy) && aligned16(dx) && aligned16(gamma) &&
+            (act == ACT_IDENTITY || aligned16(beta));
+        int cfg = -1;
+        const bool reg_ok = reg_v4pp(C / G, HW, x, dy, dx, gamma, cfg) != 0 &&
+            (act == ACT_IDENTITY || aligned16(beta));
+        if (stream_aligned &&
+            try_stream(true, B, HW, C, G, reg_ok, ws, s, what, [&](float* w) {
+                return nnk_gns_backward(act, dx, ggamma, gbeta, dy, x, gamma, beta, mu, rstd, B, HW, C, G, w,
+                    s);
+            })) {
+            nnk_after_launch(what, s);
+            return;
+        }
+    }
     float* scratch = ws;
     if (!scratch) {
         scratch = nnk_scratch_acquire((size_t)2 * B * C, s, what);
@@ -295,14 +367,34 @@ void launch_groupnorm_forward(float* y, float* mu, float* rstd, const float* x,
     const float* gamma, const float* beta, int batch, int HW, int C, int G, float eps,
     hipStream_t s) {
     gn_forward_impl("launch_groupnorm_forward", y, mu, rstd, x, gamma, beta, batch, HW, C, G,
-        eps, ACT_IDENTITY, s);
+        eps, ACT_IDENTITY, nullptr, s);
 }
 
 void launch_groupnorm_act_forward(float* y, float* mu, float* rstd, const float* x,
     const float* gamma, const float* beta, int batch, int HW, int C, int G, float eps,
     Activation act, hipStream_t s) {
     gn_forward_impl("launch_groupnorm_act_forward", y, mu, rstd, x, gamma, beta, batch, HW, C,
-        G, eps, (int)act, s);
+        G, eps, (int)act, nullptr, s);
+}
+
+void launch_groupnorm_act_forward_ws(float* y, float* mu, float* rstd, const float* x,
+    const float* gamma, const float* beta, int batch, int HW, int C, int G, float eps,
+    Activation act, float* workspace, hipStream_t s) {
+    gn_forward_impl("launch_groupnorm_act_forward_ws", y, mu, rstd, x, gamma, beta, batch, HW, C,
+        G, eps, (int)act, workspace, s);
+}
+
+size_t nnhip_groupnorm_forward_workspace(int batch, int HW, int C, int G) {
+    const nnk::gns::Plan p = nnk::gns::make_plan(false, batch, HW, C, G);
+    return p.ok ? p.ws_floats : 0;
+}
+
+int nnhip_groupnorm_workspace_status(const float* workspace) {
+    if (!workspace) return 0;
+    unsigned flag = 0;
+    const hipError_t e = hipMemcpy(&flag, workspace, sizeof(flag), hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return -(int)e;
+    return flag ? 1 : 0;
 }
 
 void launch_groupnorm_backward(float* dx, float* ggamma, float* gbeta, const float* dy,
@@ -331,10 +423,10 @@ void launch_groupnorm_act_backward_ws(float* dx, float* ggamma, float* gbeta, co
 }
 
 size_t nnhip_groupnorm_backward_workspace(int batch, int HW, int C, int G) {
-    (void)HW;
-    (void)G;
     if (batch <= 0 || C <= 0) return 0;
-    return (size_t)2 * batch * C;
+    const size_t reg = (size_t)2 * batch * C;
+    const nnk::gns::Plan p = nnk::gns::make_plan(true, batch, HW, C, G);
+    return p.ok && p.ws_floats > reg ? p.ws_floats : reg;
 }
 
 }  // extern "C"

@@ -2,11 +2,15 @@
 //
 // Numerical conventions (all kernels):
 //   * fp32 storage and arithmetic; the library is compiled with
-//     -ffp-contract=off, so a*b+c is a multiply and an add unless a kernel
-//     writes __builtin_fmaf explicitly.  The CPU oracle is compiled the same
-//     way, which makes the elementwise kernels bit-identical to it.
+//     -ffp-contract=off, so a*b+c is a multiply and an add unless a function
+//     opts in with `#pragma clang fp contract(fast)` (the fast Pade tanh and
+//     the GroupNorm/LayerNorm bodies do).  Copies, single products and the
+//     optimizer updates stay uncontracted, so they are bit-identical to the
+//     CPU oracle, which is compiled with -ffp-contract=off.
 //   * Division and sqrt are the correctly rounded IEEE operations (hipcc's
-//     default); rsqrtf maps to the hardware reciprocal square root.
+//     default) except in the fast form of the Pade activations (reciprocal,
+//     see below);
+//     rsqrtf maps to the hardware reciprocal square root.
 //   * Reductions are fixed-shape trees (DPP within a row of 16 lanes, lane
 //     reads across the 4 rows, LDS across waves), so every result is
 //     reproducible run to run.
@@ -22,59 +26,89 @@ namespace nnk {
 // ---------------------------------------------------------------------------
 // Activation family.  Reference: src/kernels.cu:6-68.
 // The tanh is the Pade [7/6] approximant of the Lambert continued fraction
-// x/(1+x^2/(3+x^2/(5+x^2/(7+...)))), clamped to [-1,1]; the sigmoid is built
+// x/(1+x^2/(3+x^2/(5+...+x^2/13))), clamped to [-1,1]; the sigmoid is built
 // on it as (tanh(x/2)+1)/2.  Backward formulas are the reference's (the SiLU
 // derivative uses the approximate sigmoid, it is not the derivative of the
 // approximate SiLU).
+//
+// Arithmetic, two forms (the reference build, Makefile:11, uses --use_fast_math,
+// so its own quotient is approximate and its multiply-adds are contracted):
+//   exact (FAST = false): the reference's operation order, no contraction,
+//     correctly rounded division -- bit-identical to the CPU restatement;
+//     used by the standalone activation kernels, which are HBM-bound.
+//   fast (FAST = true): polynomials contracted to FMAs and the quotient as
+//     numerator times the hardware reciprocal (v_rcp_f32, 1 ulp); within a
+//     few ulp of the exact form.  Used inside the fused GroupNorm kernels,
+//     where the activation is most of the VALU work.  Near |tanh| = 1 the
+//     terms 1 - t*t and 1 +- t cancel, so there the difference is relative to
+//     the upstream gradient / input scale, not to the (tiny) result.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float pade_tanh(float x) {
+__device__ __forceinline__ float pade_tanh_exact(float x) {
     const float x2 = x * x;
     const float p = x * (135135.0f + x2 * (17325.0f + x2 * (378.0f + x2)));
     const float q = 135135.0f + x2 * (62370.0f + x2 * (3150.0f + x2 * 28.0f));
     return fmaxf(-1.0f, fminf(1.0f, p / q));
 }
 
+__device__ __forceinline__ float pade_tanh_fast(float x) {
+#pragma clang fp contract(fast)
+    const float x2 = x * x;
+    const float p = x * (135135.0f + x2 * (17325.0f + x2 * (378.0f + x2)));
+    const float q = 135135.0f + x2 * (62370.0f + x2 * (3150.0f + x2 * 28.0f));
+    return fmaxf(-1.0f, fminf(1.0f, p * __builtin_amdgcn_rcpf(q)));
+}
+
+template <bool FAST>
+__device__ __forceinline__ float pade_tanh(float x) {
+    if constexpr (FAST) return pade_tanh_fast(x);
+    else return pade_tanh_exact(x);
+}
+
+template <bool FAST>
 __device__ __forceinline__ float pade_sigmoid(float x) {
-    return fmaxf(0.0f, fminf(1.0f, (pade_tanh(x * 0.5f) + 1.0f) * 0.5f));
+    // pade_tanh is clamped to [-1, 1], so (t + 1) * 0.5 already lies in [0, 1]:
+    // the reference's outer clamp (kernels.cu:16) never changes the value and
+    // is not evaluated.
+    return (pade_tanh<FAST>(x * 0.5f) + 1.0f) * 0.5f;
 }
 
 constexpr float kGeluC = 0.7978845608f;
 constexpr float kGeluA = 0.044715f;
 constexpr float kMpSiluScale = 1.0f / 0.596f;
 
-template <int ACT>
+template <int ACT, bool FAST = true>
 __device__ __forceinline__ float act_fwd(float v) {
     if constexpr (ACT == ACT_RELU) {
         return v > 0.0f ? v : 0.0f;
     } else if constexpr (ACT == ACT_GELU) {
-        return 0.5f * v * (1.0f + pade_tanh(kGeluC * (v + kGeluA * v * v * v)));
+        return 0.5f * v * (1.0f + pade_tanh<FAST>(kGeluC * (v + kGeluA * v * v * v)));
     } else if constexpr (ACT == ACT_SILU) {
-        return v * pade_sigmoid(v);
+        return v * pade_sigmoid<FAST>(v);
     } else if constexpr (ACT == ACT_MP_SILU) {
-        return v * pade_sigmoid(v) * kMpSiluScale;
+        return v * pade_sigmoid<FAST>(v) * kMpSiluScale;
     } else if constexpr (ACT == ACT_TANH) {
-        return pade_tanh(v);
+        return pade_tanh<FAST>(v);
     } else {
         return v;
     }
 }
 
-template <int ACT>
+template <int ACT, bool FAST = true>
 __device__ __forceinline__ float act_grad(float z) {
     if constexpr (ACT == ACT_RELU) {
         return z > 0.0f ? 1.0f : 0.0f;
     } else if constexpr (ACT == ACT_TANH) {
-        const float t = pade_tanh(z);
+        const float t = pade_tanh<FAST>(z);
         return 1.0f - t * t;
     } else if constexpr (ACT == ACT_SILU) {
-        const float s = pade_sigmoid(z);
+        const float s = pade_sigmoid<FAST>(z);
         return s * (1.0f + z * (1.0f - s));
     } else if constexpr (ACT == ACT_MP_SILU) {
-        const float s = pade_sigmoid(z);
+        const float s = pade_sigmoid<FAST>(z);
         return s * (1.0f + z * (1.0f - s)) * kMpSiluScale;
     } else if constexpr (ACT == ACT_GELU) {
         const float u = kGeluC * (z + kGeluA * z * z * z);
-        const float t = pade_tanh(u);
+        const float t = pade_tanh<FAST>(u);
         const float du = kGeluC * (1.0f + 3.0f * kGeluA * z * z);
         return 0.5f * (1.0f + t) + 0.5f * z * (1.0f - t * t) * du;
     } else {

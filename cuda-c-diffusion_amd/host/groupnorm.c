@@ -13,15 +13,16 @@ typedef struct {
     float *gamma, *beta;
     float *ggamma, *gbeta;
     float *mu, *rstd;
-    float* work;
+    float* work;     /* backward workspace, sized for max_batch */
+    float* fwork;    /* forward workspace, sized for max_batch (NULL when none is needed) */
 } GroupNormState;
 
 static void groupnorm_forward(Module* self, const float* in, float* out, int batch, Context* ctx)
 {
     GroupNormState* st = (GroupNormState*)self->state;
     NN_ASSERT(batch <= st->max_batch, "groupnorm: batch exceeds max_batch");
-    launch_groupnorm_act_forward(out, st->mu, st->rstd, in, st->gamma, st->beta, batch,
-        st->H * st->W, st->C, st->G, st->eps, st->act, ctx->stream);
+    launch_groupnorm_act_forward_ws(out, st->mu, st->rstd, in, st->gamma, st->beta, batch,
+        st->H * st->W, st->C, st->G, st->eps, st->act, st->fwork, ctx->stream);
 }
 
 static void groupnorm_backward(Module* self, const float* in, const float* out,
@@ -52,6 +53,7 @@ static void groupnorm_free(Module* self)
     (void)hipFree(st->mu);
     (void)hipFree(st->rstd);
     (void)hipFree(st->work);
+    if (st->fwork) (void)hipFree(st->fwork);
     free(st);
     free(self);
 }
@@ -76,6 +78,13 @@ static Module* groupnorm_make(int C, int num_groups, int H, int W, int max_batch
     st->mu = nn_device_alloc((size_t)max_batch * num_groups);
     st->rstd = nn_device_alloc((size_t)max_batch * num_groups);
     st->work = nn_device_alloc(nnhip_groupnorm_backward_workspace(max_batch, H * W, C, num_groups));
+    {
+        /* The forward need grows with the batch, so the max_batch size covers
+         * every smaller batch; 0 means no workspace (the launcher then draws
+         * one from the stream-ordered pool if a smaller batch wants one). */
+        const size_t fw = nnhip_groupnorm_forward_workspace(max_batch, H * W, C, num_groups);
+        st->fwork = fw ? nn_device_alloc(fw) : NULL;
+    }
 
     float* ones = (float*)malloc((size_t)C * sizeof(float));
     for (int i = 0; i < C; ++i) ones[i] = 1.0f;

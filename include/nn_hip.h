@@ -198,13 +198,20 @@ void launch_groupnorm_act_backward(float* dx, float* ggamma, float* gbeta,
     const float* mu, const float* rstd,
     int batch, int HW, int C, int G, Activation act, hipStream_t s);
 
-/* Number of floats of device workspace that the *_ws backward variants need. */
+/* Number of floats of device workspace that the *_ws variants need (0 when a
+   shape needs none). */
+size_t nnhip_groupnorm_forward_workspace(int batch, int HW, int C, int G);
 size_t nnhip_groupnorm_backward_workspace(int batch, int HW, int C, int G);
 size_t nnhip_layernorm_backward_workspace(int batch, int C);
 
 /* Workspace variants: identical results; the caller lends `workspace` (at least
    the size reported above, 16-byte aligned) instead of the launcher drawing it
-   from the stream-ordered pool.  Used by the host modules. */
+   from the stream-ordered pool.  Launches that may run concurrently need
+   separate workspaces.  Used by the host modules and the benchmark. */
+void launch_groupnorm_act_forward_ws(float* y, float* mu, float* rstd,
+    const float* x, const float* gamma, const float* beta,
+    int batch, int HW, int C, int G, float eps, Activation act,
+    float* workspace, hipStream_t s);
 void launch_groupnorm_act_backward_ws(float* dx, float* ggamma, float* gbeta,
     const float* dy, const float* x, const float* gamma, const float* beta,
     const float* mu, const float* rstd,
@@ -214,6 +221,13 @@ void launch_layernorm_backward_ws(float* grad_in, float* ggamma, float* gbeta,
     const float* grad_out, const float* x, const float* gamma,
     const float* mu, const float* rstd,
     int batch, int C, float* workspace, hipStream_t s);
+
+/* Large GroupNorm launches use persistent workgroups that exchange per-tile
+   statistics through the workspace and wait for each other with bounded
+   polls.  Returns 1 when a wait in the last launch on `workspace` exceeded its
+   bound (its outputs are then not valid), 0 otherwise, < 0 on a HIP error.
+   Synchronous (reads one word of device memory). */
+int nnhip_groupnorm_workspace_status(const float* workspace);
 
 /* grad_im = col2im(grad_col) written, not accumulated: the same fixed order as
    launch_col2im starting from +0.0f.  Replaces the caller's memset + col2im pair

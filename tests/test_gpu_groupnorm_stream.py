@@ -1,0 +1,193 @@
+"""Streaming GroupNorm (+ fused activation) parity: the persistent-grid
+kernels that exchange per-tile group statistics through the workspace.
+
+Same maths as the register-resident path (reference src/kernels.cu:622-745,
+GN -> activation as in src/conv_residual.c:28-29, 51-52), different schedule:
+tiles of 256 (forward) / 128 (backward) pixel rows x 128 channels, records
+merged across workgroups.  NNHIP_GN_PATH=stream forces the path for every
+shape it accepts; the unset (auto) policy takes it from 4 Mi elements on.
+
+Each case also checks that the streaming kernels really ran (the workspace
+holds this launch's epoch-tagged records) and that no statistics wait ran out
+of polls (workspace status 0).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from helpers import TOL, assert_bits_equal, gn_param_floor, rel_err
+from test_gpu_groupnorm import effective_terms, make_inputs
+
+pytestmark = pytest.mark.gpu
+
+FWD_TP, BWD_TP, COLS = 256, 128, 128  # pixel rows per tile (fwd, bwd), channels per column block
+
+SHAPES = [
+    # B, H, W, C, G
+    (1, 64, 64, 256, 32),    # cpg 8: fwd 16 / bwd 32 tiles per sample and column block
+    (3, 64, 64, 256, 32),    # fewer tiles than workgroups: idle workgroups
+    (2, 32, 32, 128, 32),    # cpg 4, one column block
+    (2, 16, 16, 256, 16),    # cpg 16, one forward tile per sample
+    (4, 32, 32, 512, 32),    # cpg 16, four column blocks
+    (1, 64, 128, 128, 32),   # cpg 4: backward merges 2 records per lane
+    (1, 128, 128, 256, 32),  # cpg 8: backward merges 2 records per lane
+    (1, 128, 128, 128, 32),  # cpg 4: forward merges 2 per lane; backward too large -> register/generic path
+]
+
+
+def tiles(B, HW, C, G, tp):
+    """(applicable, records) of the streaming plan for this geometry."""
+    cpg = C // G
+    if cpg not in (4, 8, 16) or C % COLS or HW % tp:
+        return False, 0
+    T = HW // tp
+    gt = COLS // cpg
+    if T & (T - 1) or T > 2 * (1024 // gt):
+        return False, 0
+    return True, B * (C // COLS) * T * gt * 2
+
+
+def records_tagged(ws, nrec):
+    """True when the nrec 64-bit records after the 256-byte header all carry
+    one non-zero epoch in their upper words."""
+    u = ws.download().view(np.uint32)
+    hi = u[64:64 + 2 * nrec][1::2]
+    return hi.size == nrec and hi[0] != 0 and bool(np.all(hi == hi[0]))
+
+
+def run_fwd(L, x, gamma, beta, G, act, ws=None):
+    B, HW, C = x.shape
+    xd, yd = L.to_device(x), L.alloc(x.size)
+    gd, bd = L.to_device(gamma), L.to_device(beta)
+    mu, rs = L.alloc(B * G), L.alloc(B * G)
+    if ws is None:  # no caller workspace: the launcher draws one from the stream-ordered pool
+        L.launch_groupnorm_act_forward(yd.p, mu.p, rs.p, xd.p, gd.p, bd.p, B, HW, C, G, 1e-5, act, None)
+    else:
+        L.launch_groupnorm_act_forward_ws(yd.p, mu.p, rs.p, xd.p, gd.p, bd.p, B, HW, C, G, 1e-5, act, ws.p, None)
+    L.sync()
+    return yd.download(shape=x.shape), mu.download(), rs.download()
+
+
+def run_bwd(L, dy, x, gamma, beta, mu, rs, G, act, ws=None):
+    B, HW, C = x.shape
+    xd, dyd, dxd = L.to_device(x), L.to_device(dy), L.alloc(x.size)
+    gd, bd = L.to_device(gamma), L.to_device(beta)
+    mud, rsd = L.to_device(mu), L.to_device(rs)
+    ggd, gbd = L.alloc(C), L.alloc(C)
+    if ws is None:
+        L.launch_groupnorm_act_backward(dxd.p, ggd.p, gbd.p, dyd.p, xd.p, gd.p, bd.p, mud.p, rsd.p, B, HW, C, G,
+                                        act, None)
+    else:
+        L.launch_groupnorm_act_backward_ws(dxd.p, ggd.p, gbd.p, dyd.p, xd.p, gd.p, bd.p, mud.p, rsd.p, B, HW, C,
+                                           G, act, ws.p, None)
+    L.sync()
+    return dxd.download(shape=x.shape), ggd.download(), gbd.download()
+
+
+def check_case(L, orc, rng, shape, act):
+    B, H, W, C, G = shape
+    HW = H * W
+    x, gamma, beta, dy = make_inputs(rng, B, H, W, C)
+    fws = L.alloc(max(1, L.nnhip_groupnorm_forward_workspace(B, HW, C, G)))
+    bws = L.alloc(L.nnhip_groupnorm_backward_workspace(B, HW, C, G))
+
+    y_ref, mu_ref, rs_ref = orc.groupnorm_forward(x, gamma, beta, G, 1e-5, act)
+    y, mu, rs = run_fwd(L, x, gamma, beta, G, act, fws)
+    assert rel_err(y, y_ref) <= TOL
+    assert rel_err(mu, mu_ref, floor=1e-3) <= TOL
+    assert rel_err(rs, rs_ref) <= TOL
+    ok, nrec = tiles(B, HW, C, G, FWD_TP)
+    if ok:
+        assert records_tagged(fws, nrec), "forward did not take the streaming path"
+        assert L.nnhip_groupnorm_workspace_status(fws.p) == 0
+
+    dx_ref, gg_ref, gb_ref = orc.groupnorm_backward(dy, x, gamma, beta, mu_ref, rs_ref, G, act)
+    dx, gg, gb = run_bwd(L, dy, x, gamma, beta, mu_ref, rs_ref, G, act, bws)
+    d, xh = effective_terms(orc, x, gamma, beta, mu_ref, rs_ref, dy, G, act)
+    fg, fb = gn_param_floor(d, xh, C)
+    assert rel_err(dx, dx_ref) <= TOL
+    assert rel_err(gg, gg_ref, floor=fg) <= TOL
+    assert rel_err(gb, gb_ref, floor=fb) <= TOL
+    ok, nrec = tiles(B, HW, C, G, BWD_TP)
+    if ok:
+        assert records_tagged(bws, nrec), "backward did not take the streaming path"
+        assert L.nnhip_groupnorm_workspace_status(bws.p) == 0
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("act", [0, 3], ids=["identity", "silu"])
+def test_stream_groupnorm(L, orc, rng, monkeypatch, shape, act):
+    print(f"[case] stream groupnorm act={act} shape={shape}", flush=True)
+    monkeypatch.setenv("NNHIP_GN_PATH", "stream")
+    check_case(L, orc, rng, shape, act)
+
+
+@pytest.mark.parametrize("act", [1, 2, 4, 5], ids=["relu", "gelu", "tanh", "mp_silu"])
+def test_stream_groupnorm_other_activations(L, orc, rng, monkeypatch, act):
+    print(f"[case] stream groupnorm act={act}", flush=True)
+    monkeypatch.setenv("NNHIP_GN_PATH", "stream")
+    check_case(L, orc, rng, (2, 32, 32, 256, 32), act)
+
+
+def test_stream_groupnorm_auto_multi_round(L, orc, rng, monkeypatch):
+    """Auto policy at 24 samples of the north-star sample shape: every
+    workgroup walks several samples (3 forward rounds, 6 backward)."""
+    print("[case] stream groupnorm auto B=24 64x64x256", flush=True)
+    monkeypatch.delenv("NNHIP_GN_PATH", raising=False)
+    check_case(L, orc, rng, (24, 64, 64, 256, 32), 3)
+
+
+def test_stream_groupnorm_pool_workspace_and_determinism(L, orc, rng, monkeypatch):
+    """No caller workspace (pool-drawn, cleared per launch); two launches give
+    bit-identical results (fixed merge and reduction order)."""
+    print("[case] stream groupnorm pool workspace", flush=True)
+    monkeypatch.setenv("NNHIP_GN_PATH", "stream")
+    B, H, W, C, G = 3, 64, 64, 256, 32
+    x, gamma, beta, dy = make_inputs(rng, B, H, W, C)
+    y1, mu1, rs1 = run_fwd(L, x, gamma, beta, G, 3)
+    y2, mu2, rs2 = run_fwd(L, x, gamma, beta, G, 3)
+    assert_bits_equal(y1, y2, "y")
+    assert_bits_equal(mu1, mu2, "mu")
+    assert_bits_equal(rs1, rs2, "rstd")
+    y_ref, mu_ref, rs_ref = orc.groupnorm_forward(x, gamma, beta, G, 1e-5, 3)
+    assert rel_err(y1, y_ref) <= TOL
+    d1 = run_bwd(L, dy, x, gamma, beta, mu_ref, rs_ref, G, 3)
+    d2 = run_bwd(L, dy, x, gamma, beta, mu_ref, rs_ref, G, 3)
+    for a, b, what in zip(d1, d2, ("dx", "dgamma", "dbeta")):
+        assert_bits_equal(a, b, what)
+    dx_ref, _, _ = orc.groupnorm_backward(dy, x, gamma, beta, mu_ref, rs_ref, G, 3)
+    assert rel_err(d1[0], dx_ref) <= TOL
+
+
+def test_stream_groupnorm_workspace_reuse_across_shapes(L, orc, rng, monkeypatch):
+    """One workspace lent to launches of different shapes and directions in a
+    row: records left by an earlier launch never satisfy a later one."""
+    print("[case] stream groupnorm workspace reuse", flush=True)
+    monkeypatch.setenv("NNHIP_GN_PATH", "stream")
+    shapes = [(2, 64, 64, 256, 32), (2, 32, 32, 128, 32), (1, 64, 64, 256, 32)]
+    need = max(max(L.nnhip_groupnorm_forward_workspace(B, H * W, C, G),
+                   L.nnhip_groupnorm_backward_workspace(B, H * W, C, G)) for B, H, W, C, G in shapes)
+    ws = L.alloc(need)
+    for B, H, W, C, G in shapes:
+        x, gamma, beta, dy = make_inputs(rng, B, H, W, C)
+        y_ref, mu_ref, rs_ref = orc.groupnorm_forward(x, gamma, beta, G, 1e-5, 3)
+        y, _, _ = run_fwd(L, x, gamma, beta, G, 3, ws)
+        assert rel_err(y, y_ref) <= TOL
+        dx_ref, _, _ = orc.groupnorm_backward(dy, x, gamma, beta, mu_ref, rs_ref, G, 3)
+        dx, _, _ = run_bwd(L, dy, x, gamma, beta, mu_ref, rs_ref, G, 3, ws)
+        assert rel_err(dx, dx_ref) <= TOL
+        assert L.nnhip_groupnorm_workspace_status(ws.p) == 0
+
+
+def test_reg_path_switch_matches_stream(L, rng, monkeypatch):
+    """NNHIP_GN_PATH=reg and =stream agree to the parity bar on a shape both take."""
+    print("[case] stream vs register path", flush=True)
+    B, H, W, C, G = 2, 64, 64, 256, 32
+    x, gamma, beta, _ = make_inputs(rng, B, H, W, C)
+    monkeypatch.setenv("NNHIP_GN_PATH", "reg")
+    y_reg, _, rs_reg = run_fwd(L, x, gamma, beta, G, 3)
+    monkeypatch.setenv("NNHIP_GN_PATH", "stream")
+    y_str, _, rs_str = run_fwd(L, x, gamma, beta, G, 3)
+    assert rel_err(y_str, y_reg) <= TOL
+    assert rel_err(rs_str, rs_reg) <= TOL
