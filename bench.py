@@ -351,8 +351,9 @@ def main() -> int:
     gd, bd = L.to_device(gamma), L.to_device(beta)
     mu, rs = L.alloc(B * G), L.alloc(B * G)
     gg, gb = L.alloc(C), L.alloc(C)
-    ws = L.alloc(L.nnhip_groupnorm_backward_workspace(B, HW, C, G))
-    fws = L.alloc(max(1, L.nnhip_groupnorm_forward_workspace(B, HW, C, G)))
+    # workspaces zero-filled: their first word is the streaming kernels' timeout flag
+    ws = L.to_device(np.zeros(L.nnhip_groupnorm_backward_workspace(B, HW, C, G), np.float32))
+    fws = L.to_device(np.zeros(max(1, L.nnhip_groupnorm_forward_workspace(B, HW, C, G)), np.float32))
     stream = L.dll.nnhip_stream_create()
     if not stream:
         raise RuntimeError("stream creation failed")
@@ -460,4 +461,9 @@ def main() -> int:
 
 
 if __name__ == "__main__":
-    sys.exit(main())
+    # On success the script ends normally rather than through SystemExit:
+    # rocprofv3 (ROCm 7.2) loses its results when a process that made
+    # cooperative launches exits through sys.exit.
+    rc = main()
+    if rc:
+        sys.exit(rc)

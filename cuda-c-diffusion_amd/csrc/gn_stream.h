@@ -1,5 +1,5 @@
 // gn_stream.h -- streaming NHWC GroupNorm (+ fused activation) for large
-// per-sample groups: the HBM-bound path of the GroupNorm launchers.
+// tensors: the HBM-bound path of the GroupNorm launchers.
 //
 // Reference maths: src/kernels.cu:622-717 (forward statistics, backward-x,
 // backward-param), composed with the activation of src/kernels.cu:21-68 as the
@@ -18,13 +18,21 @@
 //                P a multiple of the tiles per sample, so workgroup w always
 //                owns the same (column block, pixel tile) position and walks
 //                the samples; tile i = round * P + w.
-//   round r    : prefetch tile i+P into registers;
+//   round r    : take tile i from the LDS stage into registers and start the
+//                direct-to-LDS loads of tile i+P into the stage;
 //                phase A on tile i (registers): per-group partial statistics
 //                -> one epoch-tagged 64-bit record per (tile, group, value);
 //                phase B on tile i-P (parked in LDS by the previous round):
 //                read the T records of each of its groups, merge them in a
 //                fixed order, normalise / form dx, store;
 //                park tile i in LDS.
+//
+// Only the current tile occupies registers (a second register tile makes the
+// compiler spill, and every spill reload waits on the in-order vector-memory
+// counter, i.e. on the whole prefetch).  The next tile lands in LDS by itself;
+// the workgroup barriers here wait for LDS operations only, so those loads
+// stay in flight through phases A and B.  Each lane reads back exactly the
+// stage slot its own load wrote, so the stage needs no barrier.
 //
 // Records carry the launch epoch in their upper 32 bits and are written and
 // read with agent-scope atomic 64-bit accesses, so a reader accepts exactly
@@ -52,11 +60,45 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t sample_rsrc(const float* base,
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, (int)bytes, 0x00020000);
 }
 
-// 128-bit buffer load; the whole-vector bit cast keeps all four lanes (taking
-// components of the integer vector one by one lets this hipcc shrink the load).
-__device__ __forceinline__ float4 bload(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-    const f32x4 f = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
-    return make_float4(f.x, f.y, f.z, f.w);
+// Direct-to-LDS 128-bit buffer load: lane i of the wave reads 16 bytes at
+// voff + soff and writes them to wave_slots + i (wave_slots uniform over the wave).
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, float4* wave_slots, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)wave_slots, 16, (int)voff, (int)soff, 0, 0);
+}
+
+// Workgroup barrier for LDS traffic: waits for this wave's LDS operations but
+// not for its vector-memory loads, so the direct-to-LDS loads of the next tile
+// stay in flight across it (__syncthreads' release fence would wait for them:
+// they write LDS).  The signal fences keep the compiler from moving memory
+// accesses across the barrier.
+__device__ __forceinline__ void lds_barrier() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt at their maximum
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// This wave's LDS reads have returned (before a direct-to-LDS load reuses the slots).
+__device__ __forceinline__ void lds_reads_done() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// Make v's loads complete here.  Values loaded before the tile pipeline and
+// used inside it would otherwise make the compiler's wait at their first use
+// inside the loop a full vector-memory wait, i.e. a wait for the staged tile.
+__device__ __forceinline__ void settle(const float4& v) {
+    asm volatile("" ::"v"(v.x), "v"(v.y), "v"(v.z), "v"(v.w));
+}
+
+// Same for prefetched records, on every lane of the wave: a prefetch that
+// stays pending on lanes that never consume it makes the compiler fully drain
+// the vector-memory counter before it reuses those registers.
+template <int N>
+__device__ __forceinline__ void settle(const unsigned long long (&r)[N]) {
+#pragma unroll
+    for (int u = 0; u < N; ++u) asm volatile("" ::"v"(r[u]));
 }
 
 __device__ __forceinline__ unsigned long long tagged(unsigned long long tag, float v) {
@@ -131,7 +173,7 @@ struct Shape {
 // Workspace layout (device): [err u32 (padded to 256 B)] [records u64] [channel partials f32].
 struct Work {
     unsigned* err;
-    unsigned long long* rec;   // ntiles * GT * 2
+    unsigned long long* rec;   // ntiles * GT * 2, [sample, column block][group][value][pixel tile]
     float* cpart;              // bwd: P * 2 * (4 * CW4)
 };
 
@@ -154,7 +196,8 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
     const float* __restrict__ beta, Shape sh, Work wk, float eps, unsigned epoch, unsigned spin_limit) {
 #pragma clang fp contract(fast)
     constexpr int NW = Gm::NW, NV = Gm::NV, GT = Gm::GT, TPB = Gm::TPB, CW4 = Gm::CW4;
-    extern __shared__ float4 parked[];          // NV * TPB float4: the tile awaiting phase B
+    __shared__ float4 stage[NV * TPB];          // next tile, written by direct-to-LDS loads
+    __shared__ float4 parked[NV * TPB];         // the tile awaiting phase B
     // Double-buffered by loop parity pb: consecutive phase A's (and phase B's)
     // may run with no barrier between them (first and last rounds), so a
     // buffer is rewritten only two phases later, past the other phase's barrier.
@@ -171,22 +214,29 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
     const uint32_t voff = (uint32_t)(row0 * sh.C + c0) * 4u;
     const uint32_t row_bytes = (uint32_t)sh.C * 4u;
     const float4 gm = ld4(gamma + c0), bt = ld4(beta + c0);
+    settle(gm);
+    settle(bt);
     const float nthr = (float)(NV * 4);
     const unsigned long long tag = (unsigned long long)epoch << 32;
-    // merge role in phase B: LPG = T / RPL lanes per group (a power of two,
-    // at most TPB / GT); lane rj merges records rj, rj + LPG, ... (RPL of them)
+    // merge role in phase B: LPG = T / RPL lanes per group (a power of two, at
+    // most one wave and TPB / GT, so a group's mergers share a wave); lane rj
+    // merges records rj, rj + LPG, ... (RPL of them)
     const int LPG = T / RPL;
     const int rg = tid / LPG, rj = tid % LPG;
     const bool merger = rg < GT;
 
     auto sample_of = [&](int tile) { return tile / (NCB * T); };
-    auto load_tile = [&](float4 (&v)[NV], int b) {
-        const __amdgpu_buffer_rsrc_t r = sample_rsrc(x + (size_t)b * sh.HW * sh.C, sh.sample_bytes);
+    // Record layout [unit = sample * NCB + column block][group][value][pixel tile]:
+    // the mergers of a group read consecutive tiles, i.e. contiguous records.
+    auto rec_slot = [&](int unit, int g, int tt) { return wk.rec + ((size_t)(unit * GT + g) * 2) * T + tt; };
+    auto issue = [&](int tile) {  // start the loads of `tile` into this thread's stage slots
+        const __amdgpu_buffer_rsrc_t r = sample_rsrc(x + (size_t)sample_of(tile) * sh.HW * sh.C, sh.sample_bytes);
         const uint32_t base = (uint32_t)(t * Gm::TP) * row_bytes;
 #pragma unroll
-        for (int k = 0; k < NV; ++k) v[k] = bload(r, voff, base + (uint32_t)(k * Gm::RSTEP) * row_bytes);
+        for (int k = 0; k < NV; ++k)
+            dma16(r, stage + k * TPB + wid * kWave, voff, base + (uint32_t)(k * Gm::RSTEP) * row_bytes);
     };
-    auto phase_a = [&](float4 (&v)[NV], int tile, int pb) {
+    auto phase_a = [&](const float4 (&v)[NV], int tile, int pb) {
         float s = 0.0f;
 #pragma unroll
         for (int k = 0; k < NV; ++k) s += (v[k].x + v[k].y) + (v[k].z + v[k].w);
@@ -205,7 +255,7 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
             wred[pb][wid][gl][0] = m;
             wred[pb][wid][gl][1] = q;
         }
-        __syncthreads();
+        lds_barrier();
         if (tid < GT) {
             float mm[NW], qq[NW];
 #pragma unroll
@@ -219,23 +269,36 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
                 for (int i = 0; i < half; ++i) chan_merge_eq(mm[i], qq[i], mm[i + half], qq[i + half], cnt);
                 cnt *= 2.0f;
             }
-            unsigned long long* r = wk.rec + ((size_t)tile * GT + tid) * 2;
+            unsigned long long* r = rec_slot(tile / T, tid, tile % T);
             rec_store(r, tagged(tag, mm[0]));
-            rec_store(r + 1, tagged(tag, qq[0]));
+            rec_store(r + T, tagged(tag, qq[0]));
+        }
+    };
+    // Every lane loads (lanes past the mergers read group GT-1 and ignore it):
+    // a branch here would put a path without these loads in front of the
+    // staged-tile wait.
+    auto records_prefetch = [&](int tile, unsigned long long (&r0)[RPL], unsigned long long (&r1)[RPL]) {
+        const int rgc = merger ? rg : GT - 1;
+#pragma unroll
+        for (int u = 0; u < RPL; ++u) {
+            const unsigned long long* p = rec_slot(tile / T, rgc, rj + u * LPG);
+            r0[u] = rec_load(p);
+            r1[u] = rec_load(p + T);
         }
     };
     auto phase_b = [&](int tile, const unsigned long long (&r0)[RPL], const unsigned long long (&r1)[RPL], int pb) {
         const int b = sample_of(tile);
+        settle(r0);
+        settle(r1);
         if (merger) {
             // lane rj merges records rj, rj+LPG, ... of group rg in tile order, then a fixed xor tree
             const float ntile = (float)(Gm::TP * Gm::CPG4 * 4);
             float n = 0.0f, m = 0.0f, q = 0.0f;
-            const size_t unit = (size_t)b * NCB + cb;
 #pragma unroll
             for (int u = 0; u < RPL; ++u) {
-                const unsigned long long* p = wk.rec + (((unit * T) + rj + u * LPG) * GT + rg) * 2;
+                const unsigned long long* p = rec_slot(tile / T, rg, rj + u * LPG);
                 const float mj = rec_wait(p, r0[u], epoch, spin_limit, wk.err);
-                const float qj = rec_wait(p + 1, r1[u], epoch, spin_limit, wk.err);
+                const float qj = rec_wait(p + T, r1[u], epoch, spin_limit, wk.err);
                 if (u == 0) {
                     n = ntile;
                     m = mj;
@@ -253,7 +316,7 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
                 stat[pb][rg][1] = rsqrtf(q / n + eps);
             }
         }
-        __syncthreads();
+        lds_barrier();
         const float mean = stat[pb][gl][0], rs = stat[pb][gl][1];
         if (t == 0 && tid < GT) {
             mu_out[b * sh.G + cb * GT + tid] = stat[pb][tid][0];
@@ -271,56 +334,59 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
             st4(ys + (size_t)(k * Gm::RSTEP) * sh.C, o);
         }
     };
-    auto records_prefetch = [&](int tile, unsigned long long (&r0)[RPL], unsigned long long (&r1)[RPL]) {
-        if (!merger) return;
-        const int b = sample_of(tile);
-        const size_t unit = (size_t)b * NCB + cb;
+
+    // Tile i = round * P + w; its sample = i / (NCB * T).  The rounds are laid
+    // out as prologue / steady loop / last tile / final phase B so that the
+    // steady loop has no branch around its loads: the compiler's waits for the
+    // records and the staged tile then count only older operations instead of
+    // draining the counter at a control-flow merge.
+    const int nt = sh.ntiles;
+    if (w >= nt) return;
+    float4 v[NV];
+    auto take = [&]() {
 #pragma unroll
-        for (int u = 0; u < RPL; ++u) {
-            const unsigned long long* p = wk.rec + (((unit * T) + rj + u * LPG) * GT + rg) * 2;
-            r0[u] = rec_load(p);
-            r1[u] = rec_load(p + 1);
-        }
+        for (int k = 0; k < NV; ++k) v[k] = stage[k * TPB + tid];
     };
-    auto park = [&](float4 (&v)[NV]) {
+    auto park = [&]() {
 #pragma unroll
         for (int k = 0; k < NV; ++k) parked[k * TPB + tid] = v[k];
     };
-
-    // tile i = round * P + w; its sample = i / (NCB * T)
-    float4 ra[NV], rb[NV];
-    int tA = w, tB = -1;
-    const int nt = sh.ntiles;
-    if (tA < nt) load_tile(ra, sample_of(tA));
-    for (;;) {
-        unsigned long long r0[RPL], r1[RPL];
-        int tN = tA < nt ? tA + P : nt;
-        if (tN < nt) load_tile(rb, sample_of(tN));
-        if (tB >= 0) records_prefetch(tB, r0, r1);
-        if (tA < nt) phase_a(ra, tA, 0);
-        if (tB >= 0) phase_b(tB, r0, r1, 0);
-        if (tA < nt) {
-            park(ra);
-            tB = tA;
-        } else {
-            tB = -1;
-        }
-        tA = tN;
-        if (tA >= nt && tB < 0) break;
-        tN = tA < nt ? tA + P : nt;
-        if (tN < nt) load_tile(ra, sample_of(tN));
-        if (tB >= 0) records_prefetch(tB, r0, r1);
-        if (tA < nt) phase_a(rb, tA, 1);
-        if (tB >= 0) phase_b(tB, r0, r1, 1);
-        if (tA < nt) {
-            park(rb);
-            tB = tA;
-        } else {
-            tB = -1;
-        }
-        tA = tN;
-        if (tA >= nt && tB < 0) break;
+    unsigned long long r0[RPL] = {}, r1[RPL] = {};
+    int tA = w, pb = 0;
+    issue(tA);
+    take();
+    if (tA + P < nt) {
+        lds_reads_done();
+        issue(tA + P);
     }
+    phase_a(v, tA, pb);
+    park();
+    int tB = tA;
+    tA += P;
+    pb ^= 1;
+    while (tA + P < nt) {
+        records_prefetch(tB, r0, r1);
+        take();
+        lds_reads_done();
+        issue(tA + P);
+        phase_a(v, tA, pb);
+        phase_b(tB, r0, r1, pb);
+        park();
+        tB = tA;
+        tA += P;
+        pb ^= 1;
+    }
+    if (tA < nt) {
+        records_prefetch(tB, r0, r1);
+        take();
+        phase_a(v, tA, pb);
+        phase_b(tB, r0, r1, pb);
+        park();
+        tB = tA;
+        pb ^= 1;
+    }
+    records_prefetch(tB, r0, r1);
+    phase_b(tB, r0, r1, pb);
 }
 
 // ---------------------------------------------------------------------------
@@ -334,12 +400,11 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, const
     unsigned spin_limit) {
 #pragma clang fp contract(fast)
     constexpr int NW = Gm::NW, NV = Gm::NV, GT = Gm::GT, TPB = Gm::TPB, CW4 = Gm::CW4;
-    extern __shared__ float4 parked[];          // 2 * NV * TPB float4: xhat then g of the tile awaiting phase B
-    // Double-buffered by loop parity pb: consecutive phase A's (and phase B's)
-    // may run with no barrier between them (first and last rounds), so a
-    // buffer is rewritten only two phases later, past the other phase's barrier.
-    __shared__ float wred[2][NW][GT][2];
+    __shared__ float4 stage[2 * NV * TPB];      // x then dy of the next tile (direct-to-LDS loads)
+    __shared__ float4 parked[2 * NV * TPB];     // xhat then g of the tile awaiting phase B
+    __shared__ float wred[2][NW][GT][2];        // double-buffered by loop parity, as in the forward
     __shared__ float stat[2][GT][2];
+    __shared__ float cred[NW][CW4][8];          // per-wave dgamma/dbeta sums at the end
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
     const int col = lane % CW4, row0 = wid * Gm::RW + lane / CW4;
     const int gl = col / Gm::CPG4;
@@ -354,6 +419,8 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, const
     const float4 gm = ld4(gamma + c0);
     float4 bt = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if constexpr (ACT != ACT_IDENTITY) bt = ld4(beta + c0);
+    settle(gm);
+    settle(bt);
     const unsigned long long tag = (unsigned long long)epoch << 32;
     const int LPG = T / RPL;
     const int rg = tid / LPG, rj = tid % LPG;
@@ -361,15 +428,20 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, const
     float4 cg = make_float4(0.0f, 0.0f, 0.0f, 0.0f), cbs = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 
     auto sample_of = [&](int tile) { return tile / (NCB * T); };
-    auto load_tile = [&](float4 (&xv)[NV], float4 (&gv)[NV], int b) {
-        const size_t so = (size_t)b * sh.HW * sh.C;
+    // Record layout [unit = sample * NCB + column block][group][value][pixel tile]:
+    // the mergers of a group read consecutive tiles, i.e. contiguous records.
+    auto rec_slot = [&](int unit, int g, int tt) { return wk.rec + ((size_t)(unit * GT + g) * 2) * T + tt; };
+    auto issue = [&](int tile) {
+        const size_t so = (size_t)sample_of(tile) * sh.HW * sh.C;
         const __amdgpu_buffer_rsrc_t rx = sample_rsrc(x + so, sh.sample_bytes);
         const __amdgpu_buffer_rsrc_t rd = sample_rsrc(dy + so, sh.sample_bytes);
         const uint32_t base = (uint32_t)(t * Gm::TP) * row_bytes;
 #pragma unroll
-        for (int k = 0; k < NV; ++k) xv[k] = bload(rx, voff, base + (uint32_t)(k * Gm::RSTEP) * row_bytes);
+        for (int k = 0; k < NV; ++k)
+            dma16(rx, stage + k * TPB + wid * kWave, voff, base + (uint32_t)(k * Gm::RSTEP) * row_bytes);
 #pragma unroll
-        for (int k = 0; k < NV; ++k) gv[k] = bload(rd, voff, base + (uint32_t)(k * Gm::RSTEP) * row_bytes);
+        for (int k = 0; k < NV; ++k)
+            dma16(rd, stage + (NV + k) * TPB + wid * kWave, voff, base + (uint32_t)(k * Gm::RSTEP) * row_bytes);
     };
     // phase A: xv -> xhat, gv -> g in place; per-group S1 = sum g, S2 = sum g*xhat -> records
     auto phase_a = [&](float4 (&xv)[NV], float4 (&gv)[NV], int tile, float mean, float rs, int pb) {
@@ -414,7 +486,7 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, const
             wred[pb][wid][gl][0] = s1;
             wred[pb][wid][gl][1] = s2;
         }
-        __syncthreads();
+        lds_barrier();
         if (tid < GT) {
             float a = wred[pb][0][tid][0], c = wred[pb][0][tid][1];
 #pragma unroll
@@ -422,32 +494,35 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, const
                 a += wred[pb][i][tid][0];
                 c += wred[pb][i][tid][1];
             }
-            unsigned long long* r = wk.rec + ((size_t)tile * GT + tid) * 2;
+            unsigned long long* r = rec_slot(tile / T, tid, tile % T);
             rec_store(r, tagged(tag, a));
-            rec_store(r + 1, tagged(tag, c));
+            rec_store(r + T, tagged(tag, c));
         }
     };
+    // Every lane loads (lanes past the mergers read group GT-1 and ignore it):
+    // a branch here would put a path without these loads in front of the
+    // staged-tile wait.
     auto records_prefetch = [&](int tile, unsigned long long (&r0)[RPL], unsigned long long (&r1)[RPL]) {
-        if (!merger) return;
-        const size_t unit = (size_t)sample_of(tile) * NCB + cb;
+        const int rgc = merger ? rg : GT - 1;
 #pragma unroll
         for (int u = 0; u < RPL; ++u) {
-            const unsigned long long* p = wk.rec + (((unit * T) + rj + u * LPG) * GT + rg) * 2;
+            const unsigned long long* p = rec_slot(tile / T, rgc, rj + u * LPG);
             r0[u] = rec_load(p);
-            r1[u] = rec_load(p + 1);
+            r1[u] = rec_load(p + T);
         }
     };
     auto phase_b = [&](int tile, const unsigned long long (&r0)[RPL], const unsigned long long (&r1)[RPL],
                        float rs, int pb) {
         const int b = sample_of(tile);
+        settle(r0);
+        settle(r1);
         if (merger) {
-            const size_t unit = (size_t)b * NCB + cb;
             float a = 0.0f, c = 0.0f;
 #pragma unroll
             for (int u = 0; u < RPL; ++u) {
-                const unsigned long long* p = wk.rec + (((unit * T) + rj + u * LPG) * GT + rg) * 2;
+                const unsigned long long* p = rec_slot(tile / T, rg, rj + u * LPG);
                 a += rec_wait(p, r0[u], epoch, spin_limit, wk.err);
-                c += rec_wait(p + 1, r1[u], epoch, spin_limit, wk.err);
+                c += rec_wait(p + T, r1[u], epoch, spin_limit, wk.err);
             }
             for (int o = 1; o < LPG; o <<= 1) {
                 a += __shfl_xor(a, o, kWave);
@@ -458,7 +533,7 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, const
                 stat[pb][rg][1] = c * sh.inv_n;
             }
         }
-        __syncthreads();
+        lds_barrier();
         const float m1 = stat[pb][gl][0], m2 = stat[pb][gl][1];
         float* dxs = dx + (size_t)b * sh.HW * sh.C + (size_t)(t * Gm::TP + row0) * sh.C + c0;
 #pragma unroll
@@ -474,80 +549,79 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, const
         }
     };
 
-    auto park = [&](const float4 (&xh)[NV], const float4 (&g)[NV]) {
-#pragma unroll
-        for (int k = 0; k < NV; ++k) {
-            parked[k * TPB + tid] = xh[k];
-            parked[(NV + k) * TPB + tid] = g[k];
-        }
-    };
-
-    float4 xa[NV], ga[NV], xb[NV], gb[NV];
-    int tA = w, tB = -1;
-    float rsB = 0.0f;
+    // Rounds laid out as in the forward (prologue / steady loop / last tile /
+    // final phase B); mean and rstd of a tile are loaded with its data.
     const int nt = sh.ntiles;
-    float meanA = 0.0f, rsA = 0.0f;
-    if (tA < nt) {
-        const int b = sample_of(tA);
-        load_tile(xa, ga, b);
-        meanA = mu[b * sh.G + gglob];
-        rsA = rstd[b * sh.G + gglob];
-    }
-    for (;;) {
-        unsigned long long r0[RPL], r1[RPL];
-        int tN = tA < nt ? tA + P : nt;
-        float meanN = 0.0f, rsN = 0.0f;
-        if (tN < nt) {
-            const int b = sample_of(tN);
-            load_tile(xb, gb, b);
-            meanN = mu[b * sh.G + gglob];
-            rsN = rstd[b * sh.G + gglob];
+    if (w < nt) {
+        float4 xv[NV], gv[NV];
+        auto take = [&]() {
+#pragma unroll
+            for (int k = 0; k < NV; ++k) {
+                xv[k] = stage[k * TPB + tid];
+                gv[k] = stage[(NV + k) * TPB + tid];
+            }
+        };
+        auto park = [&]() {
+#pragma unroll
+            for (int k = 0; k < NV; ++k) {
+                parked[k * TPB + tid] = xv[k];
+                parked[(NV + k) * TPB + tid] = gv[k];
+            }
+        };
+        float meanA, rsA, meanN = 0.0f, rsN = 0.0f;
+        auto issue_with_stats = [&](int tile, float& mean, float& rs) {
+            const int b = sample_of(tile);
+            mean = mu[b * sh.G + gglob];
+            rs = rstd[b * sh.G + gglob];
+            issue(tile);
+        };
+        unsigned long long r0[RPL] = {}, r1[RPL] = {};
+        int tA = w, pb = 0;
+        issue_with_stats(tA, meanA, rsA);
+        take();
+        if (tA + P < nt) {
+            lds_reads_done();
+            issue_with_stats(tA + P, meanN, rsN);
         }
-        if (tB >= 0) records_prefetch(tB, r0, r1);
-        if (tA < nt) phase_a(xa, ga, tA, meanA, rsA, 0);
-        if (tB >= 0) phase_b(tB, r0, r1, rsB, 0);
-        if (tA < nt) {
-            park(xa, ga);
-            tB = tA;
-            rsB = rsA;
-        } else {
-            tB = -1;
-        }
-        tA = tN;
+        phase_a(xv, gv, tA, meanA, rsA, pb);
+        park();
+        int tB = tA;
+        float rsB = rsA;
+        tA += P;
         meanA = meanN;
         rsA = rsN;
-        if (tA >= nt && tB < 0) break;
-        tN = tA < nt ? tA + P : nt;
-        meanN = 0.0f;
-        rsN = 0.0f;
-        if (tN < nt) {
-            const int b = sample_of(tN);
-            load_tile(xa, ga, b);
-            meanN = mu[b * sh.G + gglob];
-            rsN = rstd[b * sh.G + gglob];
-        }
-        if (tB >= 0) records_prefetch(tB, r0, r1);
-        if (tA < nt) phase_a(xb, gb, tA, meanA, rsA, 1);
-        if (tB >= 0) phase_b(tB, r0, r1, rsB, 1);
-        if (tA < nt) {
-            park(xb, gb);
+        pb ^= 1;
+        while (tA + P < nt) {
+            records_prefetch(tB, r0, r1);
+            take();
+            lds_reads_done();
+            issue_with_stats(tA + P, meanN, rsN);
+            phase_a(xv, gv, tA, meanA, rsA, pb);
+            phase_b(tB, r0, r1, rsB, pb);
+            park();
             tB = tA;
             rsB = rsA;
-        } else {
-            tB = -1;
+            tA += P;
+            meanA = meanN;
+            rsA = rsN;
+            pb ^= 1;
         }
-        tA = tN;
-        meanA = meanN;
-        rsA = rsN;
-        if (tA >= nt && tB < 0) break;
+        if (tA < nt) {
+            records_prefetch(tB, r0, r1);
+            take();
+            phase_a(xv, gv, tA, meanA, rsA, pb);
+            phase_b(tB, r0, r1, rsB, pb);
+            park();
+            tB = tA;
+            rsB = rsA;
+            pb ^= 1;
+        }
+        records_prefetch(tB, r0, r1);
+        phase_b(tB, r0, r1, rsB, pb);
     }
 
     // dgamma/dbeta partials of this workgroup: lanes with equal column own the
     // same 4 channels; sum over the wave's rows, then over the waves in order.
-    // The parked region is free now and holds the per-wave sums.
-    static_assert(NW * CW4 * 8 <= 2 * NV * TPB * 4, "channel partials fit the parked region");
-    float(*cred)[CW4][8] = reinterpret_cast<float(*)[CW4][8]>(parked);
-    __syncthreads();  // every thread has finished its last phase B read of the parked tile
     float c8[8] = {cg.x, cg.y, cg.z, cg.w, cbs.x, cbs.y, cbs.z, cbs.w};
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -575,14 +649,16 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, const
 // ---------------------------------------------------------------------------
 // Host side (k_gns_fwd.hip / k_gns_bwd.hip).
 // ---------------------------------------------------------------------------
-// Streaming geometry: 1024 threads, half-row tiles of 32 float4 (128
-// channels); forward tiles of 256 pixel rows, backward of 128.
+// Streaming geometry: 1024 threads, tiles of 32 float4 columns (128
+// channels); forward tiles of 128 pixel rows, backward of 64 (one tile of
+// each input tensor is 64 KB: the staged and the parked tile fill 128 KB of
+// the workgroup's LDS).
 namespace nnk {
 namespace gns {
 constexpr int kTpb = 1024;
 constexpr int kCw4 = 32;
-constexpr int kFwdTp = 256;
-constexpr int kBwdTp = 128;
+constexpr int kFwdTp = 128;
+constexpr int kBwdTp = 64;
 constexpr int kMaxGrid = 1024;        // persistent workgroups at most
 constexpr unsigned kSpinLimit = 1u << 16;
 
@@ -604,7 +680,7 @@ unsigned next_epoch();
 // Launch the streaming kernels when the shape fits and the device can hold
 // the persistent grid; return false (nothing launched) otherwise.  `ws` is a
 // device workspace of at least plan.ws_floats floats whose records region
-// never holds this launch's epoch (zero-filled once, or cleared by the caller).
+// never holds this launch's epoch (the launchers clear it first).
 bool nnk_gns_forward(int act, float* y, float* mu, float* rstd, const float* x, const float* gamma,
     const float* beta, int B, int HW, int C, int G, float eps, float* ws, hipStream_t s);
 bool nnk_gns_backward(int act, float* dx, float* ggamma, float* gbeta, const float* dy, const float* x,

@@ -24,7 +24,9 @@ Plan make_plan(bool bwd, int B, int HW, int C, int G) {
     const int T = HW / TP;
     if (!is_pow2(T)) return p;
     const int GT = kCw4 / cpg4;
-    const int lpg_max = kTpb / GT;
+    // merging lanes per group: their xor tree runs inside one wave, and the
+    // GT groups' mergers must fit in the workgroup
+    const int lpg_max = kTpb / GT < kWave ? kTpb / GT : kWave;
     int rpl = 0;
     if (T <= lpg_max) rpl = 1;
     else if (T <= 2 * lpg_max) rpl = 2;
@@ -128,14 +130,20 @@ int nnk_gns_grid(const void* fn, int key, size_t lds, int unit) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kDev || key < 0 || key >= kKeys) return 0;
     if (occ_cache[dev][key] == 0) {
-        if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
+        const hipError_t ea =
+            lds ? hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) : hipSuccess;
+        if (ea != hipSuccess) {
             (void)hipGetLastError();
+            nnk_path_note("streaming GroupNorm kernel %d: LDS attribute of %zu bytes: %s", key, lds,
+                hipGetErrorString(ea));
             occ_cache[dev][key] = -1;
             return 0;
         }
         int occ = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, nnk::gns::kTpb, lds) != hipSuccess || occ <= 0) {
+        const hipError_t eo = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, nnk::gns::kTpb, lds);
+        if (eo != hipSuccess || occ <= 0) {
             (void)hipGetLastError();
+            nnk_path_note("streaming GroupNorm kernel %d: occupancy %d (%s)", key, occ, hipGetErrorString(eo));
             occ_cache[dev][key] = -1;
             return 0;
         }
@@ -153,5 +161,8 @@ int nnk_gns_grid(const void* fn, int key, size_t lds, int unit) {
     long long P = (long long)occ_cache[dev][key] * cu_cache[dev];
     if (P > nnk::gns::kMaxGrid) P = nnk::gns::kMaxGrid;
     P = P / unit * unit;
+    if (P <= 0)
+        nnk_path_note("streaming GroupNorm kernel %d: %d resident workgroups < %d tiles per sample row", key,
+            occ_cache[dev][key] * cu_cache[dev], unit);
     return (int)P;
 }

@@ -16,7 +16,7 @@ bool launch(const Plan& p, float* dx, float* ggamma, float* gbeta, const float* 
     const float* gamma, const float* beta, const float* mu, const float* rstd, float* ws, hipStream_t s) {
     using Gm = Geom<kTpb, kBwdTp, kCw4, CPG4>;
     const void* fn = reinterpret_cast<const void*>(&gns_bwd<Gm, ACT, RPL>);
-    const size_t lds = (size_t)2 * Gm::NV * kTpb * sizeof(float4);
+    const size_t lds = 0;  // all LDS is static (stage, parked, reduction buffers)
     const int key = 64 + (ACT * 3 + (CPG4 == 1 ? 0 : CPG4 == 2 ? 1 : 2)) * 2 + (RPL - 1);
     const int P = nnk_gns_grid(fn, key, lds, p.sh.T * p.sh.NCB);
     if (P <= 0) return false;
@@ -30,8 +30,11 @@ bool launch(const Plan& p, float* dx, float* ggamma, float* gbeta, const float* 
     void* args[] = {&dx, const_cast<float**>(&dy), const_cast<float**>(&x), const_cast<float**>(&gamma),
         const_cast<float**>(&beta), const_cast<float**>(&mu), const_cast<float**>(&rstd), &sh, &wk, &epoch,
         &limit};
-    if (hipLaunchCooperativeKernel(fn, dim3((unsigned)P), dim3(kTpb), args, (unsigned)lds, s) != hipSuccess) {
+    const hipError_t e = hipLaunchCooperativeKernel(fn, dim3((unsigned)P), dim3(kTpb), args, (unsigned)lds, s);
+    if (e != hipSuccess) {
         (void)hipGetLastError();
+        nnk_path_note("streaming GroupNorm backward: cooperative launch of %d x %d: %s", P, kTpb,
+            hipGetErrorString(e));
         return false;
     }
     nnk_gns_param_reduce(ggamma, gbeta, wk.cpart, P, sh.T, sh.NCB, sh.C, s);

@@ -14,7 +14,7 @@ bool launch(const Plan& p, float* y, float* mu, float* rstd, const float* x, con
     const float* beta, float eps, float* ws, hipStream_t s) {
     using Gm = Geom<kTpb, kFwdTp, kCw4, CPG4>;
     const void* fn = reinterpret_cast<const void*>(&gns_fwd<Gm, ACT, RPL>);
-    const size_t lds = (size_t)Gm::NV * kTpb * sizeof(float4);
+    const size_t lds = 0;  // all LDS is static (stage, parked, reduction buffers)
     const int key = (ACT * 3 + (CPG4 == 1 ? 0 : CPG4 == 2 ? 1 : 2)) * 2 + (RPL - 1);
     const int P = nnk_gns_grid(fn, key, lds, p.sh.T * p.sh.NCB);
     if (P <= 0) return false;
@@ -27,8 +27,11 @@ bool launch(const Plan& p, float* y, float* mu, float* rstd, const float* x, con
     unsigned limit = kSpinLimit;
     void* args[] = {&y, &mu, &rstd, const_cast<float**>(&x), const_cast<float**>(&gamma),
         const_cast<float**>(&beta), &sh, &wk, &eps, &epoch, &limit};
-    if (hipLaunchCooperativeKernel(fn, dim3((unsigned)P), dim3(kTpb), args, (unsigned)lds, s) != hipSuccess) {
+    const hipError_t e = hipLaunchCooperativeKernel(fn, dim3((unsigned)P), dim3(kTpb), args, (unsigned)lds, s);
+    if (e != hipSuccess) {
         (void)hipGetLastError();
+        nnk_path_note("streaming GroupNorm forward: cooperative launch of %d x %d: %s", P, kTpb,
+            hipGetErrorString(e));
         return false;
     }
     return true;

@@ -235,6 +235,11 @@ bool shape_ok(const char* what, int B, int HW, int C, int G) {
 // and for any size the register-resident kernels cannot take (their
 // alternative is the two-pass generic kernel).
 enum class GnPath { kAuto, kStream, kReg };
+
+// A lent workspace starts with a 256-byte header whose first word is the
+// streaming kernels' wait-timeout flag; only the streaming path writes it
+// (zeroes it, then flags), the others keep their data after the header.
+constexpr size_t kWsHeader = 64;
 constexpr long long kStreamMinElems = 1LL << 22;
 
 GnPath gn_path() {  // read per launch, so a process can switch paths
@@ -332,11 +337,11 @@ void gn_backward_impl(const char* what, float* dx, float* ggamma, float* gbeta, 
     }
     float* scratch = ws;
     if (!scratch) {
-        scratch = nnk_scratch_acquire((size_t)2 * B * C, s, what);
+        scratch = nnk_scratch_acquire(kWsHeader + (size_t)2 * B * C, s, what);
         if (!scratch) return;
     }
-    float* part_g = scratch;
-    float* part_b = scratch + (size_t)B * C;
+    float* part_g = scratch + kWsHeader;  // past the status word of a lent workspace
+    float* part_b = part_g + (size_t)B * C;
     const int cpg = C / G;
     int cfg = -1;
     const int v4pp = reg_v4pp(cpg, HW, x, dy, dx, gamma, cfg);
@@ -424,7 +429,7 @@ void launch_groupnorm_act_backward_ws(float* dx, float* ggamma, float* gbeta, co
 
 size_t nnhip_groupnorm_backward_workspace(int batch, int HW, int C, int G) {
     if (batch <= 0 || C <= 0) return 0;
-    const size_t reg = (size_t)2 * batch * C;
+    const size_t reg = kWsHeader + (size_t)2 * batch * C;
     const nnk::gns::Plan p = nnk::gns::make_plan(true, batch, HW, C, G);
     return p.ok && p.ws_floats > reg ? p.ws_floats : reg;
 }

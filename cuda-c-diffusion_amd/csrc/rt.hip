@@ -42,6 +42,22 @@ void nnk_set_error(int code, const char* fmt, ...) {
     }
 }
 
+// NNHIP_VERBOSE=1: report on stderr why a launcher left its fast path.
+void nnk_path_note(const char* fmt, ...) {
+    static int verbose = -1;
+    if (verbose < 0) {
+        const char* e = getenv("NNHIP_VERBOSE");
+        verbose = (e && e[0] == '1') ? 1 : 0;
+    }
+    if (!verbose) return;
+    va_list ap;
+    va_start(ap, fmt);
+    fputs("nnhip: ", stderr);
+    vfprintf(stderr, fmt, ap);
+    fputc('\n', stderr);
+    va_end(ap);
+}
+
 void nnk_after_launch(const char* what, hipStream_t s) {
     hipError_t e = hipGetLastError();
     if (e == hipSuccess && check_mode()) e = hipStreamSynchronize(s);

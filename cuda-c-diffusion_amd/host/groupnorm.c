@@ -77,13 +77,18 @@ static Module* groupnorm_make(int C, int num_groups, int H, int W, int max_batch
     st->gbeta = nn_device_alloc((size_t)C);
     st->mu = nn_device_alloc((size_t)max_batch * num_groups);
     st->rstd = nn_device_alloc((size_t)max_batch * num_groups);
-    st->work = nn_device_alloc(nnhip_groupnorm_backward_workspace(max_batch, H * W, C, num_groups));
+    {
+        const size_t bw = nnhip_groupnorm_backward_workspace(max_batch, H * W, C, num_groups);
+        st->work = nn_device_alloc(bw);
+        NN_HIP_CHECK(hipMemset(st->work, 0, (bw ? bw : 1) * sizeof(float)));  /* status word starts clear */
+    }
     {
         /* The forward need grows with the batch, so the max_batch size covers
          * every smaller batch; 0 means no workspace (the launcher then draws
          * one from the stream-ordered pool if a smaller batch wants one). */
         const size_t fw = nnhip_groupnorm_forward_workspace(max_batch, H * W, C, num_groups);
         st->fwork = fw ? nn_device_alloc(fw) : NULL;
+        if (st->fwork) NN_HIP_CHECK(hipMemset(st->fwork, 0, fw * sizeof(float)));
     }
 
     float* ones = (float*)malloc((size_t)C * sizeof(float));

@@ -224,8 +224,11 @@ void launch_layernorm_backward_ws(float* grad_in, float* ggamma, float* gbeta,
 
 /* Large GroupNorm launches use persistent workgroups that exchange per-tile
    statistics through the workspace and wait for each other with bounded
-   polls.  Returns 1 when a wait in the last launch on `workspace` exceeded its
-   bound (its outputs are then not valid), 0 otherwise, < 0 on a HIP error.
+   polls.  The first word of a lent workspace is their timeout flag: each such
+   launch zeroes it and sets it when a wait exceeds its bound (the launch's
+   outputs are then not valid); other GroupNorm paths leave it alone.  Returns
+   that word as 1/0 -- the outcome of the last streaming launch on `workspace`,
+   or 0 if none ran on it since it was zero-filled -- or < 0 on a HIP error.
    Synchronous (reads one word of device memory). */
 int nnhip_groupnorm_workspace_status(const float* workspace);
 

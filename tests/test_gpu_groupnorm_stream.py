@@ -3,7 +3,7 @@ kernels that exchange per-tile group statistics through the workspace.
 
 Same maths as the register-resident path (reference src/kernels.cu:622-745,
 GN -> activation as in src/conv_residual.c:28-29, 51-52), different schedule:
-tiles of 256 (forward) / 128 (backward) pixel rows x 128 channels, records
+tiles of 128 (forward) / 64 (backward) pixel rows x 128 channels, records
 merged across workgroups.  NNHIP_GN_PATH=stream forces the path for every
 shape it accepts; the unset (auto) policy takes it from 4 Mi elements on.
 
@@ -21,29 +21,34 @@ from test_gpu_groupnorm import effective_terms, make_inputs
 
 pytestmark = pytest.mark.gpu
 
-FWD_TP, BWD_TP, COLS = 256, 128, 128  # pixel rows per tile (fwd, bwd), channels per column block
+FWD_TP, BWD_TP, COLS = 128, 64, 128  # pixel rows per tile (fwd, bwd), channels per column block
 
 SHAPES = [
     # B, H, W, C, G
-    (1, 64, 64, 256, 32),    # cpg 8: fwd 16 / bwd 32 tiles per sample and column block
-    (3, 64, 64, 256, 32),    # fewer tiles than workgroups: idle workgroups
+    (1, 64, 64, 256, 32),    # cpg 8: fwd 32 / bwd 64 tiles per sample and column block
+    (3, 64, 64, 256, 32),    # forward: fewer tiles than workgroups (idle workgroups)
     (2, 32, 32, 128, 32),    # cpg 4, one column block
-    (2, 16, 16, 256, 16),    # cpg 16, one forward tile per sample
+    (2, 16, 16, 256, 16),    # cpg 16, two forward tiles per sample
     (4, 32, 32, 512, 32),    # cpg 16, four column blocks
-    (1, 64, 128, 128, 32),   # cpg 4: backward merges 2 records per lane
-    (1, 128, 128, 256, 32),  # cpg 8: backward merges 2 records per lane
-    (1, 128, 128, 128, 32),  # cpg 4: forward merges 2 per lane; backward too large -> register/generic path
+    (1, 64, 64, 128, 32),    # cpg 4: backward merges 2 records per lane
+    (1, 64, 128, 256, 32),   # cpg 8: backward merges 2 records per lane
+    (1, 64, 128, 128, 8),    # cpg 16: backward merges 2 records per lane
+    (1, 128, 128, 128, 8),   # cpg 16: forward merges 2 records per lane; backward too large
+    (1, 64, 128, 128, 32),   # cpg 4: forward merges 2 records per lane; backward too large -> register/generic
+    (1, 128, 128, 128, 32),  # cpg 4: neither direction fits the streaming plan
 ]
 
 
-def tiles(B, HW, C, G, tp):
-    """(applicable, records) of the streaming plan for this geometry."""
+def tiles(L, B, HW, C, G, tp):
+    """(applicable, records) of the streaming plan for this geometry.  The
+    persistent grid holds one 1024-thread workgroup per CU (LDS-bound), and a
+    multiple of the tiles per sample row must fit in it."""
     cpg = C // G
     if cpg not in (4, 8, 16) or C % COLS or HW % tp:
         return False, 0
     T = HW // tp
     gt = COLS // cpg
-    if T & (T - 1) or T > 2 * (1024 // gt):
+    if T & (T - 1) or T > 2 * min(64, 1024 // gt) or T * (C // COLS) > L.device_info()["cus"]:
         return False, 0
     return True, B * (C // COLS) * T * gt * 2
 
@@ -97,7 +102,7 @@ def check_case(L, orc, rng, shape, act):
     assert rel_err(y, y_ref) <= TOL
     assert rel_err(mu, mu_ref, floor=1e-3) <= TOL
     assert rel_err(rs, rs_ref) <= TOL
-    ok, nrec = tiles(B, HW, C, G, FWD_TP)
+    ok, nrec = tiles(L, B, HW, C, G, FWD_TP)
     if ok:
         assert records_tagged(fws, nrec), "forward did not take the streaming path"
         assert L.nnhip_groupnorm_workspace_status(fws.p) == 0
@@ -109,7 +114,7 @@ def check_case(L, orc, rng, shape, act):
     assert rel_err(dx, dx_ref) <= TOL
     assert rel_err(gg, gg_ref, floor=fg) <= TOL
     assert rel_err(gb, gb_ref, floor=fb) <= TOL
-    ok, nrec = tiles(B, HW, C, G, BWD_TP)
+    ok, nrec = tiles(L, B, HW, C, G, BWD_TP)
     if ok:
         assert records_tagged(bws, nrec), "backward did not take the streaming path"
         assert L.nnhip_groupnorm_workspace_status(bws.p) == 0
@@ -132,7 +137,7 @@ def test_stream_groupnorm_other_activations(L, orc, rng, monkeypatch, act):
 
 def test_stream_groupnorm_auto_multi_round(L, orc, rng, monkeypatch):
     """Auto policy at 24 samples of the north-star sample shape: every
-    workgroup walks several samples (3 forward rounds, 6 backward)."""
+    workgroup walks several samples (6 forward rounds, 12 backward)."""
     print("[case] stream groupnorm auto B=24 64x64x256", flush=True)
     monkeypatch.delenv("NNHIP_GN_PATH", raising=False)
     check_case(L, orc, rng, (24, 64, 64, 256, 32), 3)
@@ -191,3 +196,21 @@ def test_reg_path_switch_matches_stream(L, rng, monkeypatch):
     y_str, _, rs_str = run_fwd(L, x, gamma, beta, G, 3)
     assert rel_err(y_str, y_reg) <= TOL
     assert rel_err(rs_str, rs_reg) <= TOL
+
+
+def test_workspace_status_untouched_by_register_path(L, orc, rng, monkeypatch):
+    """A zero-filled lent workspace keeps status 0 through register-path
+    launches: their channel partials live after the 256-byte header."""
+    print("[case] workspace status after register path", flush=True)
+    monkeypatch.setenv("NNHIP_GN_PATH", "reg")
+    B, H, W, C, G = 2, 32, 32, 128, 32
+    x, gamma, beta, dy = make_inputs(rng, B, H, W, C)
+    ws = L.to_device(np.zeros(L.nnhip_groupnorm_backward_workspace(B, H * W, C, G), np.float32))
+    _, mu_ref, rs_ref = orc.groupnorm_forward(x, gamma, beta, G, 1e-5, 3)
+    dx_ref, gg_ref, _ = orc.groupnorm_backward(dy, x, gamma, beta, mu_ref, rs_ref, G, 3)
+    dx, gg, _ = run_bwd(L, dy, x, gamma, beta, mu_ref, rs_ref, G, 3, ws)
+    d, xh = effective_terms(orc, x, gamma, beta, mu_ref, rs_ref, dy, G, 3)
+    fg, _ = gn_param_floor(d, xh, C)
+    assert rel_err(dx, dx_ref) <= TOL
+    assert rel_err(gg, gg_ref, floor=fg) <= TOL
+    assert L.nnhip_groupnorm_workspace_status(ws.p) == 0
