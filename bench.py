@@ -10,8 +10,9 @@ x, dy, write dx) = 5,368,709,120 B.
 
 Timing: HIP events on the launch stream around exactly --steps steps after
 --warmup untimed steps, device synchronised on both sides.  The roofline
-object is for the dominant kernel (the backward: 12 B/elem), timed per launch
-with events on the same stream.  cpu_baseline times the oracle's fp32 OpenMP
+object is for the dominant launch, the backward (12 B/elem; one cooperative
+kernel at this shape), timed per launch with events on the same stream; the
+event interval includes the runtime's cooperative-launch overhead.  cpu_baseline times the oracle's fp32 OpenMP
 transcription of the reference kernels on a bounded batch sample on the host.
 
 Prints ONE JSON line.  --gpus N > 1 is not supported (one GPU per box).
@@ -34,13 +35,19 @@ METRIC = "GroupNorm+SiLU fwd+bwd µs and HBM GB/s (% of 8 TB/s peak), N=256 64×
 HBM_PEAK_GBS = 8000.0
 SEED = 410293
 
-# HBM bytes per launch of the dominant (backward) kernel at the north-star
-# shape, from `rocprofv3 --pmc FETCH_SIZE` and `--pmc WRITE_SIZE` runs of this
-# bench, scaled by a plain copy's counters (FETCH x2, WRITE x1); the commands
-# and raw values are in profiles/gn_silu_fwd_bwd_n256_64x64x256.md.
-# Re-measure when the kernel changes.
-TRAFFIC_BYTES = {"gn_bwd_reg<1024, 8, 2, 3>": (2 * 1_056_987 + 1_050_046) * 1024}
-ROOFLINE_KERNEL = "gn_bwd_reg<1024, 8, 2, 3>"
+# The dominant launch is the backward, launch_groupnorm_act_backward_ws, which
+# at the north-star shape (lent, zero-filled workspace) is one cooperative
+# kernel.  Its HBM bytes per launch come from `rocprofv3 --pmc FETCH_SIZE` and
+# `--pmc WRITE_SIZE` runs of this bench (KiB per dispatch), scaled by what the
+# same counters read for the 1 GiB calibration copy (`--calibrate`): FETCH x2,
+# WRITE x1.  The commands and raw values are kept with the rocprof summaries
+# under profiles/.  Re-measure when the kernel changes.
+ROOFLINE_KERNEL = "gns_bwd<Geom<1024, 64, 32, 2>, 3, 1>"
+ROOFLINE_SEQUENCE = ROOFLINE_KERNEL + " (launch_groupnorm_act_backward_ws)"
+_PMC_KIB = {  # kernel: (FETCH_SIZE, WRITE_SIZE) per dispatch
+    ROOFLINE_KERNEL: (1_090_314, 1_081_858),
+}
+TRAFFIC_BYTES = sum(2 * f + w for f, w in _PMC_KIB.values()) * 1024
 
 
 def log(msg: str) -> None:
@@ -311,6 +318,30 @@ def run_suite(L, nn, reps):
     L.dll.nnhip_stream_destroy(stream)
 
 
+def run_calibration(L, reps):
+    """A plain float4 copy of 1 GiB into 1 GiB: the known-size kernel whose
+    FETCH_SIZE / WRITE_SIZE readings give the counters' scale factors."""
+    n = 1 << 28
+    src, dst = L.alloc(n), L.alloc(n)
+    L.dll.nnhip_memset(src.p, 0, n * 4)
+    stream = L.dll.nnhip_stream_create()
+    ev = [L.dll.nnhip_event_create() for _ in range(2)]
+    times = []
+    for _ in range(reps):
+        L.dll.nnhip_event_record(ev[0], stream)
+        L.nnhip_copy_f32(dst.p, src.p, n, stream)
+        L.dll.nnhip_event_record(ev[1], stream)
+        L.dll.nnhip_event_synchronize(ev[1])
+        times.append(1e3 * L.dll.nnhip_event_elapsed_ms(ev[0], ev[1]))
+    L.check("calibrate")
+    us = float(np.median(times))
+    print(json.dumps({"calibration": "copy_f32_kernel", "bytes_read": n * 4, "bytes_written": n * 4, "us": round(us, 2),
+                      "GB_s": round(2 * n * 4 / (us * 1e-6) / 1e9, 1)}), flush=True)
+    for e in ev:
+        L.dll.nnhip_event_destroy(e)
+    L.dll.nnhip_stream_destroy(stream)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -321,11 +352,13 @@ def main() -> int:
     ap.add_argument("--cpu-sample", type=int, default=16, help="batch samples timed on the CPU")
     ap.add_argument("--suite", action="store_true",
                     help="time every hot-path row at its BASELINE config (one JSON line per row) instead")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="run the 1 GiB -> 1 GiB calibration copy (for scaling rocprofv3 FETCH/WRITE_SIZE) instead")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one GPU "
-              f"(the path shards over the batch with no exchange but a 2*C-float dgamma/dbeta "
-              f"all-reduce; see DESIGN.md)", file=sys.stderr)
+              f"(the path would shard over the batch, exchanging only a 2*C-float "
+              f"dgamma/dbeta all-reduce)", file=sys.stderr)
         return 2
 
     from __graft_entry__ import load_package
@@ -339,6 +372,9 @@ def main() -> int:
     if args.suite:
         log(f"[suite] device {info}")
         run_suite(L, nn, max(5, args.steps))
+        return 0
+    if args.calibrate:
+        run_calibration(L, max(1, args.steps))
         return 0
     B, H, W, C, G = args.batch, 64, 64, 256, 32
     HW = H * W
@@ -441,13 +477,13 @@ def main() -> int:
                    "layout": "NHWC", "algorithmic_bytes_per_step": int(algo_bytes),
                    "device": info["arch"]},
         "roofline": {
-            "kernel": ROOFLINE_KERNEL + " + gn_param_reduce (launch_groupnorm_act_backward_ws)",
+            "kernel": ROOFLINE_SEQUENCE,
             "bound": "hbm",
             "achieved": round(bwd_gbs, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(bwd_gbs / HBM_PEAK_GBS, 4),
-            "traffic": TRAFFIC_BYTES.get(ROOFLINE_KERNEL),
+            "traffic": TRAFFIC_BYTES,
             "algorithmic_bytes_per_launch": int(bwd_bytes),
             "avg_launch_us": round(bwd_us, 2),
         },

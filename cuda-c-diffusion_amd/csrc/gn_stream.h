@@ -170,11 +170,11 @@ struct Shape {
     float inv_n;       // 1 / (HW * cpg)
 };
 
-// Workspace layout (device): [err u32 (padded to 256 B)] [records u64] [channel partials f32].
+// Workspace layout (device): [err u32 (padded to 256 B)] [records u64] [channel partials u64].
 struct Work {
     unsigned* err;
     unsigned long long* rec;   // ntiles * GT * 2, [sample, column block][group][value][pixel tile]
-    float* cpart;              // bwd: P * 2 * (4 * CW4)
+    unsigned long long* cpart; // bwd: P * 2 * (4 * CW4) epoch-tagged dgamma/dbeta partials
 };
 
 // Lanes that share this lane's group inside a wave: xor over the column bits
@@ -201,7 +201,7 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
     // Double-buffered by loop parity pb: consecutive phase A's (and phase B's)
     // may run with no barrier between them (first and last rounds), so a
     // buffer is rewritten only two phases later, past the other phase's barrier.
-    __shared__ float wred[2][NW][GT][2];
+    __shared__ float wred[2][GT][NW][2];        // [parity][group][wave][mean, M2]
     __shared__ float stat[2][GT][2];
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
     const int col = lane % CW4, row0 = wid * Gm::RW + lane / CW4;
@@ -252,26 +252,27 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
             cnt *= 2.0f;
         });
         if (lane % CW4 % Gm::CPG4 == 0 && lane < CW4) {
-            wred[pb][wid][gl][0] = m;
-            wred[pb][wid][gl][1] = q;
+            wred[pb][gl][wid][0] = m;
+            wred[pb][gl][wid][1] = q;
         }
         lds_barrier();
-        if (tid < GT) {
-            float mm[NW], qq[NW];
+        // the NW wave partials of group g merge on lanes (g, i = 0..NW-1) of
+        // one wave in a fixed xor tree (the merge is symmetric, so every lane
+        // of the pair holds the same value)
+        static_assert(kWave % NW == 0, "a group's wave partials share a wave");
+        if (tid < GT * NW) {
+            const int g = tid / NW, i = tid % NW;
+            float mm = wred[pb][g][i][0], qq = wred[pb][g][i][1];
 #pragma unroll
-            for (int i = 0; i < NW; ++i) {
-                mm[i] = wred[pb][i][tid][0];
-                qq[i] = wred[pb][i][tid][1];
-            }
-#pragma unroll
-            for (int half = NW / 2; half >= 1; half >>= 1) {
-#pragma unroll
-                for (int i = 0; i < half; ++i) chan_merge_eq(mm[i], qq[i], mm[i + half], qq[i + half], cnt);
+            for (int o = 1; o < NW; o <<= 1) {
+                chan_merge_eq(mm, qq, __shfl_xor(mm, o, kWave), __shfl_xor(qq, o, kWave), cnt);
                 cnt *= 2.0f;
             }
-            unsigned long long* r = rec_slot(tile / T, tid, tile % T);
-            rec_store(r, tagged(tag, mm[0]));
-            rec_store(r + T, tagged(tag, qq[0]));
+            if (i == 0) {
+                unsigned long long* r = rec_slot(tile / T, g, tile % T);
+                rec_store(r, tagged(tag, mm));
+                rec_store(r + T, tagged(tag, qq));
+            }
         }
     };
     // Every lane loads (lanes past the mergers read group GT-1 and ignore it):
@@ -322,15 +323,25 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
             mu_out[b * sh.G + cb * GT + tid] = stat[pb][tid][0];
             rstd_out[b * sh.G + cb * GT + tid] = stat[pb][tid][1];
         }
+        // gamma * (v - mean) * rs + beta = v * sc + sh0 per channel
+        float4 sc, s0;
+        sc.x = gm.x * rs;
+        sc.y = gm.y * rs;
+        sc.z = gm.z * rs;
+        sc.w = gm.w * rs;
+        s0.x = fmaf(-sc.x, mean, bt.x);
+        s0.y = fmaf(-sc.y, mean, bt.y);
+        s0.z = fmaf(-sc.z, mean, bt.z);
+        s0.w = fmaf(-sc.w, mean, bt.w);
         float* ys = y + (size_t)b * sh.HW * sh.C + (size_t)(t * Gm::TP + row0) * sh.C + c0;
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
             const float4 v = parked[k * TPB + tid];
             float4 o;
-            o.x = act_fwd<ACT>(gm.x * ((v.x - mean) * rs) + bt.x);
-            o.y = act_fwd<ACT>(gm.y * ((v.y - mean) * rs) + bt.y);
-            o.z = act_fwd<ACT>(gm.z * ((v.z - mean) * rs) + bt.z);
-            o.w = act_fwd<ACT>(gm.w * ((v.w - mean) * rs) + bt.w);
+            o.x = act_fwd<ACT>(fmaf(v.x, sc.x, s0.x));
+            o.y = act_fwd<ACT>(fmaf(v.y, sc.y, s0.y));
+            o.z = act_fwd<ACT>(fmaf(v.z, sc.z, s0.z));
+            o.w = act_fwd<ACT>(fmaf(v.w, sc.w, s0.w));
             st4(ys + (size_t)(k * Gm::RSTEP) * sh.C, o);
         }
     };
@@ -394,7 +405,8 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
 // recomputed from x, mu, rstd, gamma, beta.  Parks xhat and g = d*gamma.
 // ---------------------------------------------------------------------------
 template <class Gm, int ACT, int RPL>
-__global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, const float* __restrict__ dy,
+__global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float* __restrict__ ggamma,
+    float* __restrict__ gbeta, const float* __restrict__ dy,
     const float* __restrict__ x, const float* __restrict__ gamma, const float* __restrict__ beta,
     const float* __restrict__ mu, const float* __restrict__ rstd, Shape sh, Work wk, unsigned epoch,
     unsigned spin_limit) {
@@ -402,9 +414,9 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, const
     constexpr int NW = Gm::NW, NV = Gm::NV, GT = Gm::GT, TPB = Gm::TPB, CW4 = Gm::CW4;
     __shared__ float4 stage[2 * NV * TPB];      // x then dy of the next tile (direct-to-LDS loads)
     __shared__ float4 parked[2 * NV * TPB];     // xhat then g of the tile awaiting phase B
-    __shared__ float wred[2][NW][GT][2];        // double-buffered by loop parity, as in the forward
+    __shared__ float wred[2][GT][NW][2];        // double-buffered by loop parity, as in the forward
     __shared__ float stat[2][GT][2];
-    __shared__ float cred[NW][CW4][8];          // per-wave dgamma/dbeta sums at the end
+    __shared__ float cred[NW][CW4][8];          // per-wave dgamma/dbeta sums at the end (then the reducer's)
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
     const int col = lane % CW4, row0 = wid * Gm::RW + lane / CW4;
     const int gl = col / Gm::CPG4;
@@ -445,14 +457,15 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, const
     };
     // phase A: xv -> xhat, gv -> g in place; per-group S1 = sum g, S2 = sum g*xhat -> records
     auto phase_a = [&](float4 (&xv)[NV], float4 (&gv)[NV], int tile, float mean, float rs, int pb) {
-        float s1 = 0.0f, s2 = 0.0f;
+        float4 s1v = make_float4(0.0f, 0.0f, 0.0f, 0.0f), s2v = s1v;
+        const float nms = -mean * rs;
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
             float4 xh, d;
-            xh.x = (xv[k].x - mean) * rs;
-            xh.y = (xv[k].y - mean) * rs;
-            xh.z = (xv[k].z - mean) * rs;
-            xh.w = (xv[k].w - mean) * rs;
+            xh.x = fmaf(xv[k].x, rs, nms);
+            xh.y = fmaf(xv[k].y, rs, nms);
+            xh.z = fmaf(xv[k].z, rs, nms);
+            xh.w = fmaf(xv[k].w, rs, nms);
             d = gv[k];
             if constexpr (ACT != ACT_IDENTITY) {
                 d.x = d.x * act_grad<ACT>(gm.x * xh.x + bt.x);
@@ -473,30 +486,43 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, const
             g.y = d.y * gm.y;
             g.z = d.z * gm.z;
             g.w = d.w * gm.w;
-            s1 += (g.x + g.y) + (g.z + g.w);
-            s2 += (g.x * xh.x + g.y * xh.y) + (g.z * xh.z + g.w * xh.w);
+            s1v.x += g.x;
+            s1v.y += g.y;
+            s1v.z += g.z;
+            s1v.w += g.w;
+            s2v.x = fmaf(g.x, xh.x, s2v.x);
+            s2v.y = fmaf(g.y, xh.y, s2v.y);
+            s2v.z = fmaf(g.z, xh.z, s2v.z);
+            s2v.w = fmaf(g.w, xh.w, s2v.w);
             xv[k] = xh;
             gv[k] = g;
         }
+        float s1 = (s1v.x + s1v.y) + (s1v.z + s1v.w);
+        float s2 = (s2v.x + s2v.y) + (s2v.z + s2v.w);
         for_group_xor<Gm>([&](int o) {
             s1 += __shfl_xor(s1, o, kWave);
             s2 += __shfl_xor(s2, o, kWave);
         });
         if (lane % CW4 % Gm::CPG4 == 0 && lane < CW4) {
-            wred[pb][wid][gl][0] = s1;
-            wred[pb][wid][gl][1] = s2;
+            wred[pb][gl][wid][0] = s1;
+            wred[pb][gl][wid][1] = s2;
         }
         lds_barrier();
-        if (tid < GT) {
-            float a = wred[pb][0][tid][0], c = wred[pb][0][tid][1];
+        // wave partials of group g summed on lanes (g, i) in a fixed xor tree
+        static_assert(kWave % NW == 0, "a group's wave partials share a wave");
+        if (tid < GT * NW) {
+            const int g = tid / NW, i = tid % NW;
+            float a = wred[pb][g][i][0], c = wred[pb][g][i][1];
 #pragma unroll
-            for (int i = 1; i < NW; ++i) {
-                a += wred[pb][i][tid][0];
-                c += wred[pb][i][tid][1];
+            for (int o = 1; o < NW; o <<= 1) {
+                a += __shfl_xor(a, o, kWave);
+                c += __shfl_xor(c, o, kWave);
             }
-            unsigned long long* r = rec_slot(tile / T, tid, tile % T);
-            rec_store(r, tagged(tag, a));
-            rec_store(r + T, tagged(tag, c));
+            if (i == 0) {
+                unsigned long long* r = rec_slot(tile / T, g, tile % T);
+                rec_store(r, tagged(tag, a));
+                rec_store(r + T, tagged(tag, c));
+            }
         }
     };
     // Every lane loads (lanes past the mergers read group GT-1 and ignore it):
@@ -534,17 +560,18 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, const
             }
         }
         lds_barrier();
-        const float m1 = stat[pb][gl][0], m2 = stat[pb][gl][1];
+        // dx = rs * ((g - m1) - xhat * m2) = g * rs + (xhat * (-rs m2) + (-rs m1))
+        const float a1 = -rs * stat[pb][gl][0], a2 = -rs * stat[pb][gl][1];
         float* dxs = dx + (size_t)b * sh.HW * sh.C + (size_t)(t * Gm::TP + row0) * sh.C + c0;
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
             const float4 xh = parked[k * TPB + tid];
             const float4 g = parked[(NV + k) * TPB + tid];
             float4 o;
-            o.x = rs * ((g.x - m1) - xh.x * m2);
-            o.y = rs * ((g.y - m1) - xh.y * m2);
-            o.z = rs * ((g.z - m1) - xh.z * m2);
-            o.w = rs * ((g.w - m1) - xh.w * m2);
+            o.x = fmaf(g.x, rs, fmaf(xh.x, a2, a1));
+            o.y = fmaf(g.y, rs, fmaf(xh.y, a2, a1));
+            o.z = fmaf(g.z, rs, fmaf(xh.z, a2, a1));
+            o.w = fmaf(g.w, rs, fmaf(xh.w, a2, a1));
             st4(dxs + (size_t)(k * Gm::RSTEP) * sh.C, o);
         }
     };
@@ -633,13 +660,65 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, const
         for (int j = 0; j < 8; ++j) cred[wid][lane][j] = c8[j];
     }
     __syncthreads();
+    // publish: cpart[w][0 = dgamma, 1 = dbeta][channel within the column block]
     for (int i = tid; i < CW4 * 8; i += TPB) {
         const int cl = i / 8, j = i % 8;
         float acc = cred[0][cl][j];
 #pragma unroll
         for (int ww = 1; ww < NW; ++ww) acc += cred[ww][cl][j];
-        // cpart[w][j>>2][channel within block]
-        wk.cpart[((size_t)w * 2 + (j >> 2)) * (CW4 * 4) + cl * 4 + (j & 3)] = acc;
+        rec_store(wk.cpart + ((size_t)w * 2 + (j >> 2)) * (CW4 * 4) + cl * 4 + (j & 3), tagged(tag, acc));
+    }
+
+    // dgamma/dbeta: workgroup w reduces the 64-channel chunks j = w, w + P, ...
+    // Lane l of wave v sums channel 64 j + l over the owners m = v, v + NW, ...
+    // of its column block (owner m = workgroup ((m / T) NCB + cb) T + m % T) in
+    // ascending m, eight partials in flight at a time; the NW wave sums are
+    // then added in wave order.  Every partial is waited for (bounded).
+    const int nred = (sh.C + kWave - 1) / kWave;
+    const int owners = P / NCB;
+    constexpr int kBatch = 8;
+    static_assert(2 * NW * kWave <= NW * CW4 * 8, "reducer sums fit the partials buffer");
+    float(*rsum)[NW][kWave] = reinterpret_cast<float(*)[NW][kWave]>(&cred[0][0][0]);
+    __syncthreads();  // the publish loop's reads of cred are done
+    for (int j = w; j < nred; j += P) {
+        const int c = j * kWave + lane;
+        float sg = 0.0f, sb = 0.0f;
+        if (c < sh.C) {
+            const int cbc = c / (CW4 * 4), cl = c % (CW4 * 4);
+            for (int m0 = wid; m0 < owners; m0 += NW * kBatch) {
+                unsigned long long vg[kBatch], vb[kBatch];
+                const unsigned long long* pg[kBatch];
+#pragma unroll
+                for (int u = 0; u < kBatch; ++u) {
+                    const int m = m0 + u * NW < owners ? m0 + u * NW : m0;
+                    const int wo = ((m / T) * NCB + cbc) * T + (m % T);
+                    pg[u] = wk.cpart + ((size_t)wo * 2) * (CW4 * 4) + cl;
+                    vg[u] = rec_load(pg[u]);
+                    vb[u] = rec_load(pg[u] + CW4 * 4);
+                }
+#pragma unroll
+                for (int u = 0; u < kBatch; ++u) {
+                    if (m0 + u * NW < owners) {
+                        sg += rec_wait(pg[u], vg[u], epoch, spin_limit, wk.err);
+                        sb += rec_wait(pg[u] + CW4 * 4, vb[u], epoch, spin_limit, wk.err);
+                    }
+                }
+            }
+        }
+        rsum[0][wid][lane] = sg;
+        rsum[1][wid][lane] = sb;
+        __syncthreads();
+        if (wid == 0 && c < sh.C) {
+            float ag = rsum[0][0][lane], ab = rsum[1][0][lane];
+#pragma unroll
+            for (int v = 1; v < NW; ++v) {
+                ag += rsum[0][v][lane];
+                ab += rsum[1][v][lane];
+            }
+            ggamma[c] = ag;
+            gbeta[c] = ab;
+        }
+        __syncthreads();
     }
 }
 

@@ -1,6 +1,6 @@
 // k_gns.hip -- host side shared by the streaming GroupNorm launchers
-// (k_gns_fwd.hip, k_gns_bwd.hip): shape plan, launch epochs, and the
-// deterministic dgamma/dbeta reduction over the persistent workgroups.
+// (k_gns_fwd.hip, k_gns_bwd.hip): shape plan, launch epochs, workspace clear
+// and the persistent grid size.
 #include <atomic>
 
 #include "gn_stream.h"
@@ -49,7 +49,7 @@ Plan make_plan(bool bwd, int B, int HW, int C, int G) {
     p.rec_offset = 256;
     const size_t rec_bytes = (size_t)p.sh.ntiles * GT * 2 * sizeof(unsigned long long);
     p.cpart_offset = p.rec_offset + rec_bytes;
-    const size_t cpart_bytes = bwd ? (size_t)kMaxGrid * 2 * (4 * kCw4) * sizeof(float) : 0;
+    const size_t cpart_bytes = bwd ? (size_t)kMaxGrid * 2 * (4 * kCw4) * sizeof(unsigned long long) : 0;
     p.ws_floats = (p.cpart_offset + cpart_bytes + sizeof(float) - 1) / sizeof(float);
     p.ok = true;
     return p;
@@ -73,52 +73,12 @@ __global__ void gns_clear(unsigned* p, size_t n) {
         p[i] = 0u;
 }
 
-// dgamma/dbeta over the workgroups that own each column block: wave w sums
-// owners m = w, w + 16, ... (ascending), then the 16 wave sums are added in
-// wave order.  Grid: ceil(C / 64) workgroups of 1024 threads.
-__global__ __launch_bounds__(1024) void gns_param_reduce_k(float* __restrict__ ggamma,
-    float* __restrict__ gbeta, const float* __restrict__ cpart, int P, int T, int NCB, int C) {
-    constexpr int kCwc = 4 * nnk::gns::kCw4;
-    __shared__ float lg[16][64];
-    __shared__ float lb[16][64];
-    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-    const int c = blockIdx.x * 64 + lane;
-    float sg = 0.0f, sb = 0.0f;
-    if (c < C) {
-        const int cb = c / kCwc, cl = c % kCwc;
-        const int owners = P / NCB;
-        for (int m = wid; m < owners; m += 16) {
-            const int w = ((m / T) * NCB + cb) * T + (m % T);
-            sg += cpart[((size_t)w * 2) * kCwc + cl];
-            sb += cpart[((size_t)w * 2 + 1) * kCwc + cl];
-        }
-    }
-    lg[wid][lane] = sg;
-    lb[wid][lane] = sb;
-    __syncthreads();
-    if (wid == 0 && c < C) {
-        float ag = lg[0][lane], ab = lb[0][lane];
-#pragma unroll
-        for (int w = 1; w < 16; ++w) {
-            ag += lg[w][lane];
-            ab += lb[w][lane];
-        }
-        ggamma[c] = ag;
-        gbeta[c] = ab;
-    }
-}
-
 }  // namespace
 
 void nnk_gns_clear_workspace(float* ws, size_t n_floats, hipStream_t s) {
     if (n_floats == 0) return;
     const size_t blocks = (n_floats + 255) / 256 < 4096 ? (n_floats + 255) / 256 : 4096;
     gns_clear<<<dim3((unsigned)blocks), dim3(256), 0, s>>>(reinterpret_cast<unsigned*>(ws), n_floats);
-}
-
-void nnk_gns_param_reduce(float* ggamma, float* gbeta, const float* cpart, int P, int T, int NCB, int C,
-    hipStream_t s) {
-    gns_param_reduce_k<<<dim3((unsigned)((C + 63) / 64)), dim3(1024), 0, s>>>(ggamma, gbeta, cpart, P, T, NCB, C);
 }
 
 // Persistent grid size for a kernel: resident workgroups of the device

@@ -1,10 +1,8 @@
 // k_gns_bwd.hip -- instantiations and launch of the streaming GroupNorm
-// backward (gn_stream.h) and its dgamma/dbeta reduction.
+// backward (gn_stream.h); dgamma/dbeta are reduced inside the kernel.
 #include "gn_stream.h"
 
 int nnk_gns_grid(const void* fn, int key, size_t lds, int unit);
-void nnk_gns_param_reduce(float* ggamma, float* gbeta, const float* cpart, int P, int T, int NCB, int C,
-    hipStream_t s);
 
 namespace {
 
@@ -24,10 +22,10 @@ bool launch(const Plan& p, float* dx, float* ggamma, float* gbeta, const float* 
     Work wk;
     wk.err = reinterpret_cast<unsigned*>(ws);
     wk.rec = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(ws) + p.rec_offset);
-    wk.cpart = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + p.cpart_offset);
+    wk.cpart = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(ws) + p.cpart_offset);
     unsigned epoch = next_epoch();
     unsigned limit = kSpinLimit;
-    void* args[] = {&dx, const_cast<float**>(&dy), const_cast<float**>(&x), const_cast<float**>(&gamma),
+    void* args[] = {&dx, &ggamma, &gbeta, const_cast<float**>(&dy), const_cast<float**>(&x), const_cast<float**>(&gamma),
         const_cast<float**>(&beta), const_cast<float**>(&mu), const_cast<float**>(&rstd), &sh, &wk, &epoch,
         &limit};
     const hipError_t e = hipLaunchCooperativeKernel(fn, dim3((unsigned)P), dim3(kTpb), args, (unsigned)lds, s);
@@ -37,7 +35,6 @@ bool launch(const Plan& p, float* dx, float* ggamma, float* gbeta, const float* 
             hipGetErrorString(e));
         return false;
     }
-    nnk_gns_param_reduce(ggamma, gbeta, wk.cpart, P, sh.T, sh.NCB, sh.C, s);
     return true;
 }
 

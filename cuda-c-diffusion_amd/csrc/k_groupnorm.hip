@@ -237,8 +237,8 @@ bool shape_ok(const char* what, int B, int HW, int C, int G) {
 enum class GnPath { kAuto, kStream, kReg };
 
 // A lent workspace starts with a 256-byte header whose first word is the
-// streaming kernels' wait-timeout flag; only the streaming path writes it
-// (zeroes it, then flags), the others keep their data after the header.
+// streaming kernels' wait-timeout flag (set, never cleared, by them); the
+// other paths keep their data after the header.
 constexpr size_t kWsHeader = 64;
 constexpr long long kStreamMinElems = 1LL << 22;
 
@@ -257,10 +257,11 @@ bool want_stream(bool bwd, int B, int HW, int C, int G, bool reg_ok) {
 }
 
 // Streaming launch on the caller's workspace or on one drawn from the
-// stream-ordered pool.  The region is zeroed first: the kernels accept a
-// statistics record only when it carries the launch's (non-zero) epoch, and
-// clearing guarantees that nothing left in the memory by earlier calls (of
-// other shapes or paths) can carry it.
+// stream-ordered pool.  The kernels accept a statistics record only when it
+// carries the launch's epoch (unique in the process, never 0).  A lent
+// workspace is zero-filled by its owner before first use and written only by
+// these launchers, so it can hold only zeros and older epochs; a pool block
+// may hold anything and is zeroed first.
 template <class F>
 bool try_stream(bool bwd, int B, int HW, int C, int G, bool reg_ok, float* ws, hipStream_t s, const char* what,
     F launch) {
@@ -270,11 +271,19 @@ bool try_stream(bool bwd, int B, int HW, int C, int G, bool reg_ok, float* ws, h
     if (!w) {
         w = nnk_scratch_acquire(p.ws_floats, s, what);
         if (!w) return false;
+        nnk_gns_clear_workspace(w, p.ws_floats, s);
     }
-    nnk_gns_clear_workspace(w, p.ws_floats, s);
     const bool ok = launch(w);
     if (!ws) nnk_scratch_release(w, s);
     return ok;
+}
+
+// Offset (floats) of the register path's channel partials in a backward
+// workspace: past the header and, where the streaming plan applies, past its
+// records, so the two paths never write the same words.
+size_t reg_partials_offset(int B, int HW, int C, int G) {
+    const nnk::gns::Plan p = nnk::gns::make_plan(true, B, HW, C, G);
+    return p.ok ? p.ws_floats : kWsHeader;
 }
 
 void gn_forward_impl(const char* what, float* y, float* mu, float* rstd, const float* x,
@@ -336,11 +345,12 @@ void gn_backward_impl(const char* what, float* dx, float* ggamma, float* gbeta, 
         }
     }
     float* scratch = ws;
+    const size_t part_off = ws ? reg_partials_offset(B, HW, C, G) : 0;
     if (!scratch) {
-        scratch = nnk_scratch_acquire(kWsHeader + (size_t)2 * B * C, s, what);
+        scratch = nnk_scratch_acquire((size_t)2 * B * C, s, what);
         if (!scratch) return;
     }
-    float* part_g = scratch + kWsHeader;  // past the status word of a lent workspace
+    float* part_g = scratch + part_off;
     float* part_b = part_g + (size_t)B * C;
     const int cpg = C / G;
     int cfg = -1;
@@ -429,9 +439,7 @@ void launch_groupnorm_act_backward_ws(float* dx, float* ggamma, float* gbeta, co
 
 size_t nnhip_groupnorm_backward_workspace(int batch, int HW, int C, int G) {
     if (batch <= 0 || C <= 0) return 0;
-    const size_t reg = kWsHeader + (size_t)2 * batch * C;
-    const nnk::gns::Plan p = nnk::gns::make_plan(true, batch, HW, C, G);
-    return p.ok && p.ws_floats > reg ? p.ws_floats : reg;
+    return reg_partials_offset(batch, HW, C, G) + (size_t)2 * batch * C;
 }
 
 }  // extern "C"

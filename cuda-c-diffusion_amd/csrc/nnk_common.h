@@ -36,9 +36,9 @@ namespace nnk {
 //   exact (FAST = false): the reference's operation order, no contraction,
 //     correctly rounded division -- bit-identical to the CPU restatement;
 //     used by the standalone activation kernels, which are HBM-bound.
-//   fast (FAST = true): polynomials contracted to FMAs and the quotient as
-//     numerator times the hardware reciprocal (v_rcp_f32, 1 ulp); within a
-//     few ulp of the exact form.  Used inside the fused GroupNorm kernels,
+//   fast (FAST = true): multiply-adds as FMAs and the quotient as numerator
+//     times the hardware reciprocal (v_rcp_f32, 1 ulp); within a few ulp of
+//     the exact form.  Used inside the fused GroupNorm kernels,
 //     where the activation is most of the VALU work.  Near |tanh| = 1 the
 //     terms 1 - t*t and 1 +- t cancel, so there the difference is relative to
 //     the upstream gradient / input scale, not to the (tiny) result.
@@ -51,10 +51,20 @@ __device__ __forceinline__ float pade_tanh_exact(float x) {
 }
 
 __device__ __forceinline__ float pade_tanh_fast(float x) {
-#pragma clang fp contract(fast)
     const float x2 = x * x;
-    const float p = x * (135135.0f + x2 * (17325.0f + x2 * (378.0f + x2)));
-    const float q = 135135.0f + x2 * (62370.0f + x2 * (3150.0f + x2 * 28.0f));
+    const float p = x * fmaf(x2, fmaf(x2, x2 + 378.0f, 17325.0f), 135135.0f);
+    const float q = fmaf(x2, fmaf(x2, fmaf(x2, 28.0f, 3150.0f), 62370.0f), 135135.0f);
+    return fmaxf(-1.0f, fminf(1.0f, p * __builtin_amdgcn_rcpf(q)));
+}
+
+// tanh(z / 2), fast form: with w = z^2 = 4 (z/2)^2 the half-argument scaling
+// is folded into the coefficients.  Every coefficient and every intermediate
+// differs from the (z/2)-form by a power of two, so the values are identical
+// to pade_tanh_fast(z * 0.5f); one multiply fewer.
+__device__ __forceinline__ float pade_tanh_half_fast(float z) {
+    const float w = z * z;
+    const float p = z * fmaf(w, fmaf(w, fmaf(w, 0.0078125f, 11.8125f), 2165.625f), 67567.5f);
+    const float q = fmaf(w, fmaf(w, fmaf(w, 0.4375f, 196.875f), 15592.5f), 135135.0f);
     return fmaxf(-1.0f, fminf(1.0f, p * __builtin_amdgcn_rcpf(q)));
 }
 
@@ -69,15 +79,60 @@ __device__ __forceinline__ float pade_sigmoid(float x) {
     // pade_tanh is clamped to [-1, 1], so (t + 1) * 0.5 already lies in [0, 1]:
     // the reference's outer clamp (kernels.cu:16) never changes the value and
     // is not evaluated.
-    return (pade_tanh<FAST>(x * 0.5f) + 1.0f) * 0.5f;
+    if constexpr (FAST) return fmaf(pade_tanh_half_fast(x), 0.5f, 0.5f);
+    else return (pade_tanh_exact(x * 0.5f) + 1.0f) * 0.5f;
 }
 
 constexpr float kGeluC = 0.7978845608f;
 constexpr float kGeluA = 0.044715f;
 constexpr float kMpSiluScale = 1.0f / 0.596f;
 
+// Fast forms of the activation and its derivative: the reference formulas
+// with the multiply-adds written as FMAs.
+template <int ACT>
+__device__ __forceinline__ float act_fwd_fast(float v) {
+    if constexpr (ACT == ACT_RELU) {
+        return v > 0.0f ? v : 0.0f;
+    } else if constexpr (ACT == ACT_GELU) {
+        const float t = pade_tanh_fast(kGeluC * fmaf(kGeluA * v, v * v, v));
+        const float hv = 0.5f * v;
+        return fmaf(hv, t, hv);
+    } else if constexpr (ACT == ACT_SILU) {
+        return v * pade_sigmoid<true>(v);
+    } else if constexpr (ACT == ACT_MP_SILU) {
+        return v * pade_sigmoid<true>(v) * kMpSiluScale;
+    } else if constexpr (ACT == ACT_TANH) {
+        return pade_tanh_fast(v);
+    } else {
+        return v;
+    }
+}
+
+template <int ACT>
+__device__ __forceinline__ float act_grad_fast(float z) {
+    if constexpr (ACT == ACT_RELU) {
+        return z > 0.0f ? 1.0f : 0.0f;
+    } else if constexpr (ACT == ACT_TANH) {
+        const float t = pade_tanh_fast(z);
+        return fmaf(-t, t, 1.0f);
+    } else if constexpr (ACT == ACT_SILU) {
+        const float s = pade_sigmoid<true>(z);
+        return s * fmaf(z, 1.0f - s, 1.0f);
+    } else if constexpr (ACT == ACT_MP_SILU) {
+        const float s = pade_sigmoid<true>(z);
+        return s * fmaf(z, 1.0f - s, 1.0f) * kMpSiluScale;
+    } else if constexpr (ACT == ACT_GELU) {
+        const float t = pade_tanh_fast(kGeluC * fmaf(kGeluA * z, z * z, z));
+        const float du = kGeluC * fmaf(3.0f * kGeluA * z, z, 1.0f);
+        return fmaf(0.5f, 1.0f + t, 0.5f * z * fmaf(-t, t, 1.0f) * du);
+    } else {
+        return 1.0f;
+    }
+}
+
 template <int ACT, bool FAST = true>
 __device__ __forceinline__ float act_fwd(float v) {
+    if constexpr (FAST) return act_fwd_fast<ACT>(v);
     if constexpr (ACT == ACT_RELU) {
         return v > 0.0f ? v : 0.0f;
     } else if constexpr (ACT == ACT_GELU) {
@@ -95,6 +150,7 @@ __device__ __forceinline__ float act_fwd(float v) {
 
 template <int ACT, bool FAST = true>
 __device__ __forceinline__ float act_grad(float z) {
+    if constexpr (FAST) return act_grad_fast<ACT>(z);
     if constexpr (ACT == ACT_RELU) {
         return z > 0.0f ? 1.0f : 0.0f;
     } else if constexpr (ACT == ACT_TANH) {

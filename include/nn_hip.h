@@ -205,9 +205,10 @@ size_t nnhip_groupnorm_backward_workspace(int batch, int HW, int C, int G);
 size_t nnhip_layernorm_backward_workspace(int batch, int C);
 
 /* Workspace variants: identical results; the caller lends `workspace` (at least
-   the size reported above, 16-byte aligned) instead of the launcher drawing it
-   from the stream-ordered pool.  Launches that may run concurrently need
-   separate workspaces.  Used by the host modules and the benchmark. */
+   the size reported above, 16-byte aligned, zero-filled before first use)
+   instead of the launcher drawing it from the stream-ordered pool.  Launches
+   that may run concurrently need separate workspaces.  Used by the host
+   modules and the benchmark. */
 void launch_groupnorm_act_forward_ws(float* y, float* mu, float* rstd,
     const float* x, const float* gamma, const float* beta,
     int batch, int HW, int C, int G, float eps, Activation act,
@@ -224,12 +225,14 @@ void launch_layernorm_backward_ws(float* grad_in, float* ggamma, float* gbeta,
 
 /* Large GroupNorm launches use persistent workgroups that exchange per-tile
    statistics through the workspace and wait for each other with bounded
-   polls.  The first word of a lent workspace is their timeout flag: each such
-   launch zeroes it and sets it when a wait exceeds its bound (the launch's
-   outputs are then not valid); other GroupNorm paths leave it alone.  Returns
-   that word as 1/0 -- the outcome of the last streaming launch on `workspace`,
-   or 0 if none ran on it since it was zero-filled -- or < 0 on a HIP error.
-   Synchronous (reads one word of device memory). */
+   polls.  A workspace lent to the GroupNorm launchers must be zero-filled
+   before its first use and must not be written by anything else afterwards
+   (records of a launch are told apart from earlier ones by a per-launch tag).
+   Its first word is the timeout flag: a launch sets it when a wait exceeds its
+   bound (that launch's outputs are then not valid), and no launch clears it.
+   Returns that word as 1/0 (0: no streaming launch on `workspace` has timed
+   out since it was zero-filled), or < 0 on a HIP error.  Synchronous (reads
+   one word of device memory). */
 int nnhip_groupnorm_workspace_status(const float* workspace);
 
 /* grad_im = col2im(grad_col) written, not accumulated: the same fixed order as

@@ -61,6 +61,11 @@ def records_tagged(ws, nrec):
     return hi.size == nrec and hi[0] != 0 and bool(np.all(hi == hi[0]))
 
 
+def zeroed(L, n):
+    """A workspace to lend: zero-filled before its first use."""
+    return L.to_device(np.zeros(n, np.float32))
+
+
 def run_fwd(L, x, gamma, beta, G, act, ws=None):
     B, HW, C = x.shape
     xd, yd = L.to_device(x), L.alloc(x.size)
@@ -94,8 +99,8 @@ def check_case(L, orc, rng, shape, act):
     B, H, W, C, G = shape
     HW = H * W
     x, gamma, beta, dy = make_inputs(rng, B, H, W, C)
-    fws = L.alloc(max(1, L.nnhip_groupnorm_forward_workspace(B, HW, C, G)))
-    bws = L.alloc(L.nnhip_groupnorm_backward_workspace(B, HW, C, G))
+    fws = zeroed(L, max(1, L.nnhip_groupnorm_forward_workspace(B, HW, C, G)))
+    bws = zeroed(L, L.nnhip_groupnorm_backward_workspace(B, HW, C, G))
 
     y_ref, mu_ref, rs_ref = orc.groupnorm_forward(x, gamma, beta, G, 1e-5, act)
     y, mu, rs = run_fwd(L, x, gamma, beta, G, act, fws)
@@ -173,7 +178,7 @@ def test_stream_groupnorm_workspace_reuse_across_shapes(L, orc, rng, monkeypatch
     shapes = [(2, 64, 64, 256, 32), (2, 32, 32, 128, 32), (1, 64, 64, 256, 32)]
     need = max(max(L.nnhip_groupnorm_forward_workspace(B, H * W, C, G),
                    L.nnhip_groupnorm_backward_workspace(B, H * W, C, G)) for B, H, W, C, G in shapes)
-    ws = L.alloc(need)
+    ws = zeroed(L, need)
     for B, H, W, C, G in shapes:
         x, gamma, beta, dy = make_inputs(rng, B, H, W, C)
         y_ref, mu_ref, rs_ref = orc.groupnorm_forward(x, gamma, beta, G, 1e-5, 3)
@@ -200,12 +205,13 @@ def test_reg_path_switch_matches_stream(L, rng, monkeypatch):
 
 def test_workspace_status_untouched_by_register_path(L, orc, rng, monkeypatch):
     """A zero-filled lent workspace keeps status 0 through register-path
-    launches: their channel partials live after the 256-byte header."""
+    launches: their channel partials live past the header and the streaming
+    records."""
     print("[case] workspace status after register path", flush=True)
     monkeypatch.setenv("NNHIP_GN_PATH", "reg")
     B, H, W, C, G = 2, 32, 32, 128, 32
     x, gamma, beta, dy = make_inputs(rng, B, H, W, C)
-    ws = L.to_device(np.zeros(L.nnhip_groupnorm_backward_workspace(B, H * W, C, G), np.float32))
+    ws = zeroed(L, L.nnhip_groupnorm_backward_workspace(B, H * W, C, G))
     _, mu_ref, rs_ref = orc.groupnorm_forward(x, gamma, beta, G, 1e-5, 3)
     dx_ref, gg_ref, _ = orc.groupnorm_backward(dy, x, gamma, beta, mu_ref, rs_ref, G, 3)
     dx, gg, _ = run_bwd(L, dy, x, gamma, beta, mu_ref, rs_ref, G, 3, ws)
