@@ -8,7 +8,9 @@
 //   forward : read x, write y           =  8 B/elem
 //   backward: read x, dy, write dx      = 12 B/elem
 //             + per-workgroup channel partials (2*C floats per 64 rows),
-//               summed over workgroups in a fixed order by ln_colsum2.
+//               summed in a fixed order in two levels: ln_colsum_seg sums
+//               segments of 64 partial rows on many workgroups, ln_colsum2
+//               adds the segment sums.
 // Generic path: one 256-thread block per row plus a coalesced partial kernel.
 #include "nnk_common.h"
 
@@ -283,6 +285,44 @@ __global__ __launch_bounds__(kTpb) void ln_param_partial_generic(float* __restri
     }
 }
 
+// First level of the dgamma/dbeta column sum: workgroup (x, s) sums partial
+// rows p in [64 s, 64 s + 64) of channels 64 x + lane; wave w takes
+// p = 64 s + w, + 4, ... (all 16 loads in flight), then the 4 wave sums are
+// added in wave order.  out[s*C + c].
+constexpr int kSeg = 64;
+__global__ __launch_bounds__(kTpb) void ln_colsum_seg(float* __restrict__ og, float* __restrict__ ob,
+    const float* __restrict__ pg, const float* __restrict__ pb, int P, int C) {
+    __shared__ float lg[kNw][kWave];
+    __shared__ float lb[kNw][kWave];
+    constexpr int kPer = kSeg / kNw;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wid = threadIdx.x / kWave;
+    const int c = blockIdx.x * kWave + lane;
+    const int p0 = blockIdx.y * kSeg, p1 = min(P, p0 + kSeg);
+    float sg = 0.0f, sb = 0.0f;
+    if (c < C) {
+        float vg[kPer], vb[kPer];
+#pragma unroll
+        for (int u = 0; u < kPer; ++u) {
+            const int p = p0 + wid + u * kNw;
+            vg[u] = p < p1 ? pg[(size_t)p * C + c] : 0.0f;
+            vb[u] = p < p1 ? pb[(size_t)p * C + c] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < kPer; ++u) {
+            sg += vg[u];
+            sb += vb[u];
+        }
+    }
+    lg[wid][lane] = sg;
+    lb[wid][lane] = sb;
+    __syncthreads();
+    if (wid == 0 && c < C) {
+        og[(size_t)blockIdx.y * C + c] = ((lg[0][lane] + lg[1][lane]) + lg[2][lane]) + lg[3][lane];
+        ob[(size_t)blockIdx.y * C + c] = ((lb[0][lane] + lb[1][lane]) + lb[2][lane]) + lb[3][lane];
+    }
+}
+
 // out[c] = sum_p part[p*C + c] over P partial rows; wave w takes p = w, w+4, ...
 __global__ __launch_bounds__(kTpb) void ln_colsum2(float* __restrict__ og, float* __restrict__ ob,
     const float* __restrict__ pg, const float* __restrict__ pb, int P, int C) {
@@ -324,6 +364,8 @@ int fast_nv(int C, const void* a, const void* b, const void* c, const void* d) {
 }
 
 int num_chunks(int rows) { return (rows + kRowsPerWg - 1) / kRowsPerWg; }
+int num_segments(int P) { return (P + kSeg - 1) / kSeg; }
+size_t pad4(size_t n) { return (n + 3) / 4 * 4; }
 
 void ln_backward_impl(const char* what, float* dx, float* ggamma, float* gbeta, const float* dy,
     const float* x, const float* gamma, const float* mu, const float* rstd, int rows, int C,
@@ -338,13 +380,17 @@ void ln_backward_impl(const char* what, float* dx, float* ggamma, float* gbeta, 
     NNK_REQUIRE(dx && dy && x && gamma && mu && rstd, what, "%s: null pointer", what);
     NNK_REQUIRE(ws == nullptr || aligned16(ws), what, "%s: workspace must be 16-byte aligned", what);
     const int P = num_chunks(rows);
+    const int S = num_segments(P);
+    const size_t pc = pad4((size_t)P * C), sc = pad4((size_t)S * C);
     float* scratch = ws;
     if (!scratch) {
-        scratch = nnk_scratch_acquire((size_t)2 * P * C, s, what);
+        scratch = nnk_scratch_acquire(2 * pc + 2 * sc, s, what);
         if (!scratch) return;
     }
     float* part_g = scratch;
-    float* part_b = scratch + (size_t)P * C;
+    float* part_b = scratch + pc;
+    float* seg_g = scratch + 2 * pc;
+    float* seg_b = seg_g + sc;
     const int nv = fast_nv(C, dx, dy, x, gamma);
     if (nv && (C % 4 == 0) && aligned16(part_b)) {
         switch (nv) {
@@ -357,7 +403,9 @@ void ln_backward_impl(const char* what, float* dx, float* ggamma, float* gbeta, 
         ln_param_partial_generic<<<dim3((unsigned)((C + kWave - 1) / kWave), (unsigned)P), kTpb, 0, s>>>(
             part_g, part_b, dy, x, mu, rstd, rows, C);
     }
-    ln_colsum2<<<dim3((unsigned)((C + kWave - 1) / kWave)), kTpb, 0, s>>>(ggamma, gbeta, part_g, part_b, P, C);
+    const unsigned cblocks = (unsigned)((C + kWave - 1) / kWave);
+    ln_colsum_seg<<<dim3(cblocks, (unsigned)S), kTpb, 0, s>>>(seg_g, seg_b, part_g, part_b, P, C);
+    ln_colsum2<<<dim3(cblocks), kTpb, 0, s>>>(ggamma, gbeta, seg_g, seg_b, S, C);
     if (!ws) nnk_scratch_release(scratch, s);
     nnk_after_launch(what, s);
 }
@@ -408,9 +456,9 @@ void launch_layernorm_backward_ws(float* grad_in, float* ggamma, float* gbeta,
 
 size_t nnhip_layernorm_backward_workspace(int batch, int C) {
     if (batch <= 0 || C <= 0) return 0;
-    // 2*P*C floats; P*C is padded to a float4 multiple so part_b stays aligned
-    const size_t pc = (size_t)num_chunks(batch) * C;
-    return 2 * ((pc + 3) / 4 * 4);
+    // partials (2 P C) and segment sums (2 S C), each padded to a float4 multiple
+    const int P = num_chunks(batch);
+    return 2 * pad4((size_t)P * C) + 2 * pad4((size_t)num_segments(P) * C);
 }
 
 }  // extern "C"
