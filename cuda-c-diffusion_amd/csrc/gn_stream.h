@@ -61,9 +61,12 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t sample_rsrc(const float* base,
 }
 
 // Direct-to-LDS 128-bit buffer load: lane i of the wave reads 16 bytes at
-// voff + soff and writes them to wave_slots + i (wave_slots uniform over the wave).
+// voff + soff and writes them to wave_slots + i (wave_slots uniform over the
+// wave).  NT sets cache policy nt (bit 1) for inputs streamed once.
+constexpr int kCpolNt = 2;
+template <bool NT>
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, float4* wave_slots, uint32_t voff, uint32_t soff) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)wave_slots, 16, (int)voff, (int)soff, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)wave_slots, 16, (int)voff, (int)soff, 0, NT ? kCpolNt : 0);
 }
 
 // Workgroup barrier for LDS traffic: waits for this wave's LDS operations but
@@ -190,7 +193,7 @@ __device__ __forceinline__ void for_group_xor(F f) {
 // ---------------------------------------------------------------------------
 // Forward.
 // ---------------------------------------------------------------------------
-template <class Gm, int ACT, int RPL>
+template <class Gm, int ACT, int RPL, bool NT>
 __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float* __restrict__ mu_out,
     float* __restrict__ rstd_out, const float* __restrict__ x, const float* __restrict__ gamma,
     const float* __restrict__ beta, Shape sh, Work wk, float eps, unsigned epoch, unsigned spin_limit) {
@@ -234,7 +237,7 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
         const uint32_t base = (uint32_t)(t * Gm::TP) * row_bytes;
 #pragma unroll
         for (int k = 0; k < NV; ++k)
-            dma16(r, stage + k * TPB + wid * kWave, voff, base + (uint32_t)(k * Gm::RSTEP) * row_bytes);
+            dma16<NT>(r, stage + k * TPB + wid * kWave, voff, base + (uint32_t)(k * Gm::RSTEP) * row_bytes);
     };
     auto phase_a = [&](const float4 (&v)[NV], int tile, int pb) {
         float s = 0.0f;
@@ -342,7 +345,7 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
             o.y = act_fwd<ACT>(fmaf(v.y, sc.y, s0.y));
             o.z = act_fwd<ACT>(fmaf(v.z, sc.z, s0.z));
             o.w = act_fwd<ACT>(fmaf(v.w, sc.w, s0.w));
-            st4(ys + (size_t)(k * Gm::RSTEP) * sh.C, o);
+            stS<NT>(ys + (size_t)(k * Gm::RSTEP) * sh.C, o);
         }
     };
 
@@ -404,7 +407,7 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
 // Backward.  dy is the gradient of act(GN(x)); the pre-activation is
 // recomputed from x, mu, rstd, gamma, beta.  Parks xhat and g = d*gamma.
 // ---------------------------------------------------------------------------
-template <class Gm, int ACT, int RPL>
+template <class Gm, int ACT, int RPL, bool NT>
 __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float* __restrict__ ggamma,
     float* __restrict__ gbeta, const float* __restrict__ dy,
     const float* __restrict__ x, const float* __restrict__ gamma, const float* __restrict__ beta,
@@ -450,10 +453,10 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
         const uint32_t base = (uint32_t)(t * Gm::TP) * row_bytes;
 #pragma unroll
         for (int k = 0; k < NV; ++k)
-            dma16(rx, stage + k * TPB + wid * kWave, voff, base + (uint32_t)(k * Gm::RSTEP) * row_bytes);
+            dma16<NT>(rx, stage + k * TPB + wid * kWave, voff, base + (uint32_t)(k * Gm::RSTEP) * row_bytes);
 #pragma unroll
         for (int k = 0; k < NV; ++k)
-            dma16(rd, stage + (NV + k) * TPB + wid * kWave, voff, base + (uint32_t)(k * Gm::RSTEP) * row_bytes);
+            dma16<NT>(rd, stage + (NV + k) * TPB + wid * kWave, voff, base + (uint32_t)(k * Gm::RSTEP) * row_bytes);
     };
     // phase A: xv -> xhat, gv -> g in place; per-group S1 = sum g, S2 = sum g*xhat -> records
     auto phase_a = [&](float4 (&xv)[NV], float4 (&gv)[NV], int tile, float mean, float rs, int pb) {
@@ -572,7 +575,7 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
             o.y = fmaf(g.y, rs, fmaf(xh.y, a2, a1));
             o.z = fmaf(g.z, rs, fmaf(xh.z, a2, a1));
             o.w = fmaf(g.w, rs, fmaf(xh.w, a2, a1));
-            st4(dxs + (size_t)(k * Gm::RSTEP) * sh.C, o);
+            stS<NT>(dxs + (size_t)(k * Gm::RSTEP) * sh.C, o);
         }
     };
 

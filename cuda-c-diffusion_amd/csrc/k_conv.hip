@@ -11,6 +11,9 @@
 //   is kh descending then kw descending, as plain fp32 adds starting from the
 //   value already in grad_im (launch_col2im) or from +0.0f (launch_col2im_set).
 //   Every col element is read once; no memset and no atomics.
+// In large launches (use_nt) col and grad_im stream with nontemporal stores
+// and loads; the image side of im2col, read up to K*K times, always uses
+// ordinary loads.
 #include "nnk_common.h"
 
 namespace {
@@ -26,7 +29,7 @@ struct ConvGeom {
 };
 
 // VW = 4 (float4, C % 4 == 0) or 1.  Unit index u walks col in memory order.
-template <int VW>
+template <int VW, bool NT>
 __global__ __launch_bounds__(kTpb) void im2col_kernel(float* __restrict__ col,
     const float* __restrict__ im, ConvGeom g, long long units, FastDiv div_row,
     FastDiv div_cv, FastDiv div_k, FastDiv div_wo, FastDiv div_ho) {
@@ -48,7 +51,7 @@ __global__ __launch_bounds__(kTpb) void im2col_kernel(float* __restrict__ col,
         const size_t src = (((size_t)b * g.H + (in ? ih : 0)) * g.W + (in ? iw : 0)) * g.C + (size_t)cv * VW;
         if constexpr (VW == 4) {
             const float4 v = in ? ld4(im + src) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            st4(col + 4 * q, v);
+            stS<NT>(col + 4 * q, v);
         } else {
             col[q] = in ? im[src] : 0.0f;
             (void)CV;
@@ -56,7 +59,63 @@ __global__ __launch_bounds__(kTpb) void im2col_kernel(float* __restrict__ col,
     }
 }
 
-template <int VW, bool UNIT_STRIDE, bool ACCUM>
+// Fast im2col (C % 4 == 0 and CV = C/4 dividing the workgroup size, CV >= 4).
+// A workgroup writes RT = SPI whole col rows (SPI = kTpb / CV kernel-window
+// segments per pass), so every thread keeps one float4 column cv and walks
+// the segments s = tid / CV, + SPI, ... of the tile: exactly K*K passes, each
+// pass storing kTpb consecutive float4 of col.  The per-row image origin
+// (b, oh*stride - pad, ow*stride - pad) comes from an LDS table.  Bit-exact.
+constexpr int kMaxRowsPerTile = 64;
+// NB = passes whose loads are in flight together: K*K for the common 3x3
+// kernel (all nine), kUnroll otherwise.
+template <int NB, bool NT>
+__global__ __launch_bounds__(kTpb) void im2col_rows_kernel(float* __restrict__ col,
+    const float* __restrict__ im, ConvGeom g, int rows, int CV, FastDiv div_k, FastDiv div_kk,
+    FastDiv div_wo, FastDiv div_ho) {
+    __shared__ int4 origin[kMaxRowsPerTile];  // (ih0, iw0, b * H, row valid)
+    const int SPI = kTpb / CV;
+    const int KK = g.K * g.K;
+    const int row0 = blockIdx.x * SPI;
+    if ((int)threadIdx.x < SPI) {
+        const int row = row0 + (int)threadIdx.x;
+        int4 o = make_int4(0, 0, 0, 0);
+        if (row < rows) {
+            uint32_t pix, ow, b, oh;
+            div_wo.divmod((uint32_t)row, pix, ow);
+            div_ho.divmod(pix, b, oh);
+            o = make_int4((int)oh * g.stride - g.pad, (int)ow * g.stride - g.pad, (int)b * g.H, 1);
+        }
+        origin[threadIdx.x] = o;
+    }
+    __syncthreads();
+    const int cv = (int)threadIdx.x % CV;
+    uint32_t r, seg;  // segment index s = tid / CV + pass * SPI = r * KK + seg
+    div_kk.divmod((uint32_t)threadIdx.x / (uint32_t)CV, r, seg);
+    float* out = col + ((size_t)row0 * KK) * g.C + (size_t)threadIdx.x * 4;
+    // passes in batches of NB: all loads of a batch are in flight together
+    for (int p0 = 0; p0 < KK; p0 += NB) {
+        float4 v[NB];
+        bool st[NB];
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+            const int4 o = origin[r];
+            st[u] = p0 + u < KK && o.w;
+            uint32_t kh, kw;
+            div_k.divmod(seg, kh, kw);
+            const int ih = o.x + (int)kh, iw = o.y + (int)kw;
+            const bool in = st[u] && ih >= 0 && ih < g.H && iw >= 0 && iw < g.W;
+            v[u] = in ? ld4(im + ((size_t)(o.z + ih) * g.W + iw) * g.C + cv * 4) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            uint32_t q;
+            div_kk.divmod(seg + (uint32_t)SPI, q, seg);
+            r = r + q < (uint32_t)SPI ? r + q : (uint32_t)SPI - 1;  // stays inside the origin table
+        }
+#pragma unroll
+        for (int u = 0; u < NB; ++u)
+            if (st[u]) stS<NT>(out + (size_t)(p0 + u) * kTpb * 4, v[u]);
+    }
+}
+
+template <int VW, bool UNIT_STRIDE, bool ACCUM, bool NT>
 __global__ __launch_bounds__(kTpb) void col2im_kernel(float* __restrict__ grad_im,
     const float* __restrict__ grad_col, ConvGeom g, long long units, FastDiv div_cv,
     FastDiv div_w, FastDiv div_h) {
@@ -73,7 +132,7 @@ __global__ __launch_bounds__(kTpb) void col2im_kernel(float* __restrict__ grad_i
         const int ci = (int)cv * VW;
         float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         if constexpr (ACCUM) {
-            if constexpr (VW == 4) acc = ld4(grad_im + 4 * q);
+            if constexpr (VW == 4) acc = ldS<NT>(grad_im + 4 * q);
             else acc.x = grad_im[q];
         }
         for (int kh = g.K - 1; kh >= 0; --kh) {
@@ -96,7 +155,7 @@ __global__ __launch_bounds__(kTpb) void col2im_kernel(float* __restrict__ grad_i
                 if (ow >= g.Wo) continue;
                 const size_t src = (((size_t)b * g.Ho + oh) * g.Wo + ow) * KKC + (size_t)(kh * g.K + kw) * g.C + ci;
                 if constexpr (VW == 4) {
-                    const float4 v = ld4(grad_col + src);
+                    const float4 v = ldS<NT>(grad_col + src);
                     acc.x = acc.x + v.x;
                     acc.y = acc.y + v.y;
                     acc.z = acc.z + v.z;
@@ -106,7 +165,7 @@ __global__ __launch_bounds__(kTpb) void col2im_kernel(float* __restrict__ grad_i
                 }
             }
         }
-        if constexpr (VW == 4) st4(grad_im + 4 * q, acc);
+        if constexpr (VW == 4) stS<NT>(grad_im + 4 * q, acc);
         else grad_im[q] = acc.x;
     }
 }
@@ -146,12 +205,15 @@ void col2im_impl(const char* what, float* grad_im, const float* grad_col, int ba
     const long long units = (long long)batch * H * W * (C / VWr);
     const FastDiv dcv((uint32_t)(C / VWr)), dw((uint32_t)W), dh((uint32_t)H);
     const unsigned blocks = blocks_for(units);
+    const bool nt = use_nt(4LL * ((long long)batch * Ho * Wo * K * K * C + (long long)batch * H * W * C));
     if (vec) {
-        if (stride == 1) col2im_kernel<4, true, ACCUM><<<blocks, kTpb, 0, s>>>(grad_im, grad_col, g, units, dcv, dw, dh);
-        else col2im_kernel<4, false, ACCUM><<<blocks, kTpb, 0, s>>>(grad_im, grad_col, g, units, dcv, dw, dh);
+        if (stride == 1 && nt) col2im_kernel<4, true, ACCUM, true><<<blocks, kTpb, 0, s>>>(grad_im, grad_col, g, units, dcv, dw, dh);
+        else if (stride == 1) col2im_kernel<4, true, ACCUM, false><<<blocks, kTpb, 0, s>>>(grad_im, grad_col, g, units, dcv, dw, dh);
+        else if (nt) col2im_kernel<4, false, ACCUM, true><<<blocks, kTpb, 0, s>>>(grad_im, grad_col, g, units, dcv, dw, dh);
+        else col2im_kernel<4, false, ACCUM, false><<<blocks, kTpb, 0, s>>>(grad_im, grad_col, g, units, dcv, dw, dh);
     } else {
-        if (stride == 1) col2im_kernel<1, true, ACCUM><<<blocks, kTpb, 0, s>>>(grad_im, grad_col, g, units, dcv, dw, dh);
-        else col2im_kernel<1, false, ACCUM><<<blocks, kTpb, 0, s>>>(grad_im, grad_col, g, units, dcv, dw, dh);
+        if (stride == 1) col2im_kernel<1, true, ACCUM, false><<<blocks, kTpb, 0, s>>>(grad_im, grad_col, g, units, dcv, dw, dh);
+        else col2im_kernel<1, false, ACCUM, false><<<blocks, kTpb, 0, s>>>(grad_im, grad_col, g, units, dcv, dw, dh);
     }
     nnk_after_launch(what, s);
 }
@@ -173,8 +235,22 @@ void launch_im2col(float* col, const float* im, int batch, int H, int W, int C, 
     const long long units = (long long)batch * H_out * W_out * K * K * CV;
     const FastDiv drow((uint32_t)(K * K * CV)), dcv((uint32_t)CV), dk((uint32_t)K),
         dwo((uint32_t)W_out), dho((uint32_t)H_out);
-    if (vec) im2col_kernel<4><<<blocks_for(units), kTpb, 0, s>>>(col, im, g, units, drow, dcv, dk, dwo, dho);
-    else im2col_kernel<1><<<blocks_for(units), kTpb, 0, s>>>(col, im, g, units, drow, dcv, dk, dwo, dho);
+    const bool nt = use_nt(4LL * (units * VWr + (long long)batch * H * W * C));
+    if (vec && CV >= kTpb / kMaxRowsPerTile && kTpb % CV == 0) {
+        const long long rows = (long long)batch * H_out * W_out;
+        const int rows_per_tile = kTpb / CV;
+        const unsigned tiles = (unsigned)((rows + rows_per_tile - 1) / rows_per_tile);
+        const FastDiv dkk((uint32_t)(K * K));
+        if (K == 3 && nt) im2col_rows_kernel<9, true><<<tiles, kTpb, 0, s>>>(col, im, g, (int)rows, CV, dk, dkk, dwo, dho);
+        else if (K == 3) im2col_rows_kernel<9, false><<<tiles, kTpb, 0, s>>>(col, im, g, (int)rows, CV, dk, dkk, dwo, dho);
+        else if (nt) im2col_rows_kernel<kUnroll, true><<<tiles, kTpb, 0, s>>>(col, im, g, (int)rows, CV, dk, dkk, dwo, dho);
+        else im2col_rows_kernel<kUnroll, false><<<tiles, kTpb, 0, s>>>(col, im, g, (int)rows, CV, dk, dkk, dwo, dho);
+    } else if (vec) {
+        if (nt) im2col_kernel<4, true><<<blocks_for(units), kTpb, 0, s>>>(col, im, g, units, drow, dcv, dk, dwo, dho);
+        else im2col_kernel<4, false><<<blocks_for(units), kTpb, 0, s>>>(col, im, g, units, drow, dcv, dk, dwo, dho);
+    } else {
+        im2col_kernel<1, false><<<blocks_for(units), kTpb, 0, s>>>(col, im, g, units, drow, dcv, dk, dwo, dho);
+    }
     nnk_after_launch(what, s);
 }
 

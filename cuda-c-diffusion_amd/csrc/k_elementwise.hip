@@ -4,6 +4,9 @@
 //
 // Streaming shape: 256 threads, each thread moves 4 float4 spaced 256 apart,
 // so a wave touches 1 KB contiguous per access; a scalar tail covers n % 4.
+// Launches touching at least kNtBytes stream their tensors with nontemporal
+// loads and stores (NT = true; see use_nt); per-channel vectors that are
+// re-read (bias) always use ordinary loads.
 // When any pointer is not 16-byte aligned the same kernels run in a scalar
 // shape (one float per slot).  All bandwidth-bound: bytes per element are
 // stated per kernel.
@@ -37,18 +40,18 @@ __device__ __forceinline__ void stream_loop(long long n4, long long n, Vec op, T
 // ---------------- activations: fwd 8 B/elem, bwd 12 B/elem ----------------
 // Exact Pade form (correctly rounded quotient, no contraction): these kernels
 // are HBM-bound, so the exact arithmetic costs nothing measurable.
-template <int ACT, bool VEC>
+template <int ACT, bool VEC, bool NT>
 __global__ __launch_bounds__(kTpb) void act_fwd_kernel(float* __restrict__ out,
     const float* __restrict__ in, long long n) {
     if constexpr (VEC) {
         stream_loop(n / 4, n,
             [&](long long q) {
-                float4 v = ld4(in + 4 * q);
+                float4 v = ldS<NT>(in + 4 * q);
                 v.x = act_fwd<ACT, false>(v.x);
                 v.y = act_fwd<ACT, false>(v.y);
                 v.z = act_fwd<ACT, false>(v.z);
                 v.w = act_fwd<ACT, false>(v.w);
-                st4(out + 4 * q, v);
+                stS<NT>(out + 4 * q, v);
             },
             [&](long long i) { out[i] = act_fwd<ACT, false>(in[i]); });
     } else {
@@ -61,19 +64,19 @@ __global__ __launch_bounds__(kTpb) void act_fwd_kernel(float* __restrict__ out,
     }
 }
 
-template <int ACT, bool VEC>
+template <int ACT, bool VEC, bool NT>
 __global__ __launch_bounds__(kTpb) void act_bwd_kernel(float* __restrict__ gin,
     const float* __restrict__ gout, const float* __restrict__ in, long long n) {
     if constexpr (VEC) {
         stream_loop(n / 4, n,
             [&](long long q) {
-                const float4 z = ld4(in + 4 * q);
-                float4 g = ld4(gout + 4 * q);
+                const float4 z = ldS<NT>(in + 4 * q);
+                float4 g = ldS<NT>(gout + 4 * q);
                 g.x = g.x * act_grad<ACT, false>(z.x);
                 g.y = g.y * act_grad<ACT, false>(z.y);
                 g.z = g.z * act_grad<ACT, false>(z.z);
                 g.w = g.w * act_grad<ACT, false>(z.w);
-                st4(gin + 4 * q, g);
+                stS<NT>(gin + 4 * q, g);
             },
             [&](long long i) { gin[i] = gout[i] * act_grad<ACT, false>(in[i]); });
     } else {
@@ -87,21 +90,21 @@ __global__ __launch_bounds__(kTpb) void act_bwd_kernel(float* __restrict__ gin,
 }
 
 // ---------------- out = wa*a + wb*b: 12 B/elem ----------------
-template <bool VEC>
+template <bool VEC, bool NT>
 __global__ __launch_bounds__(kTpb) void weighted_sum_kernel(float* out, const float* a,
     const float* b, float wa, float wb, long long n) {
     // out may alias a or b (EMA updates shadow in place): no __restrict__.
     if constexpr (VEC) {
         stream_loop(n / 4, n,
             [&](long long q) {
-                const float4 x = ld4(a + 4 * q);
-                const float4 y = ld4(b + 4 * q);
+                const float4 x = ldS<NT>(a + 4 * q);
+                const float4 y = ldS<NT>(b + 4 * q);
                 float4 o;
                 o.x = wa * x.x + wb * y.x;
                 o.y = wa * x.y + wb * y.y;
                 o.z = wa * x.z + wb * y.z;
                 o.w = wa * x.w + wb * y.w;
-                st4(out + 4 * q, o);
+                stS<NT>(out + 4 * q, o);
             },
             [&](long long i) { out[i] = wa * a[i] + wb * b[i]; });
     } else {
@@ -115,19 +118,19 @@ __global__ __launch_bounds__(kTpb) void weighted_sum_kernel(float* out, const fl
 }
 
 // ---------------- x *= s[0]: 8 B/elem ----------------
-template <bool VEC>
+template <bool VEC, bool NT>
 __global__ __launch_bounds__(kTpb) void scale_kernel(float* __restrict__ x,
     const float* __restrict__ s, long long n) {
     const float v = s[0];
     if constexpr (VEC) {
         stream_loop(n / 4, n,
             [&](long long q) {
-                float4 t = ld4(x + 4 * q);
+                float4 t = ldS<NT>(x + 4 * q);
                 t.x *= v;
                 t.y *= v;
                 t.z *= v;
                 t.w *= v;
-                st4(x + 4 * q, t);
+                stS<NT>(x + 4 * q, t);
             },
             [&](long long i) { x[i] *= v; });
     } else {
@@ -141,19 +144,19 @@ __global__ __launch_bounds__(kTpb) void scale_kernel(float* __restrict__ x,
 }
 
 // ---------------- p -= lr*g: 12 B/elem ----------------
-template <bool VEC>
+template <bool VEC, bool NT>
 __global__ __launch_bounds__(kTpb) void sgd_kernel(float* __restrict__ p,
     const float* __restrict__ g, float lr, long long n) {
     if constexpr (VEC) {
         stream_loop(n / 4, n,
             [&](long long q) {
-                float4 t = ld4(p + 4 * q);
-                const float4 d = ld4(g + 4 * q);
+                float4 t = ldS<NT>(p + 4 * q);
+                const float4 d = ldS<NT>(g + 4 * q);
                 t.x -= lr * d.x;
                 t.y -= lr * d.y;
                 t.z -= lr * d.z;
                 t.w -= lr * d.w;
-                st4(p + 4 * q, t);
+                stS<NT>(p + 4 * q, t);
             },
             [&](long long i) { p[i] -= lr * g[i]; });
     } else {
@@ -181,6 +184,7 @@ __global__ __launch_bounds__(kTpb) void add_bias_kernel(float* __restrict__ Y,
     }
 }
 
+template <bool NT>
 __global__ __launch_bounds__(kTpb) void add_bias_vec_kernel(float* __restrict__ Y,
     const float* __restrict__ bias, long long total4, FastDiv divN4) {
     const long long base = (long long)blockIdx.x * kPerBlock + threadIdx.x;
@@ -189,13 +193,13 @@ __global__ __launch_bounds__(kTpb) void add_bias_vec_kernel(float* __restrict__ 
         const long long q = base + (long long)u * kTpb;
         if (q < total4) {
             const uint32_t c4 = (uint32_t)q - divN4.div((uint32_t)q) * divN4.d;
-            float4 y = ld4(Y + 4 * q);
+            float4 y = ldS<NT>(Y + 4 * q);
             const float4 bb = ld4(bias + 4 * c4);
             y.x += bb.x;
             y.y += bb.y;
             y.z += bb.z;
             y.w += bb.w;
-            st4(Y + 4 * q, y);
+            stS<NT>(Y + 4 * q, y);
         }
     }
 }
@@ -252,6 +256,7 @@ __global__ __launch_bounds__(kTpb) void mp_cat_kernel(float* __restrict__ out,
 }
 
 // float4 form: Na, Nb multiples of 4, all pointers 16-byte aligned.
+template <bool NT>
 __global__ __launch_bounds__(kTpb) void mp_cat_vec_kernel(float* __restrict__ out,
     const float* __restrict__ a, const float* __restrict__ b, float wa, float wb,
     long long total4, int Na4, int Nb4, FastDiv divN4) {
@@ -265,17 +270,17 @@ __global__ __launch_bounds__(kTpb) void mp_cat_vec_kernel(float* __restrict__ ou
             float4 v;
             float w;
             if ((int)c4 < Na4) {
-                v = ld4(a + 4 * ((size_t)r * Na4 + c4));
+                v = ldS<NT>(a + 4 * ((size_t)r * Na4 + c4));
                 w = wa;
             } else {
-                v = ld4(b + 4 * ((size_t)r * Nb4 + (c4 - Na4)));
+                v = ldS<NT>(b + 4 * ((size_t)r * Nb4 + (c4 - Na4)));
                 w = wb;
             }
             v.x *= w;
             v.y *= w;
             v.z *= w;
             v.w *= w;
-            st4(out + 4 * q, v);
+            stS<NT>(out + 4 * q, v);
         }
     }
 }
@@ -297,6 +302,7 @@ __global__ __launch_bounds__(kTpb) void mp_split_kernel(float* __restrict__ ga,
     }
 }
 
+template <bool NT>
 __global__ __launch_bounds__(kTpb) void mp_split_vec_kernel(float* __restrict__ ga,
     float* __restrict__ gb, const float* __restrict__ g, float wa, float wb, long long total4,
     int Ca4, int Cb4, FastDiv divN4) {
@@ -307,19 +313,19 @@ __global__ __launch_bounds__(kTpb) void mp_split_vec_kernel(float* __restrict__ 
         if (q < total4) {
             uint32_t r, c4;
             divN4.divmod((uint32_t)q, r, c4);
-            float4 v = ld4(g + 4 * q);
+            float4 v = ldS<NT>(g + 4 * q);
             if ((int)c4 < Ca4) {
                 v.x *= wa;
                 v.y *= wa;
                 v.z *= wa;
                 v.w *= wa;
-                st4(ga + 4 * ((size_t)r * Ca4 + c4), v);
+                stS<NT>(ga + 4 * ((size_t)r * Ca4 + c4), v);
             } else {
                 v.x *= wb;
                 v.y *= wb;
                 v.z *= wb;
                 v.w *= wb;
-                st4(gb + 4 * ((size_t)r * Cb4 + (c4 - Ca4)), v);
+                stS<NT>(gb + 4 * ((size_t)r * Cb4 + (c4 - Ca4)), v);
             }
         }
     }
@@ -351,8 +357,12 @@ void mp_cat_impl(const char* what, float* out, const float* a, const float* b, f
     NNK_REQUIRE(out && a && b, what, "%s: null pointer", what);
     if (Na % 4 == 0 && Nb % 4 == 0 && aligned16(out) && aligned16(a) && aligned16(b)) {
         const long long total4 = total / 4;
-        mp_cat_vec_kernel<<<blocks_for(total4), kTpb, 0, s>>>(out, a, b, wa, wb, total4, Na / 4,
-            Nb / 4, FastDiv((uint32_t)((Na + Nb) / 4)));
+        if (use_nt(8 * total))
+            mp_cat_vec_kernel<true><<<blocks_for(total4), kTpb, 0, s>>>(out, a, b, wa, wb, total4, Na / 4,
+                Nb / 4, FastDiv((uint32_t)((Na + Nb) / 4)));
+        else
+            mp_cat_vec_kernel<false><<<blocks_for(total4), kTpb, 0, s>>>(out, a, b, wa, wb, total4, Na / 4,
+                Nb / 4, FastDiv((uint32_t)((Na + Nb) / 4)));
     } else {
         mp_cat_kernel<<<blocks_for(total), kTpb, 0, s>>>(out, a, b, wa, wb, total, Na, Nb,
             FastDiv((uint32_t)(Na + Nb)));
@@ -371,10 +381,12 @@ void launch_activation_forward(float* out, const float* in, int n, Activation ac
     NNK_REQUIRE(out && in, "act", "launch_activation_forward: null pointer");
     const bool vec = aligned16(out) && aligned16(in);
     const unsigned blocks = blocks_for(vec ? n / 4 : n);
-    if (vec)
-        NNK_ACT_DISPATCH(act, A, act_fwd_kernel<A, true><<<blocks, kTpb, 0, s>>>(out, in, n));
+    if (vec && use_nt(8LL * n))
+        NNK_ACT_DISPATCH(act, A, act_fwd_kernel<A, true, true><<<blocks, kTpb, 0, s>>>(out, in, n));
+    else if (vec)
+        NNK_ACT_DISPATCH(act, A, act_fwd_kernel<A, true, false><<<blocks, kTpb, 0, s>>>(out, in, n));
     else
-        NNK_ACT_DISPATCH(act, A, act_fwd_kernel<A, false><<<blocks, kTpb, 0, s>>>(out, in, n));
+        NNK_ACT_DISPATCH(act, A, act_fwd_kernel<A, false, false><<<blocks, kTpb, 0, s>>>(out, in, n));
     nnk_after_launch("launch_activation_forward", s);
 }
 
@@ -386,10 +398,12 @@ void launch_activation_backward(float* grad_in, const float* grad_out, const flo
     NNK_REQUIRE(grad_in && grad_out && in, "act", "launch_activation_backward: null pointer");
     const bool vec = aligned16(grad_in) && aligned16(grad_out) && aligned16(in);
     const unsigned blocks = blocks_for(vec ? n / 4 : n);
-    if (vec)
-        NNK_ACT_DISPATCH(act, A, act_bwd_kernel<A, true><<<blocks, kTpb, 0, s>>>(grad_in, grad_out, in, n));
+    if (vec && use_nt(12LL * n))
+        NNK_ACT_DISPATCH(act, A, act_bwd_kernel<A, true, true><<<blocks, kTpb, 0, s>>>(grad_in, grad_out, in, n));
+    else if (vec)
+        NNK_ACT_DISPATCH(act, A, act_bwd_kernel<A, true, false><<<blocks, kTpb, 0, s>>>(grad_in, grad_out, in, n));
     else
-        NNK_ACT_DISPATCH(act, A, act_bwd_kernel<A, false><<<blocks, kTpb, 0, s>>>(grad_in, grad_out, in, n));
+        NNK_ACT_DISPATCH(act, A, act_bwd_kernel<A, false, false><<<blocks, kTpb, 0, s>>>(grad_in, grad_out, in, n));
     nnk_after_launch("launch_activation_backward", s);
 }
 
@@ -399,10 +413,12 @@ void launch_weighted_sum(float* out, const float* a, const float* b, float wa, f
     if (n == 0) return;
     NNK_REQUIRE(out && a && b, "ws", "launch_weighted_sum: null pointer");
     const bool vec = aligned16(out) && aligned16(a) && aligned16(b);
-    if (vec)
-        weighted_sum_kernel<true><<<blocks_for(n / 4), kTpb, 0, s>>>(out, a, b, wa, wb, n);
+    if (vec && use_nt(12LL * n))
+        weighted_sum_kernel<true, true><<<blocks_for(n / 4), kTpb, 0, s>>>(out, a, b, wa, wb, n);
+    else if (vec)
+        weighted_sum_kernel<true, false><<<blocks_for(n / 4), kTpb, 0, s>>>(out, a, b, wa, wb, n);
     else
-        weighted_sum_kernel<false><<<blocks_for(n), kTpb, 0, s>>>(out, a, b, wa, wb, n);
+        weighted_sum_kernel<false, false><<<blocks_for(n), kTpb, 0, s>>>(out, a, b, wa, wb, n);
     nnk_after_launch("launch_weighted_sum", s);
 }
 
@@ -416,10 +432,12 @@ void launch_scale_by_scalar(float* x, const float* sc, int n, hipStream_t s) {
     NNK_REQUIRE(n >= 0, "scale", "launch_scale_by_scalar: n=%d", n);
     if (n == 0) return;
     NNK_REQUIRE(x && sc, "scale", "launch_scale_by_scalar: null pointer");
-    if (aligned16(x))
-        scale_kernel<true><<<blocks_for(n / 4), kTpb, 0, s>>>(x, sc, n);
+    if (aligned16(x) && use_nt(8LL * n))
+        scale_kernel<true, true><<<blocks_for(n / 4), kTpb, 0, s>>>(x, sc, n);
+    else if (aligned16(x))
+        scale_kernel<true, false><<<blocks_for(n / 4), kTpb, 0, s>>>(x, sc, n);
     else
-        scale_kernel<false><<<blocks_for(n), kTpb, 0, s>>>(x, sc, n);
+        scale_kernel<false, false><<<blocks_for(n), kTpb, 0, s>>>(x, sc, n);
     nnk_after_launch("launch_scale_by_scalar", s);
 }
 
@@ -427,10 +445,12 @@ void launch_sgd_step(float* p, const float* g, float lr, int n, hipStream_t s) {
     NNK_REQUIRE(n >= 0, "sgd", "launch_sgd_step: n=%d", n);
     if (n == 0) return;
     NNK_REQUIRE(p && g, "sgd", "launch_sgd_step: null pointer");
-    if (aligned16(p) && aligned16(g))
-        sgd_kernel<true><<<blocks_for(n / 4), kTpb, 0, s>>>(p, g, lr, n);
+    if (aligned16(p) && aligned16(g) && use_nt(12LL * n))
+        sgd_kernel<true, true><<<blocks_for(n / 4), kTpb, 0, s>>>(p, g, lr, n);
+    else if (aligned16(p) && aligned16(g))
+        sgd_kernel<true, false><<<blocks_for(n / 4), kTpb, 0, s>>>(p, g, lr, n);
     else
-        sgd_kernel<false><<<blocks_for(n), kTpb, 0, s>>>(p, g, lr, n);
+        sgd_kernel<false, false><<<blocks_for(n), kTpb, 0, s>>>(p, g, lr, n);
     nnk_after_launch("launch_sgd_step", s);
 }
 
@@ -440,8 +460,10 @@ void launch_add_bias(float* Y, const float* b, int M, int N, hipStream_t s) {
     NNK_REQUIRE(fits_i32(total), "bias", "launch_add_bias: %lld elements exceed 2^31", total);
     if (total == 0) return;
     NNK_REQUIRE(Y && b, "bias", "launch_add_bias: null pointer");
-    if (N % 4 == 0 && aligned16(Y) && aligned16(b))
-        add_bias_vec_kernel<<<blocks_for(total / 4), kTpb, 0, s>>>(Y, b, total / 4, FastDiv((uint32_t)(N / 4)));
+    if (N % 4 == 0 && aligned16(Y) && aligned16(b) && use_nt(8 * total))
+        add_bias_vec_kernel<true><<<blocks_for(total / 4), kTpb, 0, s>>>(Y, b, total / 4, FastDiv((uint32_t)(N / 4)));
+    else if (N % 4 == 0 && aligned16(Y) && aligned16(b))
+        add_bias_vec_kernel<false><<<blocks_for(total / 4), kTpb, 0, s>>>(Y, b, total / 4, FastDiv((uint32_t)(N / 4)));
     else
         add_bias_kernel<<<blocks_for(total), kTpb, 0, s>>>(Y, b, total, FastDiv((uint32_t)N));
     nnk_after_launch("launch_add_bias", s);
@@ -492,8 +514,12 @@ void launch_mp_channel_split(float* grad_a, float* grad_b, const float* grad_out
     mp_cat_weights(t, Ca, Cb, &wa, &wb);
     if (Ca % 4 == 0 && Cb % 4 == 0 && aligned16(grad_a) && aligned16(grad_b) && aligned16(grad_out)) {
         const long long total4 = total / 4;
-        mp_split_vec_kernel<<<blocks_for(total4), kTpb, 0, s>>>(grad_a, grad_b, grad_out, wa, wb,
-            total4, Ca / 4, Cb / 4, FastDiv((uint32_t)((Ca + Cb) / 4)));
+        if (use_nt(8 * total))
+            mp_split_vec_kernel<true><<<blocks_for(total4), kTpb, 0, s>>>(grad_a, grad_b, grad_out, wa, wb,
+                total4, Ca / 4, Cb / 4, FastDiv((uint32_t)((Ca + Cb) / 4)));
+        else
+            mp_split_vec_kernel<false><<<blocks_for(total4), kTpb, 0, s>>>(grad_a, grad_b, grad_out, wa, wb,
+                total4, Ca / 4, Cb / 4, FastDiv((uint32_t)((Ca + Cb) / 4)));
     } else {
         mp_split_kernel<<<blocks_for(total), kTpb, 0, s>>>(grad_a, grad_b, grad_out, wa, wb, total,
             Ca, Cb, FastDiv((uint32_t)(Ca + Cb)));

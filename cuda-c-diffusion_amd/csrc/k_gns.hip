@@ -84,7 +84,7 @@ void nnk_gns_clear_workspace(float* ws, size_t n_floats, hipStream_t s) {
 // Persistent grid size for a kernel: resident workgroups of the device
 // (cached per device and kernel), capped and rounded down to whole units.
 int nnk_gns_grid(const void* fn, int key, size_t lds, int unit) {
-    constexpr int kDev = 16, kKeys = 128;
+    constexpr int kDev = 16, kKeys = 256;
     static int occ_cache[kDev][kKeys];
     static int cu_cache[kDev];
     int dev = 0;

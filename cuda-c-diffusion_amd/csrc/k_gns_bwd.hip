@@ -9,13 +9,13 @@ namespace {
 using namespace nnk;
 using namespace nnk::gns;
 
-template <int ACT, int CPG4, int RPL>
+template <int ACT, int CPG4, int RPL, bool NT>
 bool launch(const Plan& p, float* dx, float* ggamma, float* gbeta, const float* dy, const float* x,
     const float* gamma, const float* beta, const float* mu, const float* rstd, float* ws, hipStream_t s) {
     using Gm = Geom<kTpb, kBwdTp, kCw4, CPG4>;
-    const void* fn = reinterpret_cast<const void*>(&gns_bwd<Gm, ACT, RPL>);
+    const void* fn = reinterpret_cast<const void*>(&gns_bwd<Gm, ACT, RPL, NT>);
     const size_t lds = 0;  // all LDS is static (stage, parked, reduction buffers)
-    const int key = 64 + (ACT * 3 + (CPG4 == 1 ? 0 : CPG4 == 2 ? 1 : 2)) * 2 + (RPL - 1);
+    const int key = 128 + ((ACT * 3 + (CPG4 == 1 ? 0 : CPG4 == 2 ? 1 : 2)) * 2 + (RPL - 1)) * 2 + (NT ? 1 : 0);
     const int P = nnk_gns_grid(fn, key, lds, p.sh.T * p.sh.NCB);
     if (P <= 0) return false;
     Shape sh = p.sh;
@@ -41,9 +41,11 @@ bool launch(const Plan& p, float* dx, float* ggamma, float* gbeta, const float* 
 template <int ACT>
 bool by_shape(const Plan& p, float* dx, float* ggamma, float* gbeta, const float* dy, const float* x,
     const float* gamma, const float* beta, const float* mu, const float* rstd, float* ws, hipStream_t s) {
+    const bool nt = use_nt(12LL * p.sh.B * p.sh.HW * p.sh.C);
 #define NNK_GNS_BWD_CASE(CPG4, RPL)                                                                          \
     if (p.cpg4 == CPG4 && p.rpl == RPL)                                                                      \
-        return launch<ACT, CPG4, RPL>(p, dx, ggamma, gbeta, dy, x, gamma, beta, mu, rstd, ws, s);
+        return nt ? launch<ACT, CPG4, RPL, true>(p, dx, ggamma, gbeta, dy, x, gamma, beta, mu, rstd, ws, s)  \
+                  : launch<ACT, CPG4, RPL, false>(p, dx, ggamma, gbeta, dy, x, gamma, beta, mu, rstd, ws, s);
     NNK_GNS_BWD_CASE(1, 1)
     NNK_GNS_BWD_CASE(1, 2)
     NNK_GNS_BWD_CASE(2, 1)

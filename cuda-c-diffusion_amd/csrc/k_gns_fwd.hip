@@ -9,13 +9,13 @@ namespace {
 using namespace nnk;
 using namespace nnk::gns;
 
-template <int ACT, int CPG4, int RPL>
+template <int ACT, int CPG4, int RPL, bool NT>
 bool launch(const Plan& p, float* y, float* mu, float* rstd, const float* x, const float* gamma,
     const float* beta, float eps, float* ws, hipStream_t s) {
     using Gm = Geom<kTpb, kFwdTp, kCw4, CPG4>;
-    const void* fn = reinterpret_cast<const void*>(&gns_fwd<Gm, ACT, RPL>);
+    const void* fn = reinterpret_cast<const void*>(&gns_fwd<Gm, ACT, RPL, NT>);
     const size_t lds = 0;  // all LDS is static (stage, parked, reduction buffers)
-    const int key = (ACT * 3 + (CPG4 == 1 ? 0 : CPG4 == 2 ? 1 : 2)) * 2 + (RPL - 1);
+    const int key = ((ACT * 3 + (CPG4 == 1 ? 0 : CPG4 == 2 ? 1 : 2)) * 2 + (RPL - 1)) * 2 + (NT ? 1 : 0);
     const int P = nnk_gns_grid(fn, key, lds, p.sh.T * p.sh.NCB);
     if (P <= 0) return false;
     Shape sh = p.sh;
@@ -40,8 +40,11 @@ bool launch(const Plan& p, float* y, float* mu, float* rstd, const float* x, con
 template <int ACT>
 bool by_shape(const Plan& p, float* y, float* mu, float* rstd, const float* x, const float* gamma,
     const float* beta, float eps, float* ws, hipStream_t s) {
+    const bool nt = use_nt(8LL * p.sh.B * p.sh.HW * p.sh.C);
 #define NNK_GNS_FWD_CASE(CPG4, RPL)                                                     \
-    if (p.cpg4 == CPG4 && p.rpl == RPL) return launch<ACT, CPG4, RPL>(p, y, mu, rstd, x, gamma, beta, eps, ws, s);
+    if (p.cpg4 == CPG4 && p.rpl == RPL)                                                 \
+        return nt ? launch<ACT, CPG4, RPL, true>(p, y, mu, rstd, x, gamma, beta, eps, ws, s)  \
+                  : launch<ACT, CPG4, RPL, false>(p, y, mu, rstd, x, gamma, beta, eps, ws, s);
     NNK_GNS_FWD_CASE(1, 1)
     NNK_GNS_FWD_CASE(1, 2)
     NNK_GNS_FWD_CASE(2, 1)

@@ -12,6 +12,8 @@
 //               segments of 64 partial rows on many workgroups, ln_colsum2
 //               adds the segment sums.
 // Generic path: one 256-thread block per row plus a coalesced partial kernel.
+// The fast path streams x, dy, y, dx with nontemporal loads and stores when
+// the launch is large (use_nt).
 #include "nnk_common.h"
 
 namespace {
@@ -25,7 +27,7 @@ constexpr int kRowsPerWg = 64;  // backward partial granularity (both paths)
 // ----------------------------------------------------------------------------
 // Fast forward: NV float4 per lane per row, RB rows per wave at a time.
 // ----------------------------------------------------------------------------
-template <int NV, int RB>
+template <int NV, int RB, bool NT>
 __global__ __launch_bounds__(kTpb) void ln_fwd_wave(float* __restrict__ y,
     float* __restrict__ mu, float* __restrict__ rstd, const float* __restrict__ x,
     const float* __restrict__ gamma, const float* __restrict__ beta, int rows, int C, float eps) {
@@ -42,7 +44,7 @@ __global__ __launch_bounds__(kTpb) void ln_fwd_wave(float* __restrict__ y,
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
             const int c4 = lane + k * kWave;
-            if (row < rows && c4 < C4) v[r][k] = ld4(x + (size_t)row * C + 4 * c4);
+            if (row < rows && c4 < C4) v[r][k] = ldS<NT>(x + (size_t)row * C + 4 * c4);
             else v[r][k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         }
     }
@@ -78,7 +80,7 @@ __global__ __launch_bounds__(kTpb) void ln_fwd_wave(float* __restrict__ y,
                     o.y = gm.y * ((v[r][k].y - m) * rs) + bt.y;
                     o.z = gm.z * ((v[r][k].z - m) * rs) + bt.z;
                     o.w = gm.w * ((v[r][k].w - m) * rs) + bt.w;
-                    st4(y + (size_t)row * C + 4 * c4, o);
+                    stS<NT>(y + (size_t)row * C + 4 * c4, o);
                 }
             }
         }
@@ -90,7 +92,7 @@ __global__ __launch_bounds__(kTpb) void ln_fwd_wave(float* __restrict__ y,
 // them RB at a time, then the 4 waves' channel sums are combined in LDS into
 // part_g/part_b[b*C + c].
 // ----------------------------------------------------------------------------
-template <int NV, int RB>
+template <int NV, int RB, bool NT>
 __global__ __launch_bounds__(kTpb) void ln_bwd_wave(float* __restrict__ dx,
     float* __restrict__ part_g, float* __restrict__ part_b, const float* __restrict__ dy,
     const float* __restrict__ x, const float* __restrict__ gamma,
@@ -122,8 +124,8 @@ __global__ __launch_bounds__(kTpb) void ln_bwd_wave(float* __restrict__ dx,
             for (int k = 0; k < NV; ++k) {
                 const int c4 = lane + k * kWave;
                 if (row < rows && c4 < C4) {
-                    xv[r][k] = ld4(x + (size_t)row * C + 4 * c4);
-                    gv[r][k] = ld4(dy + (size_t)row * C + 4 * c4);
+                    xv[r][k] = ldS<NT>(x + (size_t)row * C + 4 * c4);
+                    gv[r][k] = ldS<NT>(dy + (size_t)row * C + 4 * c4);
                 } else {
                     xv[r][k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
                     gv[r][k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -174,7 +176,7 @@ __global__ __launch_bounds__(kTpb) void ln_bwd_wave(float* __restrict__ dx,
                     o.y = rs * ((gv[r][k].y - m1) - xv[r][k].y * S2 * invC);
                     o.z = rs * ((gv[r][k].z - m1) - xv[r][k].z * S2 * invC);
                     o.w = rs * ((gv[r][k].w - m1) - xv[r][k].w * S2 * invC);
-                    st4(dx + (size_t)row * C + 4 * c4, o);
+                    stS<NT>(dx + (size_t)row * C + 4 * c4, o);
                 }
             }
         }
@@ -393,11 +395,16 @@ void ln_backward_impl(const char* what, float* dx, float* ggamma, float* gbeta, 
     float* seg_b = seg_g + sc;
     const int nv = fast_nv(C, dx, dy, x, gamma);
     if (nv && (C % 4 == 0) && aligned16(part_b)) {
+        const bool nt = use_nt(12LL * rows * C);
+#define NNK_LN_BWD(NV_, RB_)                                                                                \
+    (nt ? ln_bwd_wave<NV_, RB_, true><<<P, kTpb, 0, s>>>(dx, part_g, part_b, dy, x, gamma, mu, rstd, rows, C) \
+        : ln_bwd_wave<NV_, RB_, false><<<P, kTpb, 0, s>>>(dx, part_g, part_b, dy, x, gamma, mu, rstd, rows, C))
         switch (nv) {
-        case 1: ln_bwd_wave<1, 4><<<P, kTpb, 0, s>>>(dx, part_g, part_b, dy, x, gamma, mu, rstd, rows, C); break;
-        case 2: ln_bwd_wave<2, 2><<<P, kTpb, 0, s>>>(dx, part_g, part_b, dy, x, gamma, mu, rstd, rows, C); break;
-        default: ln_bwd_wave<4, 1><<<P, kTpb, 0, s>>>(dx, part_g, part_b, dy, x, gamma, mu, rstd, rows, C); break;
+        case 1: NNK_LN_BWD(1, 4); break;
+        case 2: NNK_LN_BWD(2, 2); break;
+        default: NNK_LN_BWD(4, 1); break;
         }
+#undef NNK_LN_BWD
     } else {
         ln_bwd_dx_generic<<<rows, kTpb, 0, s>>>(dx, dy, x, gamma, mu, rstd, C);
         ln_param_partial_generic<<<dim3((unsigned)((C + kWave - 1) / kWave), (unsigned)P), kTpb, 0, s>>>(
@@ -423,13 +430,22 @@ void launch_layernorm_forward(float* y, float* mu, float* rstd, const float* x, 
     const int nv = fast_nv(C, y, x, gamma, beta);
     if (nv == 1) {
         constexpr int RB = 4;
-        ln_fwd_wave<1, RB><<<(unsigned)((batch + kNw * RB - 1) / (kNw * RB)), kTpb, 0, s>>>(y, mu, rstd, x, gamma, beta, batch, C, eps);
+        if (use_nt(8LL * batch * C))
+            ln_fwd_wave<1, RB, true><<<(unsigned)((batch + kNw * RB - 1) / (kNw * RB)), kTpb, 0, s>>>(y, mu, rstd, x, gamma, beta, batch, C, eps);
+        else
+            ln_fwd_wave<1, RB, false><<<(unsigned)((batch + kNw * RB - 1) / (kNw * RB)), kTpb, 0, s>>>(y, mu, rstd, x, gamma, beta, batch, C, eps);
     } else if (nv == 2) {
         constexpr int RB = 2;
-        ln_fwd_wave<2, RB><<<(unsigned)((batch + kNw * RB - 1) / (kNw * RB)), kTpb, 0, s>>>(y, mu, rstd, x, gamma, beta, batch, C, eps);
+        if (use_nt(8LL * batch * C))
+            ln_fwd_wave<2, RB, true><<<(unsigned)((batch + kNw * RB - 1) / (kNw * RB)), kTpb, 0, s>>>(y, mu, rstd, x, gamma, beta, batch, C, eps);
+        else
+            ln_fwd_wave<2, RB, false><<<(unsigned)((batch + kNw * RB - 1) / (kNw * RB)), kTpb, 0, s>>>(y, mu, rstd, x, gamma, beta, batch, C, eps);
     } else if (nv == 4) {
         constexpr int RB = 1;
-        ln_fwd_wave<4, RB><<<(unsigned)((batch + kNw * RB - 1) / (kNw * RB)), kTpb, 0, s>>>(y, mu, rstd, x, gamma, beta, batch, C, eps);
+        if (use_nt(8LL * batch * C))
+            ln_fwd_wave<4, RB, true><<<(unsigned)((batch + kNw * RB - 1) / (kNw * RB)), kTpb, 0, s>>>(y, mu, rstd, x, gamma, beta, batch, C, eps);
+        else
+            ln_fwd_wave<4, RB, false><<<(unsigned)((batch + kNw * RB - 1) / (kNw * RB)), kTpb, 0, s>>>(y, mu, rstd, x, gamma, beta, batch, C, eps);
     } else {
         ln_fwd_generic<<<(unsigned)batch, kTpb, 0, s>>>(y, mu, rstd, x, gamma, beta, C, eps);
     }

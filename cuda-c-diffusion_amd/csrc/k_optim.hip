@@ -8,7 +8,8 @@
 // 4096-element chunks (tensor, chunk index); one workgroup updates one chunk,
 // so a whole parameter list is one launch instead of one per tensor.  Per
 // parameter the fused step moves 36 bytes (read p, g, m, v, shadow; write p,
-// m, v, shadow); p_new feeds the EMA from registers.
+// m, v, shadow); p_new feeds the EMA from registers.  Large plans stream all
+// five tensors with nontemporal loads and stores (use_nt).
 #include <stdlib.h>
 #include <string.h>
 
@@ -45,6 +46,7 @@ __device__ __forceinline__ float adam_one(float& p, float& m, float& v, float g,
     return p;
 }
 
+template <bool NT>
 __global__ __launch_bounds__(kTpb) void adam_kernel(float* __restrict__ p, float* __restrict__ m,
     float* __restrict__ v, const float* __restrict__ g, AdamArgs a, long long n, int vec) {
     const long long start = (long long)blockIdx.x * kChunk;
@@ -53,15 +55,15 @@ __global__ __launch_bounds__(kTpb) void adam_kernel(float* __restrict__ p, float
         const long long nv = (end - start) / 4;
         for (long long q = threadIdx.x; q < nv; q += kTpb) {
             const long long i = start + 4 * q;
-            float4 pp = ld4(p + i), mm = ld4(m + i), vv = ld4(v + i);
-            const float4 gg = ld4(g + i);
+            float4 pp = ldS<NT>(p + i), mm = ldS<NT>(m + i), vv = ldS<NT>(v + i);
+            const float4 gg = ldS<NT>(g + i);
             adam_one(pp.x, mm.x, vv.x, gg.x, a);
             adam_one(pp.y, mm.y, vv.y, gg.y, a);
             adam_one(pp.z, mm.z, vv.z, gg.z, a);
             adam_one(pp.w, mm.w, vv.w, gg.w, a);
-            st4(p + i, pp);
-            st4(m + i, mm);
-            st4(v + i, vv);
+            stS<NT>(p + i, pp);
+            stS<NT>(m + i, mm);
+            stS<NT>(v + i, vv);
         }
         const long long t = start + 4 * nv + threadIdx.x;
         if (t < end) adam_one(p[t], m[t], v[t], g[t], a);
@@ -71,7 +73,7 @@ __global__ __launch_bounds__(kTpb) void adam_kernel(float* __restrict__ p, float
 }
 
 // mode 0: Adam only, 1: Adam then EMA, 2: EMA only (shadow = w0*shadow + w1*p)
-template <int MODE>
+template <int MODE, bool NT>
 __global__ __launch_bounds__(kTpb) void multi_tensor_kernel(const DevSlot* __restrict__ slots,
     const int2* __restrict__ chunks, AdamArgs a, float w0, float w1) {
     const int2 ch = chunks[blockIdx.x];
@@ -83,25 +85,25 @@ __global__ __launch_bounds__(kTpb) void multi_tensor_kernel(const DevSlot* __res
         const long long nv = (end - start) / 4;
         for (long long q = threadIdx.x; q < nv; q += kTpb) {
             const long long i = start + 4 * q;
-            float4 pp = ld4(t.p + i);
+            float4 pp = ldS<NT>(t.p + i);
             if constexpr (MODE != 2) {
-                float4 mm = ld4(t.m + i), vv = ld4(t.v + i);
-                const float4 gg = ld4(t.g + i);
+                float4 mm = ldS<NT>(t.m + i), vv = ldS<NT>(t.v + i);
+                const float4 gg = ldS<NT>(t.g + i);
                 adam_one(pp.x, mm.x, vv.x, gg.x, a);
                 adam_one(pp.y, mm.y, vv.y, gg.y, a);
                 adam_one(pp.z, mm.z, vv.z, gg.z, a);
                 adam_one(pp.w, mm.w, vv.w, gg.w, a);
-                st4(t.p + i, pp);
-                st4(t.m + i, mm);
-                st4(t.v + i, vv);
+                stS<NT>(t.p + i, pp);
+                stS<NT>(t.m + i, mm);
+                stS<NT>(t.v + i, vv);
             }
             if (ema) {
-                float4 sh = ld4(t.shadow + i);
+                float4 sh = ldS<NT>(t.shadow + i);
                 sh.x = w0 * sh.x + w1 * pp.x;
                 sh.y = w0 * sh.y + w1 * pp.y;
                 sh.z = w0 * sh.z + w1 * pp.z;
                 sh.w = w0 * sh.w + w1 * pp.w;
-                st4(t.shadow + i, sh);
+                stS<NT>(t.shadow + i, sh);
             }
         }
         const long long i = start + 4 * nv + threadIdx.x;
@@ -140,7 +142,10 @@ void launch_adam_step(float* p, float* m, float* v, const float* g, float lr, fl
     NNK_REQUIRE(p && m && v && g, what, "%s: null pointer", what);
     const AdamArgs a{lr, beta1, beta2, eps, bc1, bc2};
     const int vec = aligned16(p) && aligned16(m) && aligned16(v) && aligned16(g);
-    adam_kernel<<<(unsigned)((n + kChunk - 1) / kChunk), kTpb, 0, s>>>(p, m, v, g, a, n, vec);
+    if (use_nt(28LL * n))
+        adam_kernel<true><<<(unsigned)((n + kChunk - 1) / kChunk), kTpb, 0, s>>>(p, m, v, g, a, n, vec);
+    else
+        adam_kernel<false><<<(unsigned)((n + kChunk - 1) / kChunk), kTpb, 0, s>>>(p, m, v, g, a, n, vec);
     nnk_after_launch(what, s);
 }
 
@@ -210,10 +215,19 @@ void launch_adam_ema_step(const NnMultiTensorPlan* plan, float lr, float beta1, 
     NNK_REQUIRE(plan->has_adam, what, "%s: plan lacks m/v/g for some tensor", what);
     if (plan->nchunks == 0) return;
     const AdamArgs a{lr, beta1, beta2, eps, bc1, bc2};
-    if (ema_w1 != 0.0f || ema_w0 != 1.0f)
-        multi_tensor_kernel<1><<<(unsigned)plan->nchunks, kTpb, 0, s>>>(plan->d_slots, plan->d_chunks, a, ema_w0, ema_w1);
-    else
-        multi_tensor_kernel<0><<<(unsigned)plan->nchunks, kTpb, 0, s>>>(plan->d_slots, plan->d_chunks, a, ema_w0, ema_w1);
+    const long long elems = (long long)plan->nchunks * kChunk;  // upper bound of the plan's parameters
+    const unsigned grid = (unsigned)plan->nchunks;
+    if (ema_w1 != 0.0f || ema_w0 != 1.0f) {
+        if (use_nt(36 * elems))
+            multi_tensor_kernel<1, true><<<grid, kTpb, 0, s>>>(plan->d_slots, plan->d_chunks, a, ema_w0, ema_w1);
+        else
+            multi_tensor_kernel<1, false><<<grid, kTpb, 0, s>>>(plan->d_slots, plan->d_chunks, a, ema_w0, ema_w1);
+    } else {
+        if (use_nt(28 * elems))
+            multi_tensor_kernel<0, true><<<grid, kTpb, 0, s>>>(plan->d_slots, plan->d_chunks, a, ema_w0, ema_w1);
+        else
+            multi_tensor_kernel<0, false><<<grid, kTpb, 0, s>>>(plan->d_slots, plan->d_chunks, a, ema_w0, ema_w1);
+    }
     nnk_after_launch(what, s);
 }
 
@@ -223,7 +237,10 @@ void launch_ema_update(const NnMultiTensorPlan* plan, float w0, float w1, hipStr
     NNK_REQUIRE(plan->has_ema, what, "%s: plan lacks a shadow for some tensor", what);
     if (plan->nchunks == 0) return;
     const AdamArgs a{0, 0, 0, 0, 1, 1};
-    multi_tensor_kernel<2><<<(unsigned)plan->nchunks, kTpb, 0, s>>>(plan->d_slots, plan->d_chunks, a, w0, w1);
+    if (use_nt(12LL * plan->nchunks * kChunk))
+        multi_tensor_kernel<2, true><<<(unsigned)plan->nchunks, kTpb, 0, s>>>(plan->d_slots, plan->d_chunks, a, w0, w1);
+    else
+        multi_tensor_kernel<2, false><<<(unsigned)plan->nchunks, kTpb, 0, s>>>(plan->d_slots, plan->d_chunks, a, w0, w1);
     nnk_after_launch(what, s);
 }
 

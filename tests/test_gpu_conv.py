@@ -21,6 +21,13 @@ GEOMS = [
     (2, 9, 8, 8, 4, 2, 1),        # even kernel, stride 2
     (1, 4, 4, 12, 5, 1, 2),       # kernel larger than the image's interior
     (3, 8, 8, 6, 3, 3, 0),        # stride 3, no padding
+    # row-tiled im2col (C/4 divides 256, C/4 >= 4)
+    (2, 9, 7, 16, 3, 1, 1),       # C/4 = 4: 64 rows per tile, ragged last tile
+    (3, 10, 6, 64, 4, 2, 1),      # even kernel, stride 2
+    (2, 5, 5, 32, 1, 1, 0),       # 1x1 kernel
+    (1, 9, 9, 256, 3, 2, 1),      # C/4 = 64
+    (1, 6, 5, 1024, 3, 1, 1),     # one row per tile
+    (2, 6, 6, 48, 3, 1, 1),       # C/4 = 12 does not divide 256: generic vector path
 ]
 
 
