@@ -228,6 +228,12 @@ def run_suite(L, nn, reps):
     _row("weight_normalize_backward", "cfg2 W[1152,128]",
          T.median_us(lambda: L.launch_weight_normalize_backward(M.p, W.p, gain.p, ggn.p, Kg, Co, stream), reps),
          12 * Kg * Co, "latency-bound")
+    wn_ws = L.alloc(int(L.nnhip_weight_normalize_backward_workspace(Co)))
+    wn_ws.fill_bytes(0)
+    _row("weight_normalize_backward_ws", "cfg2 W[1152,128], lent workspace",
+         T.median_us(lambda: L.launch_weight_normalize_backward_ws(M.p, W.p, gain.p, ggn.p, Kg, Co, wn_ws.p,
+                                                                   stream), reps),
+         12 * Kg * Co, "latency-bound")
     sig = np.exp(-1.2 + 1.2 * rng.standard_normal(128)).clip(0.002, 80)
     xs, fr, ph = dev(np.log(sig) / 4), dev(rng.standard_normal(256)), dev(rng.uniform(0, 1, 256))
     emb = L.alloc(128 * 256)

@@ -66,6 +66,7 @@ _SIGS = {
     "nnhip_event_synchronize": (I, [P], False),
     "nnhip_event_elapsed_ms": (F, [P, P], False),
     "nnhip_copy_f32": (None, [P, P, SZ, P], True),
+    "nnhip_fill_f32": (None, [P, F, SZ, P], True),
     # launch layer (nn_hip.h)
     "launch_add_bias": (None, [P, P, I, I, P], True),
     "launch_bias_grad": (None, [P, P, I, I, P], True),
@@ -75,6 +76,8 @@ _SIGS = {
     "launch_adam_step": (None, [P, P, P, P, F, F, F, F, F, F, I, P], True),
     "launch_weight_normalize": (None, [P, I, I, F, P], True),
     "launch_weight_normalize_backward": (None, [P, P, P, P, I, I, P], True),
+    "launch_weight_normalize_backward_ws": (None, [P, P, P, P, I, I, P, P], True),
+    "nnhip_weight_normalize_backward_workspace": (SZ, [I], False),
     "launch_scale_by_scalar": (None, [P, P, I, P], True),
     "launch_mp_sum": (None, [P, P, P, F, I, P], True),
     "launch_weighted_sum": (None, [P, P, P, F, F, I, P], True),

@@ -370,3 +370,12 @@ void nnk_scratch_release(float* p, hipStream_t s);
             return;                                          \
         }                                                    \
     } while (0)
+
+// As NNK_REQUIRE, in a function returning `ret`.
+#define NNK_REQUIRE_RET(cond, ret, what, ...)                \
+    do {                                                     \
+        if (!(cond)) {                                       \
+            nnk_set_error(hipErrorInvalidValue, __VA_ARGS__);\
+            return ret;                                      \
+        }                                                    \
+    } while (0)

@@ -5,6 +5,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "nn_hip_rt.h"
 #include "nnk_common.h"
 
@@ -64,9 +66,52 @@ void nnk_after_launch(const char* what, hipStream_t s) {
     if (e != hipSuccess) nnk_set_error((int)e, "%s: %s", what, hipGetErrorString(e));
 }
 
+// The launchers' stream-ordered scratch comes from a memory pool the library
+// owns, one per device, whose release threshold keeps freed blocks cached:
+// with the default threshold (0) every free hands the memory back at the next
+// synchronisation and the next allocation maps it again, which costs more
+// than the small kernels that use it.  The process's default pool is left as
+// it is.
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_pool_mu;
+hipMemPool_t g_pools[kMaxDevices] = {};
+
+hipMemPool_t scratch_pool(hipStream_t s, const char* what) {
+    int dev = -1;
+    hipError_t e = s ? hipStreamGetDevice(s, &dev) : hipGetDevice(&dev);
+    if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        nnk_set_error(e != hipSuccess ? (int)e : (int)hipErrorInvalidDevice, "%s: no device for the stream", what);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_pool_mu);
+    if (!g_pools[dev]) {
+        hipMemPoolProps props = {};
+        props.allocType = hipMemAllocationTypePinned;
+        props.location.type = hipMemLocationTypeDevice;
+        props.location.id = dev;
+        hipMemPool_t pool = nullptr;
+        e = hipMemPoolCreate(&pool, &props);
+        if (e == hipSuccess) {
+            uint64_t keep = UINT64_MAX;
+            e = hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
+            if (e != hipSuccess) (void)hipMemPoolDestroy(pool);
+        }
+        if (e != hipSuccess) {
+            nnk_set_error((int)e, "%s: scratch pool on device %d: %s", what, dev, hipGetErrorString(e));
+            return nullptr;
+        }
+        g_pools[dev] = pool;
+    }
+    return g_pools[dev];
+}
+}  // namespace
+
 float* nnk_scratch_acquire(size_t n_floats, hipStream_t s, const char* what) {
+    hipMemPool_t pool = scratch_pool(s, what);
+    if (!pool) return nullptr;
     void* p = nullptr;
-    hipError_t e = hipMallocAsync(&p, n_floats * sizeof(float) + 256, s);
+    hipError_t e = hipMallocFromPoolAsync(&p, n_floats * sizeof(float) + 256, pool, s);
     if (e != hipSuccess) {
         nnk_set_error((int)e, "%s: scratch of %zu floats: %s", what, n_floats, hipGetErrorString(e));
         return nullptr;
@@ -76,6 +121,11 @@ float* nnk_scratch_acquire(size_t n_floats, hipStream_t s, const char* what) {
 
 void nnk_scratch_release(float* p, hipStream_t s) {
     if (p) (void)hipFreeAsync(p, s);
+}
+
+__global__ __launch_bounds__(256) void fill_f32_kernel(float* __restrict__ p, float value, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        p[i] = value;
 }
 
 // ---------------------------------------------------------------------------
@@ -180,6 +230,14 @@ float nnhip_event_elapsed_ms(hipEvent_t start, hipEvent_t stop) {
     float ms = -1.0f;
     if (hipEventElapsedTime(&ms, start, stop) != hipSuccess) return -1.0f;
     return ms;
+}
+
+void nnhip_fill_f32(float* p, float value, size_t n, hipStream_t s) {
+    if (n == 0) return;
+    NNK_REQUIRE(p, "fill", "nnhip_fill_f32: null pointer");
+    const size_t blocks = (n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096;
+    fill_f32_kernel<<<dim3((unsigned)blocks), dim3(256), 0, s>>>(p, value, n);
+    nnk_after_launch("nnhip_fill_f32", s);
 }
 
 void nnhip_copy_f32(float* dst, const float* src, size_t n, hipStream_t s) {

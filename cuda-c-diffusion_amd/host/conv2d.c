@@ -14,6 +14,7 @@ typedef struct {
     float *Wt, *gW;
     float *b, *gb;
     float *gain, *g_gain;
+    float* wn_ws;  /* weight-norm backward workspace (mp mode; zero-filled at create) */
     float* col;
 } Conv2DState;
 
@@ -47,9 +48,9 @@ static void conv2d_backward(Module* self, const float* in, const float* out,
         st->Ho, st->Wo, ctx->stream);
     nn_gemm_dW(ctx->blas, 1.0f, st->col, grad_out, st->gW, M, Kg, st->C_out);
     if (st->mp_mode) {
-        NN_HIP_CHECK(hipMemsetAsync(st->g_gain, 0, sizeof(float), ctx->stream));
-        launch_weight_normalize_backward(st->gW, st->Wt, st->gain, st->g_gain, Kg, st->C_out,
-            ctx->stream);
+        nnhip_fill_f32(st->g_gain, 0.0f, 1, ctx->stream);
+        launch_weight_normalize_backward_ws(st->gW, st->Wt, st->gain, st->g_gain, Kg, st->C_out,
+            st->wn_ws, ctx->stream);
         nn_gemm_dX(ctx->blas, 1.0f, st->Wt, grad_out, st->col, M, Kg, st->C_out);
         launch_scale_by_scalar(st->col, st->gain, M * Kg, ctx->stream);
     } else {
@@ -77,6 +78,7 @@ static void conv2d_free(Module* self)
     if (st->mp_mode) {
         (void)hipFree(st->gain);
         (void)hipFree(st->g_gain);
+        (void)hipFree(st->wn_ws);
     } else {
         (void)hipFree(st->b);
         (void)hipFree(st->gb);
@@ -111,11 +113,15 @@ Module* conv2d_create(Context* ctx, int C_in, int C_out, int K, int stride, int 
         st->gb = NULL;
         st->gain = nn_device_alloc(1);
         st->g_gain = nn_device_alloc(1);
+        const size_t n = nnhip_weight_normalize_backward_workspace(C_out);
+        st->wn_ws = nn_device_alloc(n);
+        NN_HIP_CHECK(hipMemset(st->wn_ws, 0, (n ? n : 1) * sizeof(float)));
         nn_fill_normal(ctx, st->Wt, (size_t)Kg * C_out, 0.0f, 1.0f);
         NN_HIP_CHECK(hipMemcpy(st->gain, &gain, sizeof(float), hipMemcpyHostToDevice));
     } else {
         st->gain = NULL;
         st->g_gain = NULL;
+        st->wn_ws = NULL;
         st->b = nn_device_alloc((size_t)C_out);
         st->gb = nn_device_alloc((size_t)C_out);
         nn_fill_normal(ctx, st->Wt, (size_t)Kg * C_out, 0.0f, sqrtf(2.0f / (float)Kg));

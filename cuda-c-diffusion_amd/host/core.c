@@ -105,8 +105,7 @@ void ctx_zero_cond_grad(Context* ctx, int batch) /* src/nn.h:97-103 */
 {
     for (int i = 0; i < ctx->n_cond; ++i)
         if (ctx->cond[i].grad)
-            NN_HIP_CHECK(hipMemsetAsync(ctx->cond[i].grad, 0,
-                (size_t)batch * ctx->cond[i].dim * sizeof(float), ctx->stream));
+            nnhip_fill_f32(ctx->cond[i].grad, 0.0f, (size_t)batch * ctx->cond[i].dim, ctx->stream);
 }
 
 void ctx_free_cond(Context* ctx)

@@ -8,6 +8,7 @@ typedef struct {
     float eps;
     float *W, *gW;
     float *gain, *g_gain;
+    float* wn_ws;  /* weight-norm backward workspace (zero-filled at create) */
 } MPLinearState;
 
 static void mp_linear_forward(Module* self, const float* in, float* out, int batch, Context* ctx)
@@ -24,9 +25,9 @@ static void mp_linear_backward(Module* self, const float* in, const float* out,
     (void)out;
     MPLinearState* st = (MPLinearState*)self->state;
     nn_gemm_dW(ctx->blas, 1.0f, in, grad_out, st->gW, batch, st->in, st->out);
-    NN_HIP_CHECK(hipMemsetAsync(st->g_gain, 0, sizeof(float), ctx->stream));
-    launch_weight_normalize_backward(st->gW, st->W, st->gain, st->g_gain, st->in, st->out,
-        ctx->stream);
+    nnhip_fill_f32(st->g_gain, 0.0f, 1, ctx->stream);
+    launch_weight_normalize_backward_ws(st->gW, st->W, st->gain, st->g_gain, st->in, st->out,
+        st->wn_ws, ctx->stream);
     if (grad_in) {
         nn_gemm_dX(ctx->blas, 1.0f, st->W, grad_out, grad_in, batch, st->in, st->out);
         launch_scale_by_scalar(grad_in, st->gain, batch * st->in, ctx->stream);
@@ -47,6 +48,7 @@ static void mp_linear_free(Module* self)
     (void)hipFree(st->gW);
     (void)hipFree(st->gain);
     (void)hipFree(st->g_gain);
+    (void)hipFree(st->wn_ws);
     free(st);
     free(self);
 }
@@ -62,6 +64,11 @@ Module* mp_linear_create(Context* ctx, int in_dim, int out_dim, float gain_init)
     st->gW = nn_device_alloc((size_t)in_dim * out_dim);
     st->gain = nn_device_alloc(1);
     st->g_gain = nn_device_alloc(1);
+    {
+        const size_t n = nnhip_weight_normalize_backward_workspace(out_dim);
+        st->wn_ws = nn_device_alloc(n);
+        NN_HIP_CHECK(hipMemset(st->wn_ws, 0, (n ? n : 1) * sizeof(float)));
+    }
     nn_fill_normal(ctx, st->W, (size_t)in_dim * out_dim, 0.0f, 1.0f);
     NN_HIP_CHECK(hipMemcpy(st->gain, &gain_init, sizeof(float), hipMemcpyHostToDevice));
     m->name = "mp_linear";

@@ -91,6 +91,15 @@ void launch_weight_normalize(float* W, int in, int out, float eps, hipStream_t s
 void launch_weight_normalize_backward(float* gW, const float* Wn, const float* gain,
     float* g_gain, int in, int out, hipStream_t s);
 
+/* Workspace variant of launch_weight_normalize_backward (no counterpart in
+   the reference): identical results, one launch and no pool allocation.  The
+   caller lends `workspace` of nnhip_weight_normalize_backward_workspace(out)
+   floats, zero-filled before its first use; every launch leaves it re-armed.
+   Launches that may run concurrently need separate workspaces. */
+size_t nnhip_weight_normalize_backward_workspace(int out);
+void launch_weight_normalize_backward_ws(float* gW, const float* Wn, const float* gain,
+    float* g_gain, int in, int out, float* workspace, hipStream_t s);
+
 /* x[i] *= s[0] (device-resident scalar).  replaces nn.h:377 / kernels.cu:300-306,346-351 */
 void launch_scale_by_scalar(float* x, const float* s, int n, hipStream_t st);
 

@@ -37,6 +37,10 @@ int nnhip_memcpy_dtoh(void* dst, const void* src, size_t bytes);
 int nnhip_memcpy_dtod(void* dst, const void* src, size_t bytes);
 int nnhip_memset(void* dst, int value, size_t bytes);
 int nnhip_memset_async(void* dst, int value, size_t bytes, hipStream_t s);
+/* p[i] = value for n floats, by a kernel on stream s (so it is also safe
+   inside a captured graph, unlike a memset node).  Errors are recorded in the
+   launch layer's error record. */
+void nnhip_fill_f32(float* p, float value, size_t n, hipStream_t s);
 int nnhip_device_synchronize(void);
 
 /* ---- streams and events ---- */

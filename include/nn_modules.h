@@ -22,6 +22,7 @@
 #include <rocblas/rocblas.h>
 
 #include "nn_hip.h"
+#include "nn_hip_rt.h"
 
 #ifdef __cplusplus
 extern "C" {

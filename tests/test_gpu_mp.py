@@ -97,3 +97,45 @@ def test_mp_linear_weight_chain(L, orc, rng):
     gW_ref, gg_ref = orc.weight_normalize_backward(M, Wn_ref, 1.0, 0.0)
     assert rel_err(gWd.download(shape=M.shape), gW_ref) <= TOL
     assert abs(float(gg.download()[0]) - gg_ref) <= TOL * max(abs(gg_ref), float(np.sqrt(n_in * n_out)))
+
+
+@pytest.mark.parametrize("n_in,n_out", [(1152, 128), (12, 8), (4, 6), (300, 1000), (1, 1)])
+def test_weight_normalize_backward_workspace_matches(L, orc, rng, n_in, n_out):
+    """The lent-workspace backward (one launch; the gain-gradient sum is done
+    by the last workgroup to finish) against the pool launcher and the oracle,
+    on two calls in a row through the same workspace, the second smaller: the
+    completion counter must re-arm itself."""
+    print(f"[case] weight_normalize_backward_ws {n_in}x{n_out}", flush=True)
+    ws = L.alloc(int(L.nnhip_weight_normalize_backward_workspace(n_out)))
+    ws.fill_bytes(0)
+    for k, (ni, no) in enumerate([(n_in, n_out), (max(1, n_in // 2), max(1, n_out // 3))]):
+        W = rng.standard_normal((ni, no)).astype(np.float32)
+        Wn = orc.weight_normalize(W, 1e-4)
+        M = rng.standard_normal((ni, no)).astype(np.float32)
+        gain = np.array([0.7 + k], np.float32)
+        Wnd, gaind = L.to_device(Wn), L.to_device(gain)
+        gA, gB = L.to_device(M), L.to_device(M)
+        ggA, ggB = L.to_device(np.array([0.25], np.float32)), L.to_device(np.array([0.25], np.float32))
+        L.launch_weight_normalize_backward(gA.p, Wnd.p, gaind.p, ggA.p, ni, no, None)
+        L.launch_weight_normalize_backward_ws(gB.p, Wnd.p, gaind.p, ggB.p, ni, no, ws.p, None)
+        L.sync()
+        # same fixed-order arithmetic as the pool launcher: identical bits
+        assert_bits_equal(gB.download(shape=M.shape), gA.download(shape=M.shape), "gW ws vs pool")
+        assert_bits_equal(ggB.download(), ggA.download(), "g_gain ws vs pool")
+        gW_ref, gg_ref = orc.weight_normalize_backward(M, Wn, float(gain[0]), 0.25)
+        assert rel_err(gB.download(shape=M.shape), gW_ref) <= TOL
+        terms = Wn.astype(np.float64) * M
+        floor = float(np.sqrt(np.sum(terms ** 2)) + 0.25)
+        assert abs(float(ggB.download()[0]) - gg_ref) / max(abs(gg_ref), floor) <= TOL
+
+
+def test_fill_f32(L):
+    buf = L.alloc(100003)
+    buf.fill_bytes(0xFF)
+    L.nnhip_fill_f32(buf.p, 0.0, 100001, None)
+    L.sync()
+    got = buf.download()
+    assert np.all(got[:100001] == 0.0) and np.isnan(got[100001:]).all()
+    L.nnhip_fill_f32(buf.p, 2.5, 7, None)
+    L.sync()
+    assert np.all(buf.download()[:7] == 2.5) and buf.download()[7] == 0.0
