@@ -14,10 +14,12 @@
 //
 //   tile       = TP pixel rows x CW4 float4 columns (a column block) of one
 //                sample; it covers GT = CW4 / (cpg/4) whole groups.
-//   grid       = P persistent workgroups (cooperative launch: all resident),
-//                P a multiple of the tiles per sample, so workgroup w always
-//                owns the same (column block, pixel tile) position and walks
-//                the samples; tile i = round * P + w.
+//   grid       = P persistent workgroups (as many as the device holds at
+//                once), P a multiple of the tiles per sample, so workgroup w
+//                always owns the same (column block, pixel tile) position and
+//                walks the samples; tile i = round * P + w.  The T workgroups
+//                that own the tiles of one (sample, column block) are
+//                consecutive: a team.
 //   round r    : take tile i from the LDS stage into registers and start the
 //                direct-to-LDS loads of tile i+P into the stage;
 //                phase A on tile i (registers): per-group partial statistics
@@ -38,15 +40,30 @@
 // read with agent-scope atomic 64-bit accesses, so a reader accepts exactly
 // this launch's values and needs no fence or counter.  Every wait is bounded:
 // past `spin_limit` polls the workgroup flags an error in the workspace and
-// stops waiting (the kernel always terminates).  Deadlock freedom: waits go
-// only to tiles of earlier rounds or of the current round's phase A, which no
-// workgroup skips, and cooperative launch makes all P workgroups resident.
+// stops waiting (the kernel always terminates).
+//
+// Progress without a residency guarantee (plain launch).  A workgroup waits
+// only for records of its own team, of the current or an earlier round, and
+// never for anything else.  Workgroups are dispatched in index order on each
+// XCD, so the resident workgroups of each XCD are a prefix of its share of
+// the grid minus those already finished; the lowest unfinished team's members
+// are therefore resident or next in line on every XCD, and what holds the
+// slots they wait for either belongs to that team or is other work that ends
+// by itself.  That team completes, and by induction so does the grid.  On an
+// idle device all P workgroups are resident from the start.  Two streaming
+// launches running concurrently on different streams could each hold slots the
+// other's lowest team needs; the bounded wait then flags the error instead of
+// hanging, and NNHIP_GN_COOPERATIVE=1 selects cooperative launches (all P
+// resident by contract, at ~20 us more per launch) for such callers.
 //
 // Forward statistics are Chan et al.'s parallel mean/M2 merges of two-pass
 // per-thread values (more accurate than the reference's E[x^2]-mu^2).  The
 // backward sums S1 = sum g, S2 = sum g*xhat (g = dy*act'(h)*gamma) per group and
-// accumulates the dgamma/dbeta partials per lane across the workgroup's tiles;
-// a final fixed-order reduce over workgroups gives dgamma/dbeta.
+// accumulates the dgamma/dbeta partials per lane across the workgroup's tiles.
+// dgamma/dbeta then need no wait either: the last workgroup of a team to
+// arrive (an arrival counter) adds the team's partials in member order, and
+// the last team to finish adds the team totals in team order; arrival order
+// decides who adds, never the order of the additions.
 #pragma once
 
 #include "nnk_common.h"
@@ -173,11 +190,21 @@ struct Shape {
     float inv_n;       // 1 / (HW * cpg)
 };
 
-// Workspace layout (device): [err u32 (padded to 256 B)] [records u64] [channel partials u64].
+// Workspace layout (device), byte offsets:
+//   0      err u32 (sticky wait-timeout flag)
+//   256    arrival counters u32: [0] teams done, [1 + team] members done;
+//          zero between launches (each launch re-arms what it counted)
+//   8192   records u64, then (backward) the dgamma/dbeta partials.
+// The header has a fixed size, so a workspace lent for one shape and then
+// another never finds a counter where records were.
+constexpr size_t kHeaderBytes = 8192;
+constexpr size_t kCountOffset = 256;
 struct Work {
     unsigned* err;
+    unsigned* count;
     unsigned long long* rec;   // ntiles * GT * 2, [sample, column block][group][value][pixel tile]
-    unsigned long long* cpart; // bwd: P * 2 * (4 * CW4) epoch-tagged dgamma/dbeta partials
+    unsigned long long* part;  // bwd: [P][2][4 * CW4] per-workgroup dgamma/dbeta partials (tagged)
+    unsigned long long* tpart; // bwd: [P / T][2][4 * CW4] per-team sums (tagged)
 };
 
 // Lanes that share this lane's group inside a wave: xor over the column bits
@@ -663,66 +690,80 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
         for (int j = 0; j < 8; ++j) cred[wid][lane][j] = c8[j];
     }
     __syncthreads();
-    // publish: cpart[w][0 = dgamma, 1 = dbeta][channel within the column block]
-    for (int i = tid; i < CW4 * 8; i += TPB) {
+    // part[w][0 = dgamma, 1 = dbeta][channel within the column block], as
+    // epoch-tagged records: the adders below accept exactly this launch's
+    // values, so no fence orders them before the arrival count (an agent-scope
+    // fence writes back the whole L2, which costs more than the wait).
+    constexpr int NVAL = CW4 * 8;  // values per workgroup
+    static_assert(TPB % NVAL == 0 && TPB / NVAL * NVAL <= NW * CW4 * 8, "team-sum layout");
+    for (int i = tid; i < NVAL; i += TPB) {
         const int cl = i / 8, j = i % 8;
         float acc = cred[0][cl][j];
 #pragma unroll
         for (int ww = 1; ww < NW; ++ww) acc += cred[ww][cl][j];
-        rec_store(wk.cpart + ((size_t)w * 2 + (j >> 2)) * (CW4 * 4) + cl * 4 + (j & 3), tagged(tag, acc));
+        rec_store(wk.part + (size_t)w * NVAL + (j >> 2) * (CW4 * 4) + cl * 4 + (j & 3), tagged(tag, acc));
     }
+    __shared__ unsigned arrived;
+    const int team = w / T;
+    __syncthreads();
+    if (tid == 0) arrived = __hip_atomic_fetch_add(wk.count + 1 + team, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (arrived != (unsigned)T - 1) return;
 
-    // dgamma/dbeta: workgroup w reduces the 64-channel chunks j = w, w + P, ...
-    // Lane l of wave v sums channel 64 j + l over the owners m = v, v + NW, ...
-    // of its column block (owner m = workgroup ((m / T) NCB + cb) T + m % T) in
-    // ascending m, eight partials in flight at a time; the NW wave sums are
-    // then added in wave order.  Every partial is waited for (bounded).
-    const int nred = (sh.C + kWave - 1) / kWave;
-    const int owners = P / NCB;
-    constexpr int kBatch = 8;
-    static_assert(2 * NW * kWave <= NW * CW4 * 8, "reducer sums fit the partials buffer");
-    float(*rsum)[NW][kWave] = reinterpret_cast<float(*)[NW][kWave]>(&cred[0][0][0]);
-    __syncthreads();  // the publish loop's reads of cred are done
-    for (int j = w; j < nred; j += P) {
-        const int c = j * kWave + lane;
-        float sg = 0.0f, sb = 0.0f;
-        if (c < sh.C) {
-            const int cbc = c / (CW4 * 4), cl = c % (CW4 * 4);
-            for (int m0 = wid; m0 < owners; m0 += NW * kBatch) {
-                unsigned long long vg[kBatch], vb[kBatch];
-                const unsigned long long* pg[kBatch];
+    // Last member of the team: add the T partials in member order (Q
+    // interleaved chains, then the chains in order).  Every partial was
+    // stored before its workgroup arrived, so each wait is short.
+    constexpr int Q = TPB / NVAL;
+    float(*chain)[NVAL] = reinterpret_cast<float(*)[NVAL]>(&cred[0][0][0]);
+    {
+        const int v = tid % NVAL, q = tid / NVAL;
+        const unsigned long long* src = wk.part + (size_t)team * T * NVAL + v;
+        float acc = 0.0f;
+        int m = q;
+        constexpr int kBatch = 8;
+        for (; m + (kBatch - 1) * Q < T; m += kBatch * Q) {
+            unsigned long long r8[kBatch];
 #pragma unroll
-                for (int u = 0; u < kBatch; ++u) {
-                    const int m = m0 + u * NW < owners ? m0 + u * NW : m0;
-                    const int wo = ((m / T) * NCB + cbc) * T + (m % T);
-                    pg[u] = wk.cpart + ((size_t)wo * 2) * (CW4 * 4) + cl;
-                    vg[u] = rec_load(pg[u]);
-                    vb[u] = rec_load(pg[u] + CW4 * 4);
-                }
+            for (int u = 0; u < kBatch; ++u) r8[u] = rec_load(src + (size_t)(m + u * Q) * NVAL);
 #pragma unroll
-                for (int u = 0; u < kBatch; ++u) {
-                    if (m0 + u * NW < owners) {
-                        sg += rec_wait(pg[u], vg[u], epoch, spin_limit, wk.err);
-                        sb += rec_wait(pg[u] + CW4 * 4, vb[u], epoch, spin_limit, wk.err);
-                    }
-                }
-            }
+            for (int u = 0; u < kBatch; ++u)
+                acc += rec_wait(src + (size_t)(m + u * Q) * NVAL, r8[u], epoch, spin_limit, wk.err);
         }
-        rsum[0][wid][lane] = sg;
-        rsum[1][wid][lane] = sb;
-        __syncthreads();
-        if (wid == 0 && c < sh.C) {
-            float ag = rsum[0][0][lane], ab = rsum[1][0][lane];
-#pragma unroll
-            for (int v = 1; v < NW; ++v) {
-                ag += rsum[0][v][lane];
-                ab += rsum[1][v][lane];
-            }
-            ggamma[c] = ag;
-            gbeta[c] = ab;
+        for (; m < T; m += Q) {
+            const unsigned long long* p = src + (size_t)m * NVAL;
+            acc += rec_wait(p, rec_load(p), epoch, spin_limit, wk.err);
         }
-        __syncthreads();
+        chain[q][v] = acc;
     }
+    __syncthreads();
+    for (int v = tid; v < NVAL; v += TPB) {
+        float acc = chain[0][v];
+#pragma unroll
+        for (int q = 1; q < Q; ++q) acc += chain[q][v];
+        rec_store(wk.tpart + (size_t)team * NVAL + v, tagged(tag, acc));
+    }
+    __syncthreads();
+    if (tid == 0) {
+        __hip_atomic_store(wk.count + 1 + team, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // re-arm
+        arrived = __hip_atomic_fetch_add(wk.count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    const int nteams = P / T;
+    if (arrived != (unsigned)nteams - 1) return;
+
+    // Last team: dgamma/dbeta of channel c = the sums of the teams of its
+    // column block (team k owns column block k mod NCB), in team order.
+    for (int i = tid; i < 2 * sh.C; i += TPB) {
+        const int d = i / sh.C, c = i % sh.C;
+        const int cbc = c / (CW4 * 4), cl = c % (CW4 * 4);
+        float acc = 0.0f;
+        for (int k = cbc; k < nteams; k += NCB) {
+            const unsigned long long* p = wk.tpart + (size_t)k * NVAL + d * (CW4 * 4) + cl;
+            acc += rec_wait(p, rec_load(p), epoch, spin_limit, wk.err);
+        }
+        (d ? gbeta : ggamma)[c] = acc;
+    }
+    if (tid == 0) __hip_atomic_store(wk.count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace gns
@@ -742,15 +783,19 @@ constexpr int kCw4 = 32;
 constexpr int kFwdTp = 128;
 constexpr int kBwdTp = 64;
 constexpr int kMaxGrid = 1024;        // persistent workgroups at most
-constexpr unsigned kSpinLimit = 1u << 16;
+// Polls of one record before a wait gives up (each poll sleeps and reloads,
+// ~1 us): far beyond any wait of a correct launch, which is bounded by the
+// run time of the grid itself.
+constexpr unsigned kSpinLimit = 1u << 20;
 
 struct Plan {
     bool ok;
     int cpg4, rpl;
     Shape sh;
-    size_t ws_floats;   // workspace needed (err + records [+ channel partials])
+    size_t ws_floats;   // workspace needed (header + records [+ partials])
     size_t rec_offset;  // in bytes from the workspace start
-    size_t cpart_offset;
+    size_t part_offset;
+    size_t tpart_offset;
 };
 
 // Applicability and sizes; `bwd` selects the backward geometry.
@@ -762,7 +807,8 @@ unsigned next_epoch();
 // Launch the streaming kernels when the shape fits and the device can hold
 // the persistent grid; return false (nothing launched) otherwise.  `ws` is a
 // device workspace of at least plan.ws_floats floats whose records region
-// never holds this launch's epoch (the launchers clear it first).
+// never holds this launch's epoch and whose counters are zero (a zero-filled
+// workspace, only ever used by these launchers, is both).
 bool nnk_gns_forward(int act, float* y, float* mu, float* rstd, const float* x, const float* gamma,
     const float* beta, int B, int HW, int C, int G, float eps, float* ws, hipStream_t s);
 bool nnk_gns_backward(int act, float* dx, float* ggamma, float* gbeta, const float* dy, const float* x,

@@ -1,6 +1,8 @@
 // k_gns.hip -- host side shared by the streaming GroupNorm launchers
 // (k_gns_fwd.hip, k_gns_bwd.hip): shape plan, launch epochs, workspace clear
 // and the persistent grid size.
+#include <stdlib.h>
+
 #include <atomic>
 
 #include "gn_stream.h"
@@ -46,11 +48,16 @@ Plan make_plan(bool bwd, int B, int HW, int C, int G) {
     p.sh.ntiles = B * NCB * T;
     p.sh.sample_bytes = (uint32_t)((long long)HW * C * 4);
     p.sh.inv_n = 1.0f / (float)((long long)HW * cpg);
-    p.rec_offset = 256;
+    static_assert(kCountOffset + (kMaxGrid + 1) * sizeof(unsigned) <= kHeaderBytes, "counters fit the header");
+    p.rec_offset = kHeaderBytes;
     const size_t rec_bytes = (size_t)p.sh.ntiles * GT * 2 * sizeof(unsigned long long);
-    p.cpart_offset = p.rec_offset + rec_bytes;
-    const size_t cpart_bytes = bwd ? (size_t)kMaxGrid * 2 * (4 * kCw4) * sizeof(unsigned long long) : 0;
-    p.ws_floats = (p.cpart_offset + cpart_bytes + sizeof(float) - 1) / sizeof(float);
+    // backward partials: one [2][4 * kCw4] block per workgroup and per team
+    const size_t nval_bytes = (size_t)2 * (4 * kCw4) * sizeof(unsigned long long);
+    p.part_offset = p.rec_offset + rec_bytes;
+    const size_t part_bytes = bwd ? (size_t)kMaxGrid * nval_bytes : 0;
+    p.tpart_offset = p.part_offset + part_bytes;
+    const size_t tpart_bytes = bwd ? (size_t)((kMaxGrid + T - 1) / T) * nval_bytes : 0;
+    p.ws_floats = (p.tpart_offset + tpart_bytes + sizeof(float) - 1) / sizeof(float);
     p.ok = true;
     return p;
 }
@@ -79,6 +86,24 @@ void nnk_gns_clear_workspace(float* ws, size_t n_floats, hipStream_t s) {
     if (n_floats == 0) return;
     const size_t blocks = (n_floats + 255) / 256 < 4096 ? (n_floats + 255) / 256 : 4096;
     gns_clear<<<dim3((unsigned)blocks), dim3(256), 0, s>>>(reinterpret_cast<unsigned*>(ws), n_floats);
+}
+
+// Launch a persistent grid: a plain launch (its progress does not depend on
+// residency; see gn_stream.h), or a cooperative one with
+// NNHIP_GN_COOPERATIVE=1 for callers that run streaming GroupNorms
+// concurrently on several streams.
+bool nnk_gns_launch(const void* fn, int P, void** args, hipStream_t s, const char* what) {
+    const char* e = getenv("NNHIP_GN_COOPERATIVE");
+    const bool coop = e && e[0] == '1';
+    const hipError_t r = coop ? hipLaunchCooperativeKernel(fn, dim3((unsigned)P), dim3(nnk::gns::kTpb), args, 0, s)
+                              : hipLaunchKernel(fn, dim3((unsigned)P), dim3(nnk::gns::kTpb), args, 0, s);
+    if (r != hipSuccess) {
+        (void)hipGetLastError();
+        nnk_path_note("%s: %s launch of %d x %d: %s", what, coop ? "cooperative" : "plain", P, nnk::gns::kTpb,
+            hipGetErrorString(r));
+        return false;
+    }
+    return true;
 }
 
 // Persistent grid size for a kernel: resident workgroups of the device

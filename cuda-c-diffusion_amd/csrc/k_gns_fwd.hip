@@ -3,6 +3,7 @@
 #include "gn_stream.h"
 
 int nnk_gns_grid(const void* fn, int key, size_t lds, int unit);
+bool nnk_gns_launch(const void* fn, int P, void** args, hipStream_t s, const char* what);
 
 namespace {
 
@@ -21,20 +22,15 @@ bool launch(const Plan& p, float* y, float* mu, float* rstd, const float* x, con
     Shape sh = p.sh;
     Work wk;
     wk.err = reinterpret_cast<unsigned*>(ws);
+    wk.count = reinterpret_cast<unsigned*>(reinterpret_cast<char*>(ws) + kCountOffset);
     wk.rec = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(ws) + p.rec_offset);
-    wk.cpart = nullptr;
+    wk.part = nullptr;
+    wk.tpart = nullptr;
     unsigned epoch = next_epoch();
     unsigned limit = kSpinLimit;
     void* args[] = {&y, &mu, &rstd, const_cast<float**>(&x), const_cast<float**>(&gamma),
         const_cast<float**>(&beta), &sh, &wk, &eps, &epoch, &limit};
-    const hipError_t e = hipLaunchCooperativeKernel(fn, dim3((unsigned)P), dim3(kTpb), args, (unsigned)lds, s);
-    if (e != hipSuccess) {
-        (void)hipGetLastError();
-        nnk_path_note("streaming GroupNorm forward: cooperative launch of %d x %d: %s", P, kTpb,
-            hipGetErrorString(e));
-        return false;
-    }
-    return true;
+    return nnk_gns_launch(fn, P, args, s, "streaming GroupNorm forward");
 }
 
 template <int ACT>

@@ -236,10 +236,10 @@ bool shape_ok(const char* what, int B, int HW, int C, int G) {
 // alternative is the two-pass generic kernel).
 enum class GnPath { kAuto, kStream, kReg };
 
-// A lent workspace starts with a 256-byte header whose first word is the
-// streaming kernels' wait-timeout flag (set, never cleared, by them); the
-// other paths keep their data after the header.
-constexpr size_t kWsHeader = 64;
+// A lent workspace starts with the streaming kernels' fixed-size header (its
+// first word is their wait-timeout flag, set and never cleared by them; then
+// their arrival counters); the other paths keep their data after it.
+constexpr size_t kWsHeader = nnk::gns::kHeaderBytes / sizeof(float);
 constexpr long long kStreamMinElems = 1LL << 22;
 
 GnPath gn_path() {  // read per launch, so a process can switch paths

@@ -66,32 +66,39 @@ void nnk_after_launch(const char* what, hipStream_t s) {
     if (e != hipSuccess) nnk_set_error((int)e, "%s: %s", what, hipGetErrorString(e));
 }
 
-// The launchers' stream-ordered scratch comes from a memory pool the library
-// owns, one per device, whose release threshold keeps freed blocks cached:
-// with the default threshold (0) every free hands the memory back at the next
-// synchronisation and the next allocation maps it again, which costs more
-// than the small kernels that use it.  The process's default pool is left as
-// it is.
+// Scratch for launchers whose reference signature has no workspace argument.
+// Each (device, stream) keeps one cached block: work on one stream runs in
+// order, so the next launch on the stream may reuse the block the previous
+// one used.  A larger request replaces the block (the old one is freed in
+// stream order, after its last use); a request that finds the stream's block
+// in use (another host thread on the same stream) takes a block of its own.
+// Blocks come from a memory pool the library owns, one per device, whose
+// release threshold keeps freed memory cached; the process's default pool is
+// left as it is.  Cached blocks are held until the process ends.
 namespace {
 constexpr int kMaxDevices = 64;
-std::mutex g_pool_mu;
+std::mutex g_scratch_mu;
 hipMemPool_t g_pools[kMaxDevices] = {};
 
-hipMemPool_t scratch_pool(hipStream_t s, const char* what) {
-    int dev = -1;
-    hipError_t e = s ? hipStreamGetDevice(s, &dev) : hipGetDevice(&dev);
-    if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
-        nnk_set_error(e != hipSuccess ? (int)e : (int)hipErrorInvalidDevice, "%s: no device for the stream", what);
-        return nullptr;
-    }
-    std::lock_guard<std::mutex> lock(g_pool_mu);
+struct Slot {
+    int dev;
+    hipStream_t stream;
+    void* p;
+    size_t bytes;
+    bool busy;
+};
+Slot g_slots[256];
+int g_nslots = 0;
+
+// Caller holds g_scratch_mu.
+hipMemPool_t scratch_pool(int dev, const char* what) {
     if (!g_pools[dev]) {
         hipMemPoolProps props = {};
         props.allocType = hipMemAllocationTypePinned;
         props.location.type = hipMemLocationTypeDevice;
         props.location.id = dev;
         hipMemPool_t pool = nullptr;
-        e = hipMemPoolCreate(&pool, &props);
+        hipError_t e = hipMemPoolCreate(&pool, &props);
         if (e == hipSuccess) {
             uint64_t keep = UINT64_MAX;
             e = hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
@@ -105,22 +112,60 @@ hipMemPool_t scratch_pool(hipStream_t s, const char* what) {
     }
     return g_pools[dev];
 }
+
+void* pool_alloc(hipMemPool_t pool, size_t bytes, hipStream_t s, const char* what) {
+    void* p = nullptr;
+    const hipError_t e = hipMallocFromPoolAsync(&p, bytes, pool, s);
+    if (e != hipSuccess) {
+        nnk_set_error((int)e, "%s: scratch of %zu bytes: %s", what, bytes, hipGetErrorString(e));
+        return nullptr;
+    }
+    return p;
+}
 }  // namespace
 
 float* nnk_scratch_acquire(size_t n_floats, hipStream_t s, const char* what) {
-    hipMemPool_t pool = scratch_pool(s, what);
-    if (!pool) return nullptr;
-    void* p = nullptr;
-    hipError_t e = hipMallocFromPoolAsync(&p, n_floats * sizeof(float) + 256, pool, s);
-    if (e != hipSuccess) {
-        nnk_set_error((int)e, "%s: scratch of %zu floats: %s", what, n_floats, hipGetErrorString(e));
+    int dev = -1;
+    const hipError_t ed = s ? hipStreamGetDevice(s, &dev) : hipGetDevice(&dev);
+    if (ed != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        nnk_set_error(ed != hipSuccess ? (int)ed : (int)hipErrorInvalidDevice, "%s: no device for the stream", what);
         return nullptr;
     }
-    return static_cast<float*>(p);
+    size_t need = n_floats * sizeof(float) + 256;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    hipMemPool_t pool = scratch_pool(dev, what);
+    if (!pool) return nullptr;
+    Slot* slot = nullptr;
+    for (int i = 0; i < g_nslots; ++i)
+        if (g_slots[i].dev == dev && g_slots[i].stream == s) slot = &g_slots[i];
+    if (!slot && g_nslots < (int)(sizeof g_slots / sizeof g_slots[0])) {
+        slot = &g_slots[g_nslots++];
+        *slot = Slot{dev, s, nullptr, 0, false};
+    }
+    if (!slot || slot->busy) return static_cast<float*>(pool_alloc(pool, need, s, what));
+    if (slot->bytes < need) {
+        size_t bytes = 1 << 16;
+        while (bytes < need) bytes <<= 1;
+        void* p = pool_alloc(pool, bytes, s, what);
+        if (!p) return nullptr;
+        if (slot->p) (void)hipFreeAsync(slot->p, s);
+        slot->p = p;
+        slot->bytes = bytes;
+    }
+    slot->busy = true;
+    return static_cast<float*>(slot->p);
 }
 
 void nnk_scratch_release(float* p, hipStream_t s) {
-    if (p) (void)hipFreeAsync(p, s);
+    if (!p) return;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    for (int i = 0; i < g_nslots; ++i) {
+        if (g_slots[i].p == p && g_slots[i].stream == s && g_slots[i].busy) {
+            g_slots[i].busy = false;
+            return;
+        }
+    }
+    (void)hipFreeAsync(p, s);  // a block of its own
 }
 
 __global__ __launch_bounds__(256) void fill_f32_kernel(float* __restrict__ p, float value, size_t n) {

@@ -53,12 +53,22 @@ def tiles(L, B, HW, C, G, tp):
     return True, B * (C // COLS) * T * gt * 2
 
 
+HEADER_WORDS = 8192 // 4  # fixed workspace header: flag word, then arrival counters from byte 256
+COUNT_WORD = 256 // 4
+
+
 def records_tagged(ws, nrec):
-    """True when the nrec 64-bit records after the 256-byte header all carry
-    one non-zero epoch in their upper words."""
+    """True when the nrec 64-bit records after the header all carry one
+    non-zero epoch in their upper words."""
     u = ws.download().view(np.uint32)
-    hi = u[64:64 + 2 * nrec][1::2]
+    hi = u[HEADER_WORDS:HEADER_WORDS + 2 * nrec][1::2]
     return hi.size == nrec and hi[0] != 0 and bool(np.all(hi == hi[0]))
+
+
+def counters_rearmed(ws):
+    """The backward's arrival counters are back at zero after a launch."""
+    u = ws.download().view(np.uint32)
+    return not np.any(u[COUNT_WORD:HEADER_WORDS])
 
 
 def zeroed(L, n):
@@ -123,6 +133,7 @@ def check_case(L, orc, rng, shape, act):
     if ok:
         assert records_tagged(bws, nrec), "backward did not take the streaming path"
         assert L.nnhip_groupnorm_workspace_status(bws.p) == 0
+        assert counters_rearmed(bws), "arrival counters left non-zero"
 
 
 @pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
@@ -189,6 +200,25 @@ def test_stream_groupnorm_workspace_reuse_across_shapes(L, orc, rng, monkeypatch
         dx, _, _ = run_bwd(L, dy, x, gamma, beta, mu_ref, rs_ref, G, 3, ws)
         assert rel_err(dx, dx_ref) <= TOL
         assert L.nnhip_groupnorm_workspace_status(ws.p) == 0
+
+
+def test_cooperative_launch_matches_plain(L, rng, monkeypatch):
+    """NNHIP_GN_COOPERATIVE=1 launches the same kernels cooperatively: the
+    results are bit-identical to the plain launch's."""
+    print("[case] stream groupnorm cooperative vs plain", flush=True)
+    monkeypatch.setenv("NNHIP_GN_PATH", "stream")
+    B, H, W, C, G = 2, 64, 64, 256, 32
+    x, gamma, beta, dy = make_inputs(rng, B, H, W, C)
+    ws = zeroed(L, L.nnhip_groupnorm_backward_workspace(B, H * W, C, G))
+    out = {}
+    for coop in ("0", "1"):
+        monkeypatch.setenv("NNHIP_GN_COOPERATIVE", coop)
+        y, mu, rs = run_fwd(L, x, gamma, beta, G, 3, ws)
+        out[coop] = (y, mu, rs) + run_bwd(L, dy, x, gamma, beta, mu, rs, G, 3, ws)
+        assert counters_rearmed(ws)
+        assert L.nnhip_groupnorm_workspace_status(ws.p) == 0
+    for a, b, what in zip(out["0"], out["1"], ("y", "mu", "rstd", "dx", "dgamma", "dbeta")):
+        assert_bits_equal(a, b, what)
 
 
 def test_reg_path_switch_matches_stream(L, rng, monkeypatch):

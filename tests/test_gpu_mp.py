@@ -139,3 +139,31 @@ def test_fill_f32(L):
     L.nnhip_fill_f32(buf.p, 2.5, 7, None)
     L.sync()
     assert np.all(buf.download()[:7] == 2.5) and buf.download()[7] == 0.0
+
+
+def test_launcher_scratch_reuse_across_sizes_and_streams(L, orc, rng):
+    """Launchers without a workspace argument keep one cached scratch block per
+    stream: calls that grow and shrink it, alternating between the null stream
+    and a created one, all match the lent-workspace launcher bit for bit."""
+    print("[case] launcher scratch reuse", flush=True)
+    s1 = L.dll.nnhip_stream_create()
+    assert s1
+    try:
+        for k, (ni, no) in enumerate([(64, 16), (1152, 640), (300, 1000), (12, 8), (2048, 2048)]):
+            stream = s1 if k % 2 else None
+            W = orc.weight_normalize(rng.standard_normal((ni, no)).astype(np.float32), 1e-4)
+            M = rng.standard_normal((ni, no)).astype(np.float32)
+            Wd, gain = L.to_device(W), L.to_device(np.array([1.1], np.float32))
+            gA, gB = L.to_device(M), L.to_device(M)
+            ggA, ggB = L.to_device(np.zeros(1, np.float32)), L.to_device(np.zeros(1, np.float32))
+            ws = L.alloc(int(L.nnhip_weight_normalize_backward_workspace(no)))
+            ws.fill_bytes(0)
+            L.launch_weight_normalize_backward(gA.p, Wd.p, gain.p, ggA.p, ni, no, stream)
+            L.launch_weight_normalize_backward_ws(gB.p, Wd.p, gain.p, ggB.p, ni, no, ws.p, stream)
+            L.dll.nnhip_stream_synchronize(s1)
+            L.sync()
+            assert_bits_equal(gA.download(shape=M.shape), gB.download(shape=M.shape), f"gW call {k}")
+            assert_bits_equal(ggA.download(), ggB.download(), f"g_gain call {k}")
+    finally:
+        L.dll.nnhip_stream_synchronize(s1)
+        L.dll.nnhip_stream_destroy(s1)
