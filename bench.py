@@ -220,6 +220,29 @@ def run_suite(L, nn, reps):
     _row("mp_channel_split", "cfg2 [128,32,32,256] -> 2x128",
          T.median_us(lambda: L.launch_mp_channel_split(a.p, b_.p, o2.p, 0.3, R, Cc, Cc, stream), reps),
          16 * R * Cc)
+    # EDM block neighbours at the cfg2 shape (src/cond_conv_residual.c:30-33, 46-49)
+    cnd = dev(0.5 * rng.standard_normal(128 * Cc))
+    gcd = L.alloc(128 * Cc)
+    tmp = L.alloc(R * Cc)
+    _row("spatial_modulate_mp_silu_fwd", "EDM block [128,32,32,128] fused",
+         T.median_us(lambda: L.launch_spatial_modulate_act_forward(o.p, a.p, cnd.p, 128, 32, 32, Cc, 5, stream),
+                     reps), 8 * R * Cc)
+
+    def ref_fwd():
+        L.launch_spatial_modulate(tmp.p, a.p, cnd.p, 128, 32, 32, Cc, stream)
+        L.launch_activation_forward(o.p, tmp.p, R * Cc, 5, stream)
+    _row("spatial_modulate_mp_silu_fwd_ref", "EDM block, reference pair (2 launches)", T.median_us(ref_fwd, reps),
+         8 * R * Cc, "same algorithmic bytes as the fused row")
+    _row("spatial_modulate_mp_silu_bwd", "EDM block [128,32,32,128] fused",
+         T.median_us(lambda: L.launch_spatial_modulate_act_backward(o.p, gcd.p, b_.p, a.p, cnd.p, 128, 32, 32, Cc, 5,
+                                                                    None, stream), reps), 12 * R * Cc)
+
+    def ref_bwd():
+        L.launch_activation_backward(tmp.p, b_.p, o2.p, R * Cc, 5, stream)
+        L.launch_spatial_modulate_backward(o.p, gcd.p, tmp.p, a.p, cnd.p, 128, 32, 32, Cc, stream)
+    _row("spatial_modulate_mp_silu_bwd_ref", "EDM block, reference pair (2 launches)", T.median_us(ref_bwd, reps),
+         12 * R * Cc, "same algorithmic bytes as the fused row")
+    del tmp
     del o2
     Kg, Co = 1152, 128
     W = dev(rng.standard_normal(Kg * Co))
@@ -294,6 +317,14 @@ def run_suite(L, nn, reps):
     _row("silu_bwd", "cfg4 [256,64,64,256]",
          T.median_us(lambda: L.launch_activation_backward(ga.p, ya.p, xa.p, n4, 3, stream), max(5, reps // 4)),
          12 * n4)
+    # DDPM block neighbours at the cfg4 shape (src/conv_residual.c:33, 44-45)
+    emb = dev(rng.standard_normal(256 * 256))
+    gemb = L.alloc(256 * 256)
+    _row("spatial_add", "DDPM block [256,64,64,256] += [256,256]",
+         T.median_us(lambda: L.launch_spatial_add(ya.p, emb.p, 256, 64, 64, 256, stream), max(5, reps // 4)), 8 * n4)
+    _row("spatial_reduce_sum", "DDPM block [256,64,64,256] -> [256,256]",
+         T.median_us(lambda: L.launch_spatial_reduce_sum(gemb.p, xa.p, 256, 64 * 64, 256, stream), max(5, reps // 4)),
+         4 * n4)
     del xa, ga, ya
 
     # cfg5: fused Adam + EMA over the DDPM-UNet-like list

@@ -67,6 +67,14 @@ _SIGS = {
     "nnhip_event_elapsed_ms": (F, [P, P], False),
     "nnhip_copy_f32": (None, [P, P, SZ, P], True),
     "nnhip_fill_f32": (None, [P, F, SZ, P], True),
+    "launch_spatial_add": (None, [P, P, I, I, I, I, P], True),
+    "launch_spatial_reduce_sum": (None, [P, P, I, I, I, P], True),
+    "launch_spatial_modulate": (None, [P, P, P, I, I, I, I, P], True),
+    "launch_spatial_modulate_backward": (None, [P, P, P, P, P, I, I, I, I, P], True),
+    "launch_spatial_modulate_act_forward": (None, [P, P, P, I, I, I, I, I, P], True),
+    "launch_spatial_modulate_act_backward": (None, [P, P, P, P, P, I, I, I, I, I, P, P], True),
+    "launch_spatial_reduce_sum_ws": (None, [P, P, I, I, I, P, P], True),
+    "nnhip_spatial_reduce_workspace": (SZ, [I, I, I], False),
     # launch layer (nn_hip.h)
     "launch_add_bias": (None, [P, P, I, I, P], True),
     "launch_bias_grad": (None, [P, P, I, I, P], True),

@@ -187,9 +187,54 @@ void launch_im2col(float* col, const float* im, int batch, int H, int W, int C,
 void launch_col2im(float* grad_im, const float* grad_col, int batch, int H, int W, int C,
     int K, int stride, int pad, int H_out, int W_out, hipStream_t s);
 
+/* ------------------------------------------------------------------------
+ * Spatial (per sample and channel) broadcasts and reductions, NHWC
+ * x [batch, H*W, C], v / cond [batch, C].
+ * ------------------------------------------------------------------------ */
+
+/* inout[b,hw,c] += bias[b,c].  replaces nn.h:443-444 / kernels.cu:1132-1142,1160-1168 */
+void launch_spatial_add(float* inout, const float* bias, int batch, int H, int W, int C,
+    hipStream_t s);
+
+/* out[b,c] = sum over hw of in[b,hw,c] (overwrites out; 0 when HW = 0), summed
+   in a fixed order.  replaces nn.h:445-446 / kernels.cu:1145-1158,1170-1178 */
+void launch_spatial_reduce_sum(float* out, const float* in, int batch, int HW, int C,
+    hipStream_t s);
+
+/* out = in * (cond[b,c] + 1).  replaces nn.h:435-436 / kernels.cu:1055-1067,1103-1111 */
+void launch_spatial_modulate(float* out, const float* in, const float* cond,
+    int batch, int H, int W, int C, hipStream_t s);
+
+/* grad_in = grad_out * (cond + 1); grad_cond[b,c] = sum over hw of grad_out * in
+   (overwrites grad_cond).  replaces nn.h:437-441 / kernels.cu:1070-1101,1113-1126 */
+void launch_spatial_modulate_backward(float* grad_in, float* grad_cond,
+    const float* grad_out, const float* in, const float* cond,
+    int batch, int H, int W, int C, hipStream_t s);
+
 /* ========================================================================
  * Fused additions (no reference counterpart)
  * ======================================================================== */
+
+/* out = act(in * (cond[b,c] + 1)) in one pass; replaces the EDM block's pair
+   launch_spatial_modulate + launch_activation_forward
+   (src/cond_conv_residual.c:30-33), whose intermediate is not stored. */
+void launch_spatial_modulate_act_forward(float* out, const float* in, const float* cond,
+    int batch, int H, int W, int C, Activation act, hipStream_t s);
+
+/* Backward of launch_spatial_modulate_act_forward in one pass: with
+   g2 = grad_out * act'(in * (cond + 1)), grad_in = g2 * (cond + 1) and
+   grad_cond[b,c] = sum over hw of g2 * in.  Replaces the pair
+   launch_activation_backward + launch_spatial_modulate_backward
+   (src/cond_conv_residual.c:46-49).  `workspace` (may be NULL: library scratch)
+   holds nnhip_spatial_reduce_workspace(batch, H*W, C) floats. */
+void launch_spatial_modulate_act_backward(float* grad_in, float* grad_cond,
+    const float* grad_out, const float* in, const float* cond,
+    int batch, int H, int W, int C, Activation act, float* workspace, hipStream_t s);
+
+/* launch_spatial_reduce_sum with a lent workspace (may be NULL). */
+void launch_spatial_reduce_sum_ws(float* out, const float* in, int batch, int HW, int C,
+    float* workspace, hipStream_t s);
+size_t nnhip_spatial_reduce_workspace(int batch, int HW, int C);
 
 /* y = act(GroupNorm(x)) in one HBM pass over x.  Replaces the caller sequence
    launch_groupnorm_forward + launch_activation_forward (src/conv_residual.c:28-29,

@@ -432,6 +432,86 @@ void orc_col2im(float* grad_im, const float* grad_col, int B, int H, int W, int 
 }
 
 /* ------------------------------------------------------------------------
+ * Spatial (per sample and channel) broadcasts and reductions over NHWC
+ * tensors: kernels.cu:1052-1178.  x is [B, HW, C]; v is [B, C].
+ * ------------------------------------------------------------------------ */
+
+void orc_spatial_add(float* x, const float* v, int B, int HW, int C) /* kernels.cu:1132-1142 */
+{
+    for (long long b = 0; b < B; ++b)
+        for (long long i = 0; i < (long long)HW * C; ++i) {
+            float* p = x + b * HW * C + i;
+            *p = *p + v[b * C + i % C];
+        }
+}
+
+void orc_spatial_reduce_sum(float* out, const float* x, int B, int HW, int C) /* kernels.cu:1145-1158 */
+{
+    /* accumulated in double: the truth the parallel sums are checked against */
+    for (long long b = 0; b < B; ++b)
+        for (int c = 0; c < C; ++c) {
+            double s = 0.0;
+            for (long long r = 0; r < HW; ++r) s += (double)x[(b * HW + r) * C + c];
+            out[b * C + c] = (float)s;
+        }
+}
+
+void orc_spatial_modulate(float* out, const float* x, const float* cond, int B, int HW, int C)
+/* kernels.cu:1055-1067: out = in * (cond + 1) */
+{
+    for (long long b = 0; b < B; ++b)
+        for (long long i = 0; i < (long long)HW * C; ++i)
+            out[b * HW * C + i] = x[b * HW * C + i] * (cond[b * C + i % C] + 1.0f);
+}
+
+void orc_spatial_modulate_backward(float* gin, float* gcond, const float* gout, const float* x,
+    const float* cond, int B, int HW, int C) /* kernels.cu:1070-1101 */
+{
+    for (long long b = 0; b < B; ++b) {
+        for (long long i = 0; i < (long long)HW * C; ++i)
+            gin[b * HW * C + i] = gout[b * HW * C + i] * (cond[b * C + i % C] + 1.0f);
+        for (int c = 0; c < C; ++c) {
+            double s = 0.0;
+            for (long long r = 0; r < HW; ++r) {
+                const long long k = (b * HW + r) * C + c;
+                s += (double)(gout[k] * x[k]);
+            }
+            gcond[b * C + c] = (float)s;
+        }
+    }
+}
+
+void orc_spatial_modulate_act_forward(float* out, const float* x, const float* cond, int B, int HW,
+    int C, int act)
+/* the reference's pair spatial_modulate + activation_forward (cond_conv_residual.c:30-33) */
+{
+    for (long long b = 0; b < B; ++b)
+        for (long long i = 0; i < (long long)HW * C; ++i)
+            out[b * HW * C + i] = orc_act(x[b * HW * C + i] * (cond[b * C + i % C] + 1.0f), act);
+}
+
+void orc_spatial_modulate_act_backward(float* gin, float* gcond, const float* gout, const float* x,
+    const float* cond, int B, int HW, int C, int act)
+/* the reference's pair activation_backward + spatial_modulate_backward
+   (cond_conv_residual.c:46-49): g2 = gout * act'(x (cond + 1)),
+   gin = g2 (cond + 1), gcond = sum_hw g2 x */
+{
+    for (long long b = 0; b < B; ++b) {
+        for (int c = 0; c < C; ++c) {
+            const float m = cond[b * C + c] + 1.0f;
+            double s = 0.0;
+            for (long long r = 0; r < HW; ++r) {
+                const long long k = (b * HW + r) * C + c;
+                const float g2 = gout[k] * orc_act_grad(x[k] * m, act);
+                gin[k] = g2 * m;
+                s += (double)(g2 * x[k]);
+            }
+            gcond[b * C + c] = (float)s;
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------
  * fp32-faithful OpenMP transcription (CPU baseline): the reference kernels'
  * per-unit maths with fp32 serial accumulation (kernels.cu:622-717).
  * ------------------------------------------------------------------------ */

@@ -85,6 +85,15 @@ void orc_col2im(float* grad_im, const float* grad_col, int B, int H, int W, int 
     int stride, int pad, int Ho, int Wo);
 
 /* ---- fp32-faithful OpenMP transcription: the CPU baseline ---- */
+void orc_spatial_add(float* x, const float* v, int B, int HW, int C);
+void orc_spatial_reduce_sum(float* out, const float* x, int B, int HW, int C);
+void orc_spatial_modulate(float* out, const float* x, const float* cond, int B, int HW, int C);
+void orc_spatial_modulate_backward(float* gin, float* gcond, const float* gout, const float* x,
+    const float* cond, int B, int HW, int C);
+void orc_spatial_modulate_act_forward(float* out, const float* x, const float* cond, int B, int HW,
+    int C, int act);
+void orc_spatial_modulate_act_backward(float* gin, float* gcond, const float* gout, const float* x,
+    const float* cond, int B, int HW, int C, int act);
 void orc_set_threads(int n);
 int orc_get_threads(void);
 void orc_groupnorm_forward_f32(float* y, float* mu, float* rstd, const float* x,

@@ -44,6 +44,12 @@ _SIGS = {
     "orc_sinusoidal": (None, [P, P, I, I, F]),
     "orc_im2col": (None, [P, P, I, I, I, I, I, I, I, I, I]),
     "orc_col2im": (None, [P, P, I, I, I, I, I, I, I, I, I]),
+    "orc_spatial_add": (None, [P, P, I, I, I]),
+    "orc_spatial_reduce_sum": (None, [P, P, I, I, I]),
+    "orc_spatial_modulate": (None, [P, P, P, I, I, I]),
+    "orc_spatial_modulate_backward": (None, [P, P, P, P, P, I, I, I]),
+    "orc_spatial_modulate_act_forward": (None, [P, P, P, I, I, I, I]),
+    "orc_spatial_modulate_act_backward": (None, [P, P, P, P, P, I, I, I, I]),
     "orc_set_threads": (None, [I]),
     "orc_get_threads": (I, []),
     "orc_groupnorm_forward_f32": (None, [P, P, P, P, P, P, I, I, I, I, F, I]),
@@ -286,6 +292,55 @@ def col2im(col, shape, K: int, stride: int, pad: int, init=None) -> np.ndarray:
     out = np.zeros(shape, np.float32) if init is None else _f(init).copy()
     dll().orc_col2im(_p(out), _p(col), B, H, W, Cc, K, stride, pad, Ho, Wo)
     return out
+
+
+def spatial_add(x, v) -> np.ndarray:
+    """x [B, HW, C] + v [B, C] broadcast over HW (orc_spatial_add)."""
+    out = _f(x).copy()
+    B, HW, Cc = out.shape
+    dll().orc_spatial_add(_p(out), _p(_f(v)), B, HW, Cc)
+    return out
+
+
+def spatial_reduce_sum(x) -> np.ndarray:
+    """[B, HW, C] -> [B, C] sums over HW (orc_spatial_reduce_sum, double accumulation)."""
+    x = _f(x)
+    B, HW, Cc = x.shape
+    out = np.empty((B, Cc), np.float32)
+    dll().orc_spatial_reduce_sum(_p(out), _p(x), B, HW, Cc)
+    return out
+
+
+def spatial_modulate(x, cond) -> np.ndarray:
+    x = _f(x)
+    B, HW, Cc = x.shape
+    out = np.empty_like(x)
+    dll().orc_spatial_modulate(_p(out), _p(x), _p(_f(cond)), B, HW, Cc)
+    return out
+
+
+def spatial_modulate_backward(gout, x, cond) -> tuple[np.ndarray, np.ndarray]:
+    gout, x = _f(gout), _f(x)
+    B, HW, Cc = x.shape
+    gin, gc = np.empty_like(x), np.empty((B, Cc), np.float32)
+    dll().orc_spatial_modulate_backward(_p(gin), _p(gc), _p(gout), _p(x), _p(_f(cond)), B, HW, Cc)
+    return gin, gc
+
+
+def spatial_modulate_act_forward(x, cond, act: int) -> np.ndarray:
+    x = _f(x)
+    B, HW, Cc = x.shape
+    out = np.empty_like(x)
+    dll().orc_spatial_modulate_act_forward(_p(out), _p(x), _p(_f(cond)), B, HW, Cc, act)
+    return out
+
+
+def spatial_modulate_act_backward(gout, x, cond, act: int) -> tuple[np.ndarray, np.ndarray]:
+    gout, x = _f(gout), _f(x)
+    B, HW, Cc = x.shape
+    gin, gc = np.empty_like(x), np.empty((B, Cc), np.float32)
+    dll().orc_spatial_modulate_act_backward(_p(gin), _p(gc), _p(gout), _p(x), _p(_f(cond)), B, HW, Cc, act)
+    return gin, gc
 
 
 def set_threads(n: int) -> None:

@@ -459,3 +459,67 @@ def test_ema_geometric_decay(orc, rng):
     lerp = torch.lerp(torch.from_numpy(s0), torch.from_numpy(p), w1).numpy()
     one = orc.weighted_sum(s0, p, float(decay), w1)
     assert np.max(np.abs(one - lerp)) < 1e-6
+
+
+# ---------------------------------------------------------------------------
+# Spatial broadcasts / reductions (kernels.cu:1052-1178) and the EDM block's
+# fused modulate + activation pair (cond_conv_residual.c:30-33, 46-49)
+# ---------------------------------------------------------------------------
+def test_spatial_add_and_modulate_are_single_ops(orc, rng):
+    """One add / one multiply per element: numpy's float32 broadcast gives the
+    same bits; special cond values: 0 is the identity, -1 gives zeros."""
+    B, HW, C = 3, 10, 6
+    x = rng.standard_normal((B, HW, C)).astype(np.float32)
+    v = rng.standard_normal((B, C)).astype(np.float32)
+    assert np.array_equal(orc.spatial_add(x, v), x + v[:, None, :])
+    assert np.array_equal(orc.spatial_modulate(x, v), x * (v + np.float32(1.0))[:, None, :])
+    assert np.array_equal(orc.spatial_modulate(x, np.zeros((B, C), np.float32)), x)
+    assert not np.any(orc.spatial_modulate(x, -np.ones((B, C), np.float32)))
+
+
+def test_spatial_reduce_sum_closed_forms(orc, rng):
+    B, HW, C = 2, 257, 5
+    x = rng.standard_normal((B, HW, C)).astype(np.float32)
+    np.testing.assert_allclose(orc.spatial_reduce_sum(x), x.astype(np.float64).sum(axis=1), rtol=1e-6, atol=1e-6)
+    # constant rows: HW * value exactly (small integers)
+    ones = np.full((B, HW, C), 3.0, np.float32)
+    assert np.array_equal(orc.spatial_reduce_sum(ones), np.full((B, C), 3.0 * HW, np.float32))
+    # spatial_reduce_sum is the adjoint of spatial_add: <add(0, v), y> = <v, reduce(y)>
+    v = rng.standard_normal((B, C)).astype(np.float32)
+    lhs = float(np.sum(orc.spatial_add(np.zeros_like(x), v).astype(np.float64) * x))
+    rhs = float(np.sum(v.astype(np.float64) * orc.spatial_reduce_sum(x)))
+    assert abs(lhs - rhs) <= 1e-5 * max(1.0, abs(lhs))
+
+
+def test_spatial_modulate_backward_gradcheck(orc, rng):
+    B, HW, C = 2, 9, 4
+    x = rng.standard_normal((B, HW, C)).astype(np.float32)
+    cond = (0.5 * rng.standard_normal((B, C))).astype(np.float32)
+    g = rng.standard_normal((B, HW, C)).astype(np.float32)
+    gin, gc = orc.spatial_modulate_backward(g, x, cond)
+    _fd_check(rng, lambda xx: float(np.sum(orc.spatial_modulate(xx, cond).astype(np.float64) * g)), x.copy(), gin,
+              "grad_in")
+    _fd_check(rng, lambda cc: float(np.sum(orc.spatial_modulate(x, cc).astype(np.float64) * g)), cond.copy(), gc,
+              "grad_cond")
+
+
+@pytest.mark.parametrize("act", [IDENT, SILU, MP_SILU, GELU, TANH])
+def test_spatial_modulate_act_is_the_reference_pair(orc, rng, act):
+    """The fused forms equal the reference's two-launch sequences: bits for the
+    elementwise outputs, the double-accumulated sum for grad_cond; and the
+    backward passes the reference's finite-difference gradcheck."""
+    B, HW, C = 2, 12, 6
+    x = (1.5 * rng.standard_normal((B, HW, C))).astype(np.float32)
+    cond = (0.5 * rng.standard_normal((B, C))).astype(np.float32)
+    g = rng.standard_normal((B, HW, C)).astype(np.float32)
+    h2 = orc.spatial_modulate(x, cond)
+    assert np.array_equal(orc.spatial_modulate_act_forward(x, cond, act), orc.act_forward(h2, act))
+    gin, gc = orc.spatial_modulate_act_backward(g, x, cond, act)
+    gin_ref, gc_ref = orc.spatial_modulate_backward(orc.act_backward(g, h2, act), x, cond)
+    assert np.array_equal(gin, gin_ref)
+    np.testing.assert_allclose(gc, gc_ref, rtol=1e-6, atol=1e-6)
+    if act != IDENT:
+        _fd_check(rng, lambda xx: float(np.sum(orc.spatial_modulate_act_forward(xx, cond, act).astype(np.float64) * g)),
+                  x.copy(), gin, "grad_in")
+        _fd_check(rng, lambda cc: float(np.sum(orc.spatial_modulate_act_forward(x, cc, act).astype(np.float64) * g)),
+                  cond.copy(), gc, "grad_cond")
