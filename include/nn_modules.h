@@ -139,6 +139,19 @@ Module* spatial_groupnorm_create(int C, int num_groups, int H, int W, int max_ba
 Module* conv2d_create(Context* ctx, int C_in, int C_out, int K, int stride, int pad,
     int H, int W, int max_batch, int mp_mode, float gain);         /* src/conv2d.c:95 */
 
+Module* linear_create(Context* ctx, int in_dim, int out_dim);       /* src/linear.c:49 */
+
+/* Diffusion blocks (src/nn.h:279-283), built on the fused kernels: the DDPM
+   residual block (src/conv_residual.c:104) with fused GroupNorm+SiLU and the
+   parallel embedding broadcast / reduction, and the EDM2 block
+   (src/cond_conv_residual.c:96) with the fused modulation + MP-SiLU pair.
+   Both read the embedding from ctx->cond[cond_slot].fwd and add its gradient
+   into ctx->cond[cond_slot].grad, as the reference's blocks do. */
+Module* conv_residual_create(Context* ctx, int C, int emb_dim, int H, int W,
+    int max_batch, int num_groups, int cond_slot);                 /* src/conv_residual.c:104 */
+Module* cond_conv_residual_create(Context* ctx, int C, int emb_dim, int H, int W,
+    int max_batch, float t, int cond_slot);                        /* src/cond_conv_residual.c:96 */
+
 /* GroupNorm followed by an activation in one module (no reference
    counterpart): forward writes act(GN(x)) only, backward takes the gradient
    of the activated output.  Replaces the GroupNorm module + activation

@@ -69,7 +69,10 @@ static void restore(const ParamList* pl, float** snap)
     for (int k = 0; k < pl->count; ++k) h2d(pl->items[k].param, snap[k], pl->items[k].size);
 }
 
-static int check_module(const char* tag, Module* m, int batch, double rtol)
+/* cond_slot >= 0: the module also reads ctx->cond[cond_slot].fwd and adds its
+   gradient into ctx->cond[cond_slot].grad (the diffusion blocks); that input
+   is checked like the module input. */
+static int check_module_cond(const char* tag, Module* m, int batch, double rtol, int cond_slot)
 {
     int n_in = batch * m->in_dim, n_out = batch * m->out_dim;
     float* d_in = nn_device_alloc((size_t)n_in);
@@ -97,10 +100,16 @@ static int check_module(const char* tag, Module* m, int batch, double rtol)
         d2h(snap[k], pl.items[k].param, pl.items[k].size);
         NN_HIP_CHECK(hipMemset(pl.items[k].grad, 0, (size_t)pl.items[k].size * sizeof(float)));
     }
+    int n_cond = cond_slot >= 0 ? batch * g_ctx.cond[cond_slot].dim : 0;
+    float* h_cond = (float*)malloc((size_t)(n_cond ? n_cond : 1) * sizeof(float));
+    float* h_gcond = (float*)malloc((size_t)(n_cond ? n_cond : 1) * sizeof(float));
+    if (n_cond) d2h(h_cond, g_ctx.cond[cond_slot].fwd, n_cond);
     m->forward(m, d_in, d_out, batch, &g_ctx);
+    ctx_zero_cond_grad(&g_ctx, batch);
     m->backward(m, d_in, d_out, d_gout, d_gin, batch, &g_ctx);
     NN_HIP_CHECK(hipDeviceSynchronize());
     d2h(h_gin, d_gin, n_in);
+    if (n_cond) d2h(h_gcond, g_ctx.cond[cond_slot].grad, n_cond);
     float** ana = (float**)calloc((size_t)(pl.count > 0 ? pl.count : 1), sizeof(float*));
     for (int k = 0; k < pl.count; ++k) {
         ana[k] = (float*)malloc((size_t)pl.items[k].size * sizeof(float));
@@ -137,6 +146,33 @@ static int check_module(const char* tag, Module* m, int batch, double rtol)
         }
     }
     h2d(d_in, h_in, n_in);
+
+    n = pick_indices(n_cond, idx);
+    for (int s = 0; s < n; ++s) {
+        int j = idx[s];
+        float* d_cond = (float*)g_ctx.cond[cond_slot].fwd;
+        float save = h_cond[j];
+        restore(&pl, snap);
+        h_cond[j] = save + GC_EPS;
+        h2d(d_cond, h_cond, n_cond);
+        double lp = loss_at(m, d_in, d_out, h_out, h_g, batch, n_out);
+        restore(&pl, snap);
+        h_cond[j] = save - GC_EPS;
+        h2d(d_cond, h_cond, n_cond);
+        double lm = loss_at(m, d_in, d_out, h_out, h_g, batch, n_out);
+        h_cond[j] = save;
+        h2d(d_cond, h_cond, n_cond);
+        double num = (lp - lm) / (2.0 * GC_EPS);
+        double e = viol_ratio(num, h_gcond[j], rtol);
+        if (e > worst) {
+            worst = e;
+            where = "cond";
+            worst_k = -1;
+            worst_j = j;
+            worst_num = num;
+            worst_ana = h_gcond[j];
+        }
+    }
 
     for (int k = 0; k < pl.count; ++k) {
         int sz = pl.items[k].size;
@@ -186,11 +222,30 @@ static int check_module(const char* tag, Module* m, int batch, double rtol)
     free(h_out);
     free(h_g);
     free(h_gin);
+    free(h_cond);
+    free(h_gcond);
     (void)hipFree(d_in);
     (void)hipFree(d_out);
     (void)hipFree(d_gout);
     (void)hipFree(d_gin);
     return pass ? 0 : 1;
+}
+
+static int check_module(const char* tag, Module* m, int batch, double rtol)
+{
+    return check_module_cond(tag, m, batch, rtol, -1);
+}
+
+/* Set the k-th single-element parameter of m (e.g. an mp gain) to v. */
+static Module* with_scalar_param(Module* m, int k, float v)
+{
+    ParamList pl;
+    param_list_init(&pl);
+    m->parameters(m, &pl);
+    for (int i = 0, seen = 0; i < pl.count; ++i)
+        if (pl.items[i].size == 1 && seen++ == k) h2d(pl.items[i].param, &v, 1);
+    param_list_free(&pl);
+    return m;
 }
 
 /* Returns the number of failing modules.  Module list: the reference's
@@ -219,6 +274,24 @@ int nn_gradcheck_run(int verbose)
     fails += check_module("conv3x3_mp", conv2d_create(&g_ctx, 3, 4, 3, 1, 1, 6, 6, B, 1, 1.0f), B, 2e-2);
     fails += check_module("conv1x1_mp", conv2d_create(&g_ctx, 4, 6, 1, 1, 0, 5, 5, B, 1, 1.0f), B, 2e-2);
     fails += check_module("conv3x3_s2", conv2d_create(&g_ctx, 4, 4, 3, 2, 1, 7, 7, B, 0, 1.0f), B, 2e-2);
+    fails += check_module("linear", linear_create(&g_ctx, 12, 8), B, 2e-2);
+    /* diffusion blocks with an embedding slot; the EDM block's emb_lin gain is
+       zero at creation (src/cond_conv_residual.c:113), so it is set to 0.7
+       here to exercise the modulation path */
+    {
+        const int emb = 6;
+        int slot = ctx_add_cond(&g_ctx, emb, B);
+        float* d_emb = nn_device_alloc((size_t)B * emb);
+        nn_fill_normal(&g_ctx, d_emb, (size_t)B * emb, 0.0f, 1.0f);
+        ctx_set_cond(&g_ctx, slot, d_emb);
+        fails += check_module_cond("conv_residual", conv_residual_create(&g_ctx, 8, emb, 4, 4, B, 4, slot), B, 2e-2,
+            slot);
+        fails += check_module_cond("cond_conv_residual",
+            with_scalar_param(cond_conv_residual_create(&g_ctx, 4, emb, 4, 4, B, 0.3f, slot), 1, 0.7f), B, 2e-2,
+            slot);
+        ctx_free_cond(&g_ctx);
+        (void)hipFree(d_emb);
+    }
     nn_context_destroy(&g_ctx);
     printf("%s (%d failing module%s)\n", fails ? "GRADCHECK FAILED" : "ALL GRADIENTS OK", fails,
         fails == 1 ? "" : "s");
