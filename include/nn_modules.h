@@ -192,6 +192,21 @@ void ema_swap(EMA* ema, ParamList* pl, Context* ctx);                /* src/ema.
 void ema_free(EMA* ema);
 void ema_shadow_list(const EMA* ema, ParamList* shadow);
 
+/* ------------------------------ checkpoints ------------------------------ */
+
+/* The reference's CKPT (weights) and CKTR (params, EMA shadow, Adam m, Adam v,
+   step and Adam counters) files, byte for byte (src/checkpoint.c:1-136,
+   declared at src/nn.h:256-269).  0 on success; -1 open/write failure, -2 bad
+   magic or short file, -3 count mismatch, -4 size mismatch. */
+int checkpoint_save(const char* path, const ParamList* pl);
+int checkpoint_load(const char* path, ParamList* pl);
+int checkpoint_save_training(const char* path, int step, int adam_t,
+    const ParamList* params, const ParamList* ema_shadow,
+    const ParamList* adam_m, const ParamList* adam_v);
+int checkpoint_load_training(const char* path, int* step, int* adam_t,
+    ParamList* params, ParamList* ema_shadow,
+    ParamList* adam_m, ParamList* adam_v);
+
 /* optimizer_step followed by ema_update in one launch (no reference
    counterpart; replaces src/diffusion/train.c:53-54).  Same results as the
    two calls in sequence.  Adam optimizers only. */
