@@ -1,0 +1,53 @@
+"""The fused diffusion blocks (host/conv_residual.c, host/cond_conv_residual.c)
+against the reference's composition of the same launchers with the same
+parameters (reference src/conv_residual.c:21-66, src/cond_conv_residual.c:
+22-62): out, grad_in, every parameter gradient and the embedding gradient.
+The DDPM sides differ only where the fused GroupNorm+SiLU recomputes the
+pre-activation and uses the fast activation form: bar 1e-5 relative to
+max(|ref|, rms(ref)) (measured: <= 3e-6).  The EDM fused pair recomputes
+x (c + 1) with the same operations and reduces grad_cond with the same kernel,
+so its results are bit-identical.  The C side is tests/blockcheck.c in
+_build/libgradcheck.so; it also times both sides (printed)."""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+LIB = Path(__file__).resolve().parent / "_build" / "libgradcheck.so"
+BAR = 1e-5
+
+
+@pytest.fixture(scope="module")
+def bc(L):
+    assert LIB.exists(), f"{LIB} missing: run __graft_entry__.build()"
+    lib = C.CDLL(str(LIB))
+    lib.nn_blockcheck_ddpm.argtypes = [C.c_int] * 7 + [C.POINTER(C.c_float)]
+    lib.nn_blockcheck_ddpm.restype = C.c_double
+    lib.nn_blockcheck_edm.argtypes = [C.c_int] * 5 + [C.c_float, C.c_int, C.POINTER(C.c_float)]
+    lib.nn_blockcheck_edm.restype = C.c_double
+    return lib
+
+
+@pytest.mark.parametrize("shape", [(2, 8, 8, 32, 8, 16), (16, 32, 32, 256, 32, 128)],
+                         ids=["small", "streaming-gn"])
+def test_ddpm_block_matches_reference_composition(bc, shape):
+    print(f"[case] DDPM block {shape}", flush=True)
+    ms = (C.c_float * 2)()
+    worst = bc.nn_blockcheck_ddpm(*shape, 3, ms)
+    print(f"DDPM block {shape}: max rel diff {worst:.3e}; fwd+bwd fused {ms[0]:.3f} ms, "
+          f"reference composition {ms[1]:.3f} ms", flush=True)
+    assert worst <= BAR
+
+
+@pytest.mark.parametrize("shape", [(2, 8, 8, 16, 12), (128, 32, 32, 128, 512)], ids=["small", "cfg2"])
+def test_edm_block_matches_reference_composition(bc, shape):
+    print(f"[case] EDM block {shape}", flush=True)
+    ms = (C.c_float * 2)()
+    worst = bc.nn_blockcheck_edm(*shape, 0.3, 3, ms)
+    print(f"EDM block {shape}: max rel diff {worst:.3e}; fwd+bwd fused {ms[0]:.3f} ms, "
+          f"reference composition {ms[1]:.3f} ms", flush=True)
+    assert worst == 0.0
