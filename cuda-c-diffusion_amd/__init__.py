@@ -75,6 +75,9 @@ _SIGS = {
     "launch_spatial_modulate_act_backward": (None, [P, P, P, P, P, I, I, I, I, I, P, P], True),
     "launch_spatial_reduce_sum_ws": (None, [P, P, I, I, I, P, P], True),
     "nnhip_spatial_reduce_workspace": (SZ, [I, I, I], False),
+    "launch_conv2d_forward_implicit": (None, [P, P, P, P, P] + [I] * 10 + [P], True),
+    "nnhip_conv2d_implicit_supported": (I, [I, I], False),
+    "launch_transpose": (None, [P, P, I, I, P], True),
     # launch layer (nn_hip.h)
     "launch_add_bias": (None, [P, P, I, I, P], True),
     "launch_bias_grad": (None, [P, P, I, I, P], True),

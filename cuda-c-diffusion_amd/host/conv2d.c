@@ -1,8 +1,13 @@
-/* conv2d.c -- NHWC conv2d as im2col + GEMM, plain (bias) or magnitude-
- * preserving (forced weight norm + gain).  Reference: src/conv2d.c:6-145.
- * Weights are [K*K*C_in, C_out] row-major (conv2d.c:114-115).  The backward
- * writes grad_in with the gather col2im, which needs no memset of grad_in. */
+/* conv2d.c -- NHWC conv2d, plain (bias) or magnitude-preserving (forced
+ * weight norm + gain).  Reference: src/conv2d.c:6-145.  Weights are
+ * [K*K*C_in, C_out] row-major (conv2d.c:114-115).
+ * Forward: the implicit-GEMM kernel on the matrix cores when the channel counts
+ * allow it (C_in % 32 == 0, C_out % 128 == 0), with the bias or gain in its
+ * epilogue; otherwise im2col + rocBLAS GEMM + bias/gain pass, as the reference.
+ * NNHIP_CONV_PATH=gemm forces the latter.  Backward: im2col + rocBLAS GEMMs,
+ * and the gather col2im, which needs no memset of grad_in. */
 #include <math.h>
+#include <string.h>
 
 #include "nn_gemm.h"
 
@@ -16,7 +21,14 @@ typedef struct {
     float *gain, *g_gain;
     float* wn_ws;  /* weight-norm backward workspace (mp mode; zero-filled at create) */
     float* col;
+    float* WT;     /* [C_out, K*K*C_in] weight for the implicit GEMM (NULL when unsupported) */
 } Conv2DState;
+
+static int use_implicit(const Conv2DState* st)
+{
+    const char* e = getenv("NNHIP_CONV_PATH");
+    return st->WT && !(e && strcmp(e, "gemm") == 0);
+}
 
 static void conv2d_forward(Module* self, const float* in, float* out, int batch, Context* ctx)
 {
@@ -24,6 +36,13 @@ static void conv2d_forward(Module* self, const float* in, float* out, int batch,
     NN_ASSERT(batch <= st->max_batch, "conv2d: batch exceeds max_batch");
     int M = batch * st->Ho * st->Wo;
     int Kg = st->K * st->K * st->C_in;
+    if (use_implicit(st)) {
+        if (st->mp_mode) launch_weight_normalize(st->Wt, Kg, st->C_out, st->eps, ctx->stream);
+        launch_transpose(st->WT, st->Wt, Kg, st->C_out, ctx->stream);
+        launch_conv2d_forward_implicit(out, in, st->WT, st->mp_mode ? NULL : st->b, st->mp_mode ? st->gain : NULL,
+            batch, st->Hi, st->Wi, st->C_in, st->C_out, st->K, st->stride, st->pad, st->Ho, st->Wo, ctx->stream);
+        return;
+    }
     launch_im2col(st->col, in, batch, st->Hi, st->Wi, st->C_in, st->K, st->stride, st->pad,
         st->Ho, st->Wo, ctx->stream);
     if (st->mp_mode) {
@@ -75,6 +94,7 @@ static void conv2d_free(Module* self)
     (void)hipFree(st->Wt);
     (void)hipFree(st->gW);
     (void)hipFree(st->col);
+    if (st->WT) (void)hipFree(st->WT);
     if (st->mp_mode) {
         (void)hipFree(st->gain);
         (void)hipFree(st->g_gain);
@@ -108,6 +128,7 @@ Module* conv2d_create(Context* ctx, int C_in, int C_out, int K, int stride, int 
     st->Wt = nn_device_alloc((size_t)Kg * C_out);
     st->gW = nn_device_alloc((size_t)Kg * C_out);
     st->col = nn_device_alloc((size_t)max_batch * st->Ho * st->Wo * Kg);
+    st->WT = nnhip_conv2d_implicit_supported(C_in, C_out) ? nn_device_alloc((size_t)Kg * C_out) : NULL;
     if (mp_mode) {
         st->b = NULL;
         st->gb = NULL;

@@ -231,6 +231,21 @@ void launch_spatial_modulate_act_backward(float* grad_in, float* grad_cond,
     const float* grad_out, const float* in, const float* cond,
     int batch, int H, int W, int C, Activation act, float* workspace, hipStream_t s);
 
+/* NHWC convolution forward as an implicit GEMM on the matrix cores: the
+   im2col matrix is gathered tile by tile from x, never written.  Replaces the
+   reference's launch_im2col + gemm_forward + launch_add_bias /
+   launch_scale_by_scalar (src/conv2d.c:17-34).  WT is the [K*K*C_in, C_out]
+   weight transposed to [C_out, K*K*C_in] (launch_transpose); y [batch*H_out*W_out,
+   C_out] = conv + bias[n] (bias non-NULL) or conv * gain[0] (gain non-NULL) or
+   conv.  Needs C_in % 32 == 0 and C_out % 128 == 0
+   (nnhip_conv2d_implicit_supported); x and WT 16-byte aligned. */
+void launch_conv2d_forward_implicit(float* y, const float* x, const float* WT, const float* bias,
+    const float* gain, int batch, int H, int W, int C_in, int C_out, int K, int stride, int pad,
+    int H_out, int W_out, hipStream_t s);
+int nnhip_conv2d_implicit_supported(int C_in, int C_out);
+/* out[c, r] = in[r, c] for a row-major [rows, cols] matrix (out != in). */
+void launch_transpose(float* out, const float* in, int rows, int cols, hipStream_t s);
+
 /* launch_spatial_reduce_sum with a lent workspace (may be NULL). */
 void launch_spatial_reduce_sum_ws(float* out, const float* in, int batch, int HW, int C,
     float* workspace, hipStream_t s);

@@ -11,7 +11,9 @@
  * largest relative difference (max |a - b| / max(|b|, rms(b))) over out,
  * grad_in, every parameter gradient and the embedding gradient.  Needs a GPU.
  */
+#define _POSIX_C_SOURCE 200809L
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include "nn_modules.h"
@@ -302,4 +304,53 @@ double nn_blockcheck_edm(int B, int H, int W, int C, int emb, float t, int reps,
     (void)hipEventDestroy(t1);
     nn_context_destroy(&g);
     return worst;
+}
+
+/* conv2d module forward on its two paths (implicit GEMM vs im2col + rocBLAS
+   GEMM + bias/gain pass, selected with NNHIP_CONV_PATH): returns the largest
+   relative difference; out_ms[0..1] = implicit / gemm forward time in ms
+   (best of `reps`). */
+double nn_convcheck(int B, int H, int W, int Cin, int Cout, int K, int stride, int pad, int mp, int reps,
+    float* out_ms)
+{
+    nn_context_init(&g, 17ull, (hipStream_t)0);
+    Module* conv = conv2d_create(&g, Cin, Cout, K, stride, pad, H, W, B, mp, 1.0f);
+    if (!mp) {
+        ParamList pl;
+        param_list_init(&pl);
+        conv->parameters(conv, &pl);
+        nn_fill_normal(&g, pl.items[1].param, (size_t)Cout, 0.0f, 0.1f);  /* non-zero bias */
+        param_list_free(&pl);
+    }
+    const size_t n_in = (size_t)B * H * W * Cin, n_out = (size_t)B * conv->out_dim;
+    float* x = dev_normal(n_in, 1.0f);
+    float *y_i = nn_device_alloc(n_out), *y_g = nn_device_alloc(n_out);
+    hipEvent_t t0, t1;
+    NN_HIP_CHECK(hipEventCreate(&t0));
+    NN_HIP_CHECK(hipEventCreate(&t1));
+    float best[2] = {1e30f, 1e30f};
+    for (int rep = 0; rep < reps + 1; ++rep) {
+        for (int path = 0; path < 2; ++path) {
+            setenv("NNHIP_CONV_PATH", path ? "gemm" : "implicit", 1);
+            NN_HIP_CHECK(hipEventRecord(t0, g.stream));
+            conv->forward(conv, x, path ? y_g : y_i, B, &g);
+            NN_HIP_CHECK(hipEventRecord(t1, g.stream));
+            NN_HIP_CHECK(hipEventSynchronize(t1));
+            float ms;
+            NN_HIP_CHECK(hipEventElapsedTime(&ms, t0, t1));
+            if (rep && ms < best[path]) best[path] = ms;
+        }
+    }
+    unsetenv("NNHIP_CONV_PATH");
+    const double d = rel_diff(y_i, y_g, n_out);
+    out_ms[0] = best[0];
+    out_ms[1] = best[1];
+    conv->free(conv);
+    (void)hipFree(x);
+    (void)hipFree(y_i);
+    (void)hipFree(y_g);
+    (void)hipEventDestroy(t0);
+    (void)hipEventDestroy(t1);
+    nn_context_destroy(&g);
+    return d;
 }

@@ -51,3 +51,20 @@ def test_edm_block_matches_reference_composition(bc, shape):
     print(f"EDM block {shape}: max rel diff {worst:.3e}; fwd+bwd fused {ms[0]:.3f} ms, "
           f"reference composition {ms[1]:.3f} ms", flush=True)
     assert worst == 0.0
+
+
+@pytest.mark.parametrize("geom", [(128, 32, 32, 128, 128, 3, 1, 1, 0), (128, 32, 32, 128, 128, 3, 1, 1, 1),
+                                  (16, 64, 64, 256, 256, 3, 1, 1, 0)],
+                         ids=["cfg3", "cfg3-mp", "ddpm-256"])
+def test_conv_module_implicit_vs_gemm_path(bc, geom):
+    """The conv2d module's two forward paths agree within the reduction bar
+    (different fp32 summation orders of the same K*K*C_in products, relative
+    to max(|y|, rms(y))), and the implicit path's time is printed."""
+    bc.nn_convcheck.argtypes = [C.c_int] * 10 + [C.POINTER(C.c_float)]
+    bc.nn_convcheck.restype = C.c_double
+    print(f"[case] conv module paths {geom}", flush=True)
+    ms = (C.c_float * 2)()
+    worst = bc.nn_convcheck(*geom, 3, ms)
+    print(f"conv2d {geom}: max rel diff {worst:.3e}; forward implicit {ms[0]:.3f} ms, im2col+rocBLAS {ms[1]:.3f} ms",
+          flush=True)
+    assert worst <= 1e-5
