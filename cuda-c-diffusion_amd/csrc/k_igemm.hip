@@ -30,6 +30,7 @@
 // Summation order: each output is a fixed-order fp32 sum (per slice, pairs of
 // k in MFMA order, slices in k order); it differs from a library GEMM's order
 // by rounding only, and is the same on every run.
+#include "nn_hip_rt.h"
 #include "nnk_common.h"
 
 namespace {
@@ -76,7 +77,12 @@ __global__ __launch_bounds__(kTpb, 2) void igemm_fwd(float* __restrict__ Y, cons
     const float* wrow = WT + (size_t)(n0 + r0) * sh.KKC + ch * 4;
     const size_t wstep = (size_t)32 * sh.KKC;
 
+    // Every lane loads (a padding position reads channel ci of pixel 0 and is
+    // zeroed when stored): a branch around a load would make the compiler's
+    // later waits drain the whole vector-memory counter, i.e. wait for the
+    // next slice's loads before the current slice's MFMAs.
     float4 ra[4], rb[4];
+    bool aok[4];
     auto load = [&](int kt) {
         const int k0 = kt * kBK;
         const int khw = k0 / sh.Cin, ci = k0 - khw * sh.Cin + ch * 4;
@@ -84,15 +90,24 @@ __global__ __launch_bounds__(kTpb, 2) void igemm_fwd(float* __restrict__ Y, cons
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int ih = ihb[q] + kh, iw = iwb[q] + kw;
-            const bool ok = rok[q] && (unsigned)ih < (unsigned)sh.H && (unsigned)iw < (unsigned)sh.W;
-            ra[q] = ok ? ld4(X + (size_t)(pix[q] + ih * sh.W + iw) * sh.Cin + ci) : make_float4(0.f, 0.f, 0.f, 0.f);
+            aok[q] = rok[q] & ((unsigned)ih < (unsigned)sh.H) & ((unsigned)iw < (unsigned)sh.W);
+            const int p = aok[q] ? pix[q] + ih * sh.W + iw : 0;
+            ra[q] = ld4(X + (size_t)p * sh.Cin + ci);
             rb[q] = ld4(wrow + q * wstep + k0);
         }
     };
+    // Padding is zeroed by masking the bits (a select of whole float4 values
+    // becomes a select of their addresses, which puts them in scratch memory).
     auto store = [&](int buf) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            As[buf][slot(r0 + 32 * q, ch)] = ra[q];
+            const unsigned mk = aok[q] ? 0xffffffffu : 0u;
+            float4 v;
+            v.x = __uint_as_float(__float_as_uint(ra[q].x) & mk);
+            v.y = __uint_as_float(__float_as_uint(ra[q].y) & mk);
+            v.z = __uint_as_float(__float_as_uint(ra[q].z) & mk);
+            v.w = __uint_as_float(__float_as_uint(ra[q].w) & mk);
+            As[buf][slot(r0 + 32 * q, ch)] = v;
             Bs[buf][slot(r0 + 32 * q, ch)] = rb[q];
         }
     };
@@ -103,13 +118,15 @@ __global__ __launch_bounds__(kTpb, 2) void igemm_fwd(float* __restrict__ Y, cons
 #pragma unroll
         for (int u = 0; u < 2; ++u) acc[t][u] = (f32x16){};
     const int nk = sh.KKC / kBK;
-    load(0);
-    store(0);
-    __syncthreads();
     const int fr = lane & 31, fh = lane >> 5;
-    for (int kt = 0; kt < nk; ++kt) {
-        const int buf = kt & 1;
-        if (kt + 1 < nk) load(kt + 1);
+    // epilogue operands, loaded before the pipeline
+    float bn[2] = {0.0f, 0.0f}, g = 1.0f;
+    if constexpr (EPI == kEpiBias) {
+        bn[0] = bias[n0 + wn * 64 + fr];
+        bn[1] = bias[n0 + wn * 64 + 32 + fr];
+    }
+    if constexpr (EPI == kEpiGain) g = gain[0];
+    auto compute = [&](int buf) {
 #pragma unroll
         for (int kq = 0; kq < 4; ++kq) {
             const int c = 2 * kq + fh;
@@ -135,32 +152,197 @@ __global__ __launch_bounds__(kTpb, 2) void igemm_fwd(float* __restrict__ Y, cons
 #pragma unroll
                 for (int u = 0; u < 2; ++u) acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t].w, b[u].w, acc[t][u], 0, 0, 0);
         }
-        if (kt + 1 < nk) store(buf ^ 1);
+    };
+    // slices: prologue, a branch-free steady loop (load next, compute current,
+    // store next), last slice
+    load(0);
+    store(0);
+    __syncthreads();
+    for (int kt = 0; kt + 1 < nk; ++kt) {
+        load(kt + 1);
+        compute(kt & 1);
+        store((kt + 1) & 1);
         __syncthreads();
     }
+    compute((nk - 1) & 1);
 
-    // epilogue: lanes 0-31 and 32-63 each write 32 consecutive outputs of a row
-    float g = 1.0f;
-    if constexpr (EPI == kEpiGain) g = gain[0];
+    // epilogue: lanes 0-31 and 32-63 each write 32 consecutive outputs of a
+    // row.  A full row tile stores with no per-row test (a branch per store
+    // would make every store wait for all earlier ones).
+    auto out = [&](int t, int u, int r) {
+        float v = acc[t][u][r];
+        if constexpr (EPI == kEpiBias) v = v + bn[u];
+        if constexpr (EPI == kEpiGain) v = v * g;
+        return v;
+    };
+    float* yb = Y + (size_t)(m0 + wm * 64 + 4 * fh) * sh.Cout + n0 + wn * 64 + fr;
+    if (m0 + kBM <= sh.M) {
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        const int n = n0 + wn * 64 + 32 * u + fr;
-        float bn = 0.0f;
-        if constexpr (EPI == kEpiBias) bn = bias[n];
+        for (int u = 0; u < 2; ++u)
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    yb[(size_t)(32 * t + 8 * (r >> 2) + (r & 3)) * sh.Cout + 32 * u] = out(t, u, r);
+    } else {
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int dm = 32 * t + 8 * (r >> 2) + (r & 3);
+                    if (m0 + wm * 64 + 4 * fh + dm < sh.M) yb[(size_t)dm * sh.Cout + 32 * u] = out(t, u, r);
+                }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Weight gradient: gW[k, n] = sum_m A[m, k] dY[m, n] (the reference's
+// gemm_dW over the im2col matrix, src/conv2d.c:44-47), with A gathered from X
+// as in the forward.  The m reduction (B * Ho * Wo rows) is split over S
+// workgroups per 128 x 128 output tile; split z writes its fixed-order partial
+// tile to part[z], and a second launch adds the S partials in split order.
+//
+// Per stage a workgroup stages 32 rows of A (its 128 k columns) and of dY
+// (its 128 n columns) in LDS as [32 m][32 float4 chunks], chunk index xor 8
+// on odd rows.  MFMA operands come straight from that layout: lane l reads
+// A[m = 2 p + l / 32][k = its row] and dY[m = 2 p + l / 32][n = its column],
+// so the two half-waves read different rows that the swizzle puts in
+// different bank halves.
+// ---------------------------------------------------------------------------
+constexpr int kWgM = 32;  // m rows per stage
+
+__device__ __forceinline__ int wslot(int m, int chunk) { return m * 32 + (chunk ^ ((m & 1) << 3)); }
+
+__global__ __launch_bounds__(kTpb, 2) void igemm_wgrad(float* __restrict__ part, const float* __restrict__ X,
+    const float* __restrict__ dY, ConvShape sh, int rows_per_split) {
+    __shared__ float4 As[2][kWgM * 32];
+    __shared__ float4 Ds[2][kWgM * 32];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int wk = w >> 1, wn = w & 1;
+    const int k0 = blockIdx.x * 128, n0 = blockIdx.y * 128, z = blockIdx.z;
+    const int mbeg = z * rows_per_split;
+    const int mend = min(sh.M, mbeg + rows_per_split);
+    // loader role: chunk ch (fixed k = k0 + 4 ch, fixed n = n0 + 4 ch), rows r0 + 8 q
+    const int ch = tid & 31, r0 = tid >> 5;
+    const int kc = k0 + 4 * ch;
+    const bool kok = kc < sh.KKC;
+    const int tap = kok ? kc / sh.Cin : 0, ci = kok ? kc - tap * sh.Cin : 0;
+    const int kh = tap / sh.K, kw = tap - kh * sh.K;
+    const float* dcol = dY + n0 + 4 * ch;
+
+    float4 ra[4], rd[4];
+    bool aok[4], mok[4];
+    auto load = [&](int ms) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int m = ms + r0 + 8 * q;
+            mok[q] = m < mend;
+            const int mm = mok[q] ? m : 0;
+            const int ow = mm % sh.Wo, t = mm / sh.Wo;
+            const int oh = t % sh.Ho, b = t / sh.Ho;
+            const int ih = oh * sh.stride - sh.pad + kh, iw = ow * sh.stride - sh.pad + kw;
+            aok[q] = mok[q] & kok & ((unsigned)ih < (unsigned)sh.H) & ((unsigned)iw < (unsigned)sh.W);
+            const int p = aok[q] ? (b * sh.H + ih) * sh.W + iw : 0;
+            ra[q] = ld4(X + (size_t)p * sh.Cin + ci);
+            rd[q] = ld4(dcol + (size_t)mm * sh.Cout);
+        }
+    };
+    auto mask4 = [](float4 v, bool ok) {
+        const unsigned mk = ok ? 0xffffffffu : 0u;
+        v.x = __uint_as_float(__float_as_uint(v.x) & mk);
+        v.y = __uint_as_float(__float_as_uint(v.y) & mk);
+        v.z = __uint_as_float(__float_as_uint(v.z) & mk);
+        v.w = __uint_as_float(__float_as_uint(v.w) & mk);
+        return v;
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            As[buf][wslot(r0 + 8 * q, ch)] = mask4(ra[q], aok[q]);
+            Ds[buf][wslot(r0 + 8 * q, ch)] = mask4(rd[q], mok[q]);
+        }
+    };
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) acc[t][u] = (f32x16){};
+    const int fr = lane & 31, fh = lane >> 5;
+    const float* Af = reinterpret_cast<const float*>(&As[0][0]);
+    const float* Df = reinterpret_cast<const float*>(&Ds[0][0]);
+    // element (m, col) of a staged tile: float4 slot of its chunk, then the component
+    auto elem = [](int m, int col) { return wslot(m, col >> 2) * 4 + (col & 3); };
+    auto compute = [&](int buf) {
+        const int base = buf * kWgM * 32 * 4;
+#pragma unroll
+        for (int p = 0; p < kWgM / 2; ++p) {
+            const int m = 2 * p + fh;
+            float a[2], d[2];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) a[t] = Af[base + elem(m, wk * 64 + 32 * t + fr)];
+#pragma unroll
+            for (int u = 0; u < 2; ++u) d[u] = Df[base + elem(m, wn * 64 + 32 * u + fr)];
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int u = 0; u < 2; ++u) acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t], d[u], acc[t][u], 0, 0, 0);
+        }
+    };
+    const int nst = (mend - mbeg + kWgM - 1) / kWgM;
+    if (nst > 0) {
+        load(mbeg);
+        store(0);
+        __syncthreads();
+        for (int st = 0; st + 1 < nst; ++st) {
+            load(mbeg + (st + 1) * kWgM);
+            compute(st & 1);
+            store((st + 1) & 1);
+            __syncthreads();
+        }
+        compute((nst - 1) & 1);
+    }
+    // partial tile: D[k][n], rows k = k0 + wk 64 + 32 t + 8 (r / 4) + 4 h + r % 4
+    float* pb = part + (size_t)z * sh.KKC * sh.Cout + (size_t)(k0 + wk * 64 + 4 * fh) * sh.Cout + n0 + wn * 64 + fr;
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int m = m0 + wm * 64 + 32 * t + 8 * (r >> 2) + 4 * fh + (r & 3);
-                if (m < sh.M) {
-                    float v = acc[t][u][r];
-                    if constexpr (EPI == kEpiBias) v = v + bn;
-                    if constexpr (EPI == kEpiGain) v = v * g;
-                    Y[(size_t)m * sh.Cout + n] = v;
-                }
+                const int dk = 32 * t + 8 * (r >> 2) + (r & 3);
+                if (k0 + wk * 64 + 4 * fh + dk < sh.KKC) pb[(size_t)dk * sh.Cout + 32 * u] = acc[t][u][r];
             }
-        }
-    }
+}
+
+// gW[i] = part[0][i] + part[1][i] + ... (split order).
+__global__ __launch_bounds__(256) void wgrad_reduce(float* __restrict__ gW, const float* __restrict__ part, int S,
+    long long n) {
+    const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    float t = part[i];
+    for (int z = 1; z < S; ++z) t += part[(size_t)z * n + i];
+    gW[i] = t;
+}
+
+struct WgradPlan {
+    int S, rows;
+};
+
+WgradPlan wgrad_plan(int M, int KKC, int Cout) {
+    const int tiles = ((KKC + 127) / 128) * (Cout / 128);
+    // one round of resident workgroups (two per CU on 256 CUs)
+    int S = tiles >= 512 ? 1 : 512 / tiles;
+    const int smax = (M + kWgM - 1) / kWgM;
+    if (S > smax) S = smax;
+    if (S < 1) S = 1;
+    int rows = (M + S - 1) / S;
+    rows = (rows + kWgM - 1) / kWgM * kWgM;
+    WgradPlan p;
+    p.rows = rows;
+    p.S = (M + rows - 1) / rows;
+    return p;
 }
 
 // out[c][r] = in[r][c] for a row-major [rows, cols] matrix (32 x 32 LDS tiles).
@@ -219,6 +401,59 @@ void launch_conv2d_forward_implicit(float* Y, const float* X, const float* WT, c
     if (bias) igemm_fwd<kEpiBias><<<grid, kTpb, 0, s>>>(Y, X, WT, bias, nullptr, sh);
     else if (gain) igemm_fwd<kEpiGain><<<grid, kTpb, 0, s>>>(Y, X, WT, nullptr, gain, sh);
     else igemm_fwd<kEpiNone><<<grid, kTpb, 0, s>>>(Y, X, WT, nullptr, nullptr, sh);
+    nnk_after_launch(what, s);
+}
+
+int nnhip_conv2d_wgrad_implicit_supported(int C_in, int C_out) {
+    return C_in > 0 && C_out > 0 && C_in % 4 == 0 && C_out % kBN == 0;
+}
+
+size_t nnhip_conv2d_wgrad_workspace(int batch, int C_in, int C_out, int K, int H_out, int W_out) {
+    if (batch <= 0 || !nnhip_conv2d_wgrad_implicit_supported(C_in, C_out)) return 0;
+    const long long M = (long long)batch * H_out * W_out;
+    if (M <= 0 || M >= (1LL << 31)) return 0;
+    const WgradPlan p = wgrad_plan((int)M, K * K * C_in, C_out);
+    return p.S > 1 ? (size_t)p.S * K * K * C_in * C_out : 0;
+}
+
+void launch_conv2d_weight_grad_implicit(float* gW, const float* X, const float* dY, int batch, int H, int W,
+    int C_in, int C_out, int K, int stride, int pad, int H_out, int W_out, float* workspace, hipStream_t s) {
+    const char* what = "launch_conv2d_weight_grad_implicit";
+    NNK_REQUIRE(batch >= 0 && H > 0 && W > 0 && K > 0 && stride > 0 && pad >= 0, what, "%s: bad geometry", what);
+    NNK_REQUIRE(nnhip_conv2d_wgrad_implicit_supported(C_in, C_out), what,
+        "%s: needs C_in %% 4 == 0 and C_out %% %d == 0 (C_in=%d C_out=%d)", what, kBN, C_in, C_out);
+    NNK_REQUIRE(H_out == (H + 2 * pad - K) / stride + 1 && W_out == (W + 2 * pad - K) / stride + 1 && H_out > 0 &&
+                    W_out > 0,
+        what, "%s: output size %dx%d does not match the geometry", what, H_out, W_out);
+    NNK_REQUIRE((long long)batch * H * W * C_in < (1LL << 31) && (long long)batch * H_out * W_out * C_out < (1LL << 31),
+        what, "%s: tensor exceeds the 32-bit index range", what);
+    NNK_REQUIRE(gW && (batch == 0 || (X && dY)), what, "%s: null pointer", what);
+    const int KKC = K * K * C_in;
+    if (batch == 0) {
+        nnhip_fill_f32(gW, 0.0f, (size_t)KKC * C_out, s);
+        return;
+    }
+    NNK_REQUIRE(aligned16(X) && aligned16(dY), what, "%s: X and dY must be 16-byte aligned", what);
+    ConvShape sh{batch, H, W, C_in, C_out, K, stride, pad, H_out, W_out, batch * H_out * W_out, KKC};
+    const WgradPlan p = wgrad_plan(sh.M, KKC, C_out);
+    float* part = gW;
+    bool pooled = false;
+    if (p.S > 1) {
+        if (workspace) {
+            part = workspace;
+        } else {
+            part = nnk_scratch_acquire((size_t)p.S * KKC * C_out, s, what);
+            if (!part) return;
+            pooled = true;
+        }
+    }
+    const dim3 grid((unsigned)((KKC + 127) / 128), (unsigned)(C_out / kBN), (unsigned)p.S);
+    igemm_wgrad<<<grid, kTpb, 0, s>>>(part, X, dY, sh, p.rows);
+    if (p.S > 1) {
+        const long long n = (long long)KKC * C_out;
+        wgrad_reduce<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(gW, part, p.S, n);
+    }
+    if (pooled) nnk_scratch_release(part, s);
     nnk_after_launch(what, s);
 }
 

@@ -243,6 +243,19 @@ void launch_conv2d_forward_implicit(float* y, const float* x, const float* WT, c
     const float* gain, int batch, int H, int W, int C_in, int C_out, int K, int stride, int pad,
     int H_out, int W_out, hipStream_t s);
 int nnhip_conv2d_implicit_supported(int C_in, int C_out);
+/* Convolution weight gradient as an implicit GEMM on the matrix cores:
+   gW [K*K*C_in, C_out] = im2col(x)^T dy (overwritten), the im2col matrix
+   gathered from x tile by tile.  Replaces the reference's launch_im2col +
+   gemm_dW (src/conv2d.c:44-47).  The reduction over the batch*H_out*W_out
+   rows is split over workgroups and the partials are added in a fixed order
+   (`workspace` of nnhip_conv2d_wgrad_workspace floats, or NULL: library
+   scratch).  Needs C_in % 4 == 0 and C_out % 128 == 0; x, dy 16-byte aligned. */
+void launch_conv2d_weight_grad_implicit(float* gW, const float* x, const float* dy, int batch, int H,
+    int W, int C_in, int C_out, int K, int stride, int pad, int H_out, int W_out, float* workspace,
+    hipStream_t s);
+int nnhip_conv2d_wgrad_implicit_supported(int C_in, int C_out);
+size_t nnhip_conv2d_wgrad_workspace(int batch, int C_in, int C_out, int K, int H_out, int W_out);
+
 /* out[c, r] = in[r, c] for a row-major [rows, cols] matrix (out != in). */
 void launch_transpose(float* out, const float* in, int rows, int cols, hipStream_t s);
 

@@ -79,3 +79,40 @@ def test_conv_forward_implicit_refuses_unsupported_channels(L, nn):
         L.launch_conv2d_forward_implicit(dummy.p, dummy.p, dummy.p, None, None, 1, 4, 4, 3, 128, 3, 1, 1, 4, 4, None)
     with pytest.raises(nn.NnHipError):
         L.launch_conv2d_forward_implicit(dummy.p, dummy.p, dummy.p, None, None, 1, 4, 4, 32, 128, 3, 1, 1, 5, 4, None)
+
+
+WGRAD_GEOMS = [
+    # B, H, W, C_in, C_out, K, stride, pad
+    (128, 32, 32, 128, 128, 3, 1, 1),  # cfg3
+    (3, 5, 7, 64, 128, 3, 1, 1),       # K*K*C_in = 576: a partial k tile
+    (4, 15, 15, 12, 256, 3, 2, 1),     # stride 2, C_in = 12
+    (2, 8, 8, 32, 128, 1, 1, 0),       # 1x1
+    (1, 9, 9, 4, 128, 5, 1, 2),        # 5x5, C_in = 4
+]
+
+
+@pytest.mark.parametrize("geom", WGRAD_GEOMS, ids=lambda g: "x".join(map(str, g)))
+def test_conv_weight_grad_implicit(L, orc, rng, geom):
+    """gW = im2col(x)^T dy (the reference's gemm_dW over launch_im2col,
+    src/conv2d.c:44-47) in double, bar 1e-5 relative to
+    max(|ref|, sqrt(sum of the squared products)); a lent workspace gives the
+    same bits as the library scratch."""
+    B, H, W, Ci, Co, K, s, p = geom
+    print(f"[case] implicit conv weight grad {geom}", flush=True)
+    Ho, Wo = _out(H, K, s, p), _out(W, K, s, p)
+    x = rng.standard_normal((B, H, W, Ci)).astype(np.float32)
+    dy = rng.standard_normal((B * Ho * Wo, Co)).astype(np.float32)
+    xd, dyd, gw = L.to_device(x), L.to_device(dy), L.alloc(K * K * Ci * Co)
+    L.launch_conv2d_weight_grad_implicit(gw.p, xd.p, dyd.p, B, H, W, Ci, Co, K, s, p, Ho, Wo, None, None)
+    L.sync()
+    col = orc.im2col(x, K, s, p).astype(np.float64)
+    d = dy.astype(np.float64)
+    ref = col.T @ d
+    floor = np.sqrt((col * col).T @ (d * d))
+    got = gw.download(shape=ref.shape).astype(np.float64)
+    assert float((np.abs(got - ref) / np.maximum(np.abs(ref), floor)).max()) <= TOL
+    ws = L.alloc(max(1, L.nnhip_conv2d_wgrad_workspace(B, Ci, Co, K, Ho, Wo)))
+    gw2 = L.alloc(K * K * Ci * Co)
+    L.launch_conv2d_weight_grad_implicit(gw2.p, xd.p, dyd.p, B, H, W, Ci, Co, K, s, p, Ho, Wo, ws.p, None)
+    L.sync()
+    assert_bits_equal(gw2.download(), gw.download(), "workspace vs scratch")
