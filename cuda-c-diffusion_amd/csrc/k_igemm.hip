@@ -345,6 +345,21 @@ WgradPlan wgrad_plan(int M, int KKC, int Cout) {
     return p;
 }
 
+// WF[ci][(kh', kw', co)] = Wt[((K-1-kh') K + (K-1-kw')) C_in + ci][co]: the
+// weight of the stride-1 input gradient, which is then a forward convolution
+// of dy with the flipped kernel and padding K-1-pad.
+__global__ __launch_bounds__(256) void flip_weights_kernel(float* __restrict__ WF, const float* __restrict__ Wt,
+    int K, int Cin, int Cout) {
+    const long long n = (long long)K * K * Cin * Cout;
+    for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long long)gridDim.x * 256) {
+        const int co = (int)(i % Cout);
+        const long long r = i / Cout;                 // (ci, tap')
+        const int tap = (int)(r % (K * K)), ci = (int)(r / (K * K));
+        const int src_tap = K * K - 1 - tap;          // (K-1-kh') K + (K-1-kw')
+        WF[i] = Wt[((size_t)src_tap * Cin + ci) * Cout + co];
+    }
+}
+
 // out[c][r] = in[r][c] for a row-major [rows, cols] matrix (32 x 32 LDS tiles).
 __global__ __launch_bounds__(256) void transpose_kernel(float* __restrict__ out, const float* __restrict__ in,
     int rows, int cols) {
@@ -401,6 +416,17 @@ void launch_conv2d_forward_implicit(float* Y, const float* X, const float* WT, c
     if (bias) igemm_fwd<kEpiBias><<<grid, kTpb, 0, s>>>(Y, X, WT, bias, nullptr, sh);
     else if (gain) igemm_fwd<kEpiGain><<<grid, kTpb, 0, s>>>(Y, X, WT, nullptr, gain, sh);
     else igemm_fwd<kEpiNone><<<grid, kTpb, 0, s>>>(Y, X, WT, nullptr, nullptr, sh);
+    nnk_after_launch(what, s);
+}
+
+void launch_conv2d_flip_weights(float* WF, const float* Wt, int K, int C_in, int C_out, hipStream_t s) {
+    const char* what = "launch_conv2d_flip_weights";
+    NNK_REQUIRE(K > 0 && C_in > 0 && C_out > 0, what, "%s: bad shape", what);
+    NNK_REQUIRE(WF && Wt && WF != Wt, what, "%s: null or aliased pointers", what);
+    const long long n = (long long)K * K * C_in * C_out;
+    long long blocks = (n + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    flip_weights_kernel<<<(unsigned)blocks, 256, 0, s>>>(WF, Wt, K, C_in, C_out);
     nnk_after_launch(what, s);
 }
 

@@ -256,6 +256,12 @@ void launch_conv2d_weight_grad_implicit(float* gW, const float* x, const float* 
 int nnhip_conv2d_wgrad_implicit_supported(int C_in, int C_out);
 size_t nnhip_conv2d_wgrad_workspace(int batch, int C_in, int C_out, int K, int H_out, int W_out);
 
+/* WF [C_in, K*K*C_out] from the [K*K*C_in, C_out] weight Wt, kernel flipped:
+   WF[ci][(kh, kw, co)] = Wt[((K-1-kh) K + (K-1-kw)) C_in + ci][co].  With it the
+   stride-1 input gradient is launch_conv2d_forward_implicit(dx, dy, WF, ...)
+   over the H_out x W_out x C_out gradient with padding K-1-pad. */
+void launch_conv2d_flip_weights(float* WF, const float* Wt, int K, int C_in, int C_out, hipStream_t s);
+
 /* out[c, r] = in[r, c] for a row-major [rows, cols] matrix (out != in). */
 void launch_transpose(float* out, const float* in, int rows, int cols, hipStream_t s);
 

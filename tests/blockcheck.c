@@ -306,10 +306,11 @@ double nn_blockcheck_edm(int B, int H, int W, int C, int emb, float t, int reps,
     return worst;
 }
 
-/* conv2d module forward on its two paths (implicit GEMM vs im2col + rocBLAS
-   GEMM + bias/gain pass, selected with NNHIP_CONV_PATH): returns the largest
-   relative difference; out_ms[0..1] = implicit / gemm forward time in ms
-   (best of `reps`). */
+/* conv2d module forward and backward on its two paths (implicit GEMMs vs
+   im2col + rocBLAS GEMMs, selected with NNHIP_CONV_PATH): returns the largest
+   relative difference over y, grad_in and the parameter gradients; out_ms[0..3]
+   = implicit / gemm forward, implicit / gemm backward time in ms (best of
+   `reps`). */
 double nn_convcheck(int B, int H, int W, int Cin, int Cout, int K, int stride, int pad, int mp, int reps,
     float* out_ms)
 {
@@ -325,30 +326,61 @@ double nn_convcheck(int B, int H, int W, int Cin, int Cout, int K, int stride, i
     const size_t n_in = (size_t)B * H * W * Cin, n_out = (size_t)B * conv->out_dim;
     float* x = dev_normal(n_in, 1.0f);
     float *y_i = nn_device_alloc(n_out), *y_g = nn_device_alloc(n_out);
-    hipEvent_t t0, t1;
+    float* gy = dev_normal(n_out, 1.0f);
+    float *gx_i = nn_device_alloc(n_in), *gx_g = nn_device_alloc(n_in);
+    ParamList pl;
+    param_list_init(&pl);
+    conv->parameters(conv, &pl);
+    float* gsave[2];
+    for (int k = 0; k < 2; ++k) gsave[k] = nn_device_alloc((size_t)pl.items[k].size);
+    hipEvent_t t0, t1, t2;
     NN_HIP_CHECK(hipEventCreate(&t0));
     NN_HIP_CHECK(hipEventCreate(&t1));
-    float best[2] = {1e30f, 1e30f};
+    NN_HIP_CHECK(hipEventCreate(&t2));
+    float best[4] = {1e30f, 1e30f, 1e30f, 1e30f};
+    double worst = 0.0;
     for (int rep = 0; rep < reps + 1; ++rep) {
         for (int path = 0; path < 2; ++path) {
             setenv("NNHIP_CONV_PATH", path ? "gemm" : "implicit", 1);
             NN_HIP_CHECK(hipEventRecord(t0, g.stream));
             conv->forward(conv, x, path ? y_g : y_i, B, &g);
             NN_HIP_CHECK(hipEventRecord(t1, g.stream));
-            NN_HIP_CHECK(hipEventSynchronize(t1));
+            conv->backward(conv, x, path ? y_g : y_i, gy, path ? gx_g : gx_i, B, &g);
+            NN_HIP_CHECK(hipEventRecord(t2, g.stream));
+            NN_HIP_CHECK(hipEventSynchronize(t2));
             float ms;
             NN_HIP_CHECK(hipEventElapsedTime(&ms, t0, t1));
             if (rep && ms < best[path]) best[path] = ms;
+            NN_HIP_CHECK(hipEventElapsedTime(&ms, t1, t2));
+            if (rep && ms < best[2 + path]) best[2 + path] = ms;
+            if (path == 0) {
+                for (int k = 0; k < 2; ++k)
+                    NN_HIP_CHECK(hipMemcpy(gsave[k], pl.items[k].grad, (size_t)pl.items[k].size * sizeof(float),
+                        hipMemcpyDeviceToDevice));
+            } else if (rep == reps) {
+                for (int k = 0; k < 2; ++k) {
+                    const double d = rel_diff(gsave[k], pl.items[k].grad, (size_t)pl.items[k].size);
+                    if (d > worst) worst = d;
+                }
+            }
         }
     }
     unsetenv("NNHIP_CONV_PATH");
-    const double d = rel_diff(y_i, y_g, n_out);
-    out_ms[0] = best[0];
-    out_ms[1] = best[1];
+    double d = rel_diff(y_i, y_g, n_out);
+    if (d > worst) worst = d;
+    d = rel_diff(gx_i, gx_g, n_in);
+    if (d > worst) worst = d;
+    for (int k = 0; k < 4; ++k) out_ms[k] = best[k];
+    param_list_free(&pl);
     conv->free(conv);
     (void)hipFree(x);
     (void)hipFree(y_i);
     (void)hipFree(y_g);
+    (void)hipFree(gy);
+    (void)hipFree(gx_i);
+    (void)hipFree(gx_g);
+    for (int k = 0; k < 2; ++k) (void)hipFree(gsave[k]);
+    (void)hipEventDestroy(t2);
     (void)hipEventDestroy(t0);
     (void)hipEventDestroy(t1);
     nn_context_destroy(&g);

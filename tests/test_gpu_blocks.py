@@ -57,14 +57,16 @@ def test_edm_block_matches_reference_composition(bc, shape):
                                   (16, 64, 64, 256, 256, 3, 1, 1, 0)],
                          ids=["cfg3", "cfg3-mp", "ddpm-256"])
 def test_conv_module_implicit_vs_gemm_path(bc, geom):
-    """The conv2d module's two forward paths agree within the reduction bar
-    (different fp32 summation orders of the same K*K*C_in products, relative
-    to max(|y|, rms(y))), and the implicit path's time is printed."""
+    """The conv2d module's two paths (implicit GEMMs on the matrix cores vs
+    im2col + rocBLAS GEMMs + col2im) agree on y, grad_in and the parameter
+    gradients within the reduction bar (different fp32 summation orders of the
+    same products, relative to max(|v|, rms(v))); both paths' times are
+    printed."""
     bc.nn_convcheck.argtypes = [C.c_int] * 10 + [C.POINTER(C.c_float)]
     bc.nn_convcheck.restype = C.c_double
     print(f"[case] conv module paths {geom}", flush=True)
-    ms = (C.c_float * 2)()
+    ms = (C.c_float * 4)()
     worst = bc.nn_convcheck(*geom, 3, ms)
-    print(f"conv2d {geom}: max rel diff {worst:.3e}; forward implicit {ms[0]:.3f} ms, im2col+rocBLAS {ms[1]:.3f} ms",
-          flush=True)
+    print(f"conv2d {geom}: max rel diff {worst:.3e}; forward implicit {ms[0]:.3f} ms vs im2col+rocBLAS {ms[1]:.3f} ms;"
+          f" backward implicit {ms[2]:.3f} ms vs im2col+rocBLAS+col2im {ms[3]:.3f} ms", flush=True)
     assert worst <= 1e-5
