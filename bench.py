@@ -173,14 +173,25 @@ class _Timer:
         return float(np.median(out))
 
 
-def _row(name, cfg, us, algo_bytes, note=""):
+FP32_MFMA_PEAK_TFLOPS = 157.3
+
+
+def _row(name, cfg, us, algo_bytes, note="", flops=None):
+    """One suite line.  HBM-bound rows report algorithmic GB/s against 8 TB/s;
+    matrix-core rows (flops given) report TFLOP/s against the fp32 MFMA peak."""
     gbs = algo_bytes / (us * 1e-6) / 1e9 if algo_bytes else None
     rec = {"row": name, "config": cfg, "us": round(us, 2), "algorithmic_bytes": int(algo_bytes),
            "GB_s": round(gbs, 1) if gbs else None, "hbm_frac": round(gbs / HBM_PEAK_GBS, 4) if gbs else None}
+    if flops:
+        tf = flops / (us * 1e-6) / 1e12
+        rec.update({"flops": int(flops), "TFLOP_s": round(tf, 1), "mfma_frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)})
     if note:
         rec["note"] = note
     print(json.dumps(rec), flush=True)
-    log(f"[suite] {name:34s} {us:9.2f} us  " + (f"{gbs:7.0f} GB/s ({gbs / HBM_PEAK_GBS:.3f})" if gbs else ""))
+    if flops:
+        log(f"[suite] {name:34s} {us:9.2f} us  {rec['TFLOP_s']:7.1f} TFLOP/s ({rec['mfma_frac']:.3f} of fp32 MFMA)")
+    else:
+        log(f"[suite] {name:34s} {us:9.2f} us  " + (f"{gbs:7.0f} GB/s ({gbs / HBM_PEAK_GBS:.3f})" if gbs else ""))
 
 
 def run_suite(L, nn, reps):
@@ -287,7 +298,34 @@ def run_suite(L, nn, reps):
          T.median_us(lambda: (L.dll.nnhip_memset_async(im.p, 0, 4 * Bn * H * Wd * Ci, stream),
                               L.launch_col2im(im.p, col.p, Bn, H, Wd, Ci, K, 1, 1, H, Wd, stream)), reps),
          4 * (ncol + Bn * H * Wd * Ci))
-    del col, im
+    del col
+    # cfg3 convolution on the matrix cores (the conv2d module's implicit-GEMM path)
+    Co = 128
+    KKC = K * K * Ci
+    conv_flops = 2.0 * Bn * H * Wd * Co * KKC
+    Wt = dev(rng.standard_normal(KKC * Co) / np.sqrt(KKC))
+    WTt, bias_c = L.alloc(KKC * Co), dev(0.1 * rng.standard_normal(Co))
+    yc, gyc, gxc, gwc = L.alloc(Bn * H * Wd * Co), dev(rng.standard_normal(Bn * H * Wd * Co)), \
+        L.alloc(Bn * H * Wd * Ci), L.alloc(KKC * Co)
+    wgws = L.alloc(max(1, L.nnhip_conv2d_wgrad_workspace(Bn, Ci, Co, K, H, Wd)))
+
+    def conv_fwd():
+        L.launch_transpose(WTt.p, Wt.p, KKC, Co, stream)
+        L.launch_conv2d_forward_implicit(yc.p, im.p, WTt.p, bias_c.p, None, Bn, H, Wd, Ci, Co, K, 1, 1, H, Wd,
+                                         stream)
+    _row("conv_fwd_implicit", "cfg3 3x3 128->128, + bias (transpose + implicit GEMM)", T.median_us(conv_fwd, reps),
+         4 * (Bn * H * Wd * (Ci + Co) + KKC * Co), "matrix-core bound", flops=conv_flops)
+    _row("conv_wgrad_implicit", "cfg3 dW = im2col(x)^T dy (split-M + fixed-order sum)",
+         T.median_us(lambda: L.launch_conv2d_weight_grad_implicit(gwc.p, im.p, gyc.p, Bn, H, Wd, Ci, Co, K, 1, 1, H,
+                                                                  Wd, wgws.p, stream), reps),
+         4 * (Bn * H * Wd * (Ci + Co) + KKC * Co), "matrix-core bound", flops=conv_flops)
+
+    def conv_dgrad():
+        L.launch_conv2d_flip_weights(WTt.p, Wt.p, K, Ci, Co, stream)
+        L.launch_conv2d_forward_implicit(gxc.p, gyc.p, WTt.p, None, None, Bn, H, Wd, Co, Ci, K, 1, 1, H, Wd, stream)
+    _row("conv_dgrad_implicit", "cfg3 dx = conv(dy, flipped kernel) (flip + implicit GEMM)", T.median_us(conv_dgrad, reps),
+         4 * (Bn * H * Wd * (Ci + Co) + KKC * Co), "matrix-core bound", flops=conv_flops)
+    del im, yc, gyc, gxc
 
     # cfg4: sinusoidal, LayerNorm, SiLU over the DDPM stack
     t = dev(rng.integers(0, 1000, 256))
