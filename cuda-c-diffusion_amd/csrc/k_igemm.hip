@@ -11,8 +11,8 @@
 // directly (a k-slice of 32 channels of one (kh, kw) is 128 contiguous bytes
 // of one input pixel).
 //
-// Workgroup tile 128 (m) x 128 (n), k in slices of 32; 4 waves of 64 x 64,
-// each a 2 x 2 grid of 32 x 32 MFMA accumulators (64 registers).  Per slice a
+// Workgroup tile 128 (m) x BN (n, 128 or 64), k in slices of 32; 4 waves of
+// 64 x BN/2, each a 2 x BN/64 grid of 32 x 32 MFMA accumulators.  Per slice a
 // thread loads 4 float4 of A and 4 of WT into registers, the slice before it
 // computes from LDS, then the registers go to the other LDS buffer (two
 // buffers of 2 x 16 KB; two workgroups fit a CU).  LDS tiles are [128 rows][8
@@ -37,7 +37,8 @@ namespace {
 
 using namespace nnk;
 
-constexpr int kBM = 128, kBN = 128, kBK = 32, kTpb = 256;
+constexpr int kBM = 128, kBK = 32, kTpb = 256;
+constexpr int kBNmin = 64;  // output-channel tiles of 128 or 64
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 struct ConvShape {
@@ -51,14 +52,16 @@ __device__ __forceinline__ int slot(int row, int chunk) { return row * 8 + (chun
 
 enum { kEpiNone = 0, kEpiBias = 1, kEpiGain = 2 };
 
-template <int EPI>
+template <int EPI, int BN>
 __global__ __launch_bounds__(kTpb, 2) void igemm_fwd(float* __restrict__ Y, const float* __restrict__ X,
     const float* __restrict__ WT, const float* __restrict__ bias, const float* __restrict__ gain, ConvShape sh) {
+    constexpr int UT = BN / 64;  // 32-column accumulator tiles per wave
+    constexpr int BQ = BN / 32;  // WT rows loaded per thread
     __shared__ float4 As[2][kBM * 8];
-    __shared__ float4 Bs[2][kBN * 8];
+    __shared__ float4 Bs[2][BN * 8];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int wm = w >> 1, wn = w & 1;
-    const int m0 = blockIdx.x * kBM, n0 = blockIdx.y * kBN;
+    const int m0 = blockIdx.x * kBM, n0 = blockIdx.y * BN;
     // loader role: chunk ch of rows r0 + 32 q
     const int ch = tid & 7, r0 = tid >> 3;
     int pix[4], ihb[4], iwb[4];
@@ -81,7 +84,7 @@ __global__ __launch_bounds__(kTpb, 2) void igemm_fwd(float* __restrict__ Y, cons
     // zeroed when stored): a branch around a load would make the compiler's
     // later waits drain the whole vector-memory counter, i.e. wait for the
     // next slice's loads before the current slice's MFMAs.
-    float4 ra[4], rb[4];
+    float4 ra[4], rb[BQ];
     bool aok[4];
     auto load = [&](int kt) {
         const int k0 = kt * kBK;
@@ -93,7 +96,7 @@ __global__ __launch_bounds__(kTpb, 2) void igemm_fwd(float* __restrict__ Y, cons
             aok[q] = rok[q] & ((unsigned)ih < (unsigned)sh.H) & ((unsigned)iw < (unsigned)sh.W);
             const int p = aok[q] ? pix[q] + ih * sh.W + iw : 0;
             ra[q] = ld4(X + (size_t)p * sh.Cin + ci);
-            rb[q] = ld4(wrow + q * wstep + k0);
+            if (q < BQ) rb[q] = ld4(wrow + q * wstep + k0);
         }
     };
     // Padding is zeroed by masking the bits (a select of whole float4 values
@@ -108,49 +111,51 @@ __global__ __launch_bounds__(kTpb, 2) void igemm_fwd(float* __restrict__ Y, cons
             v.z = __uint_as_float(__float_as_uint(ra[q].z) & mk);
             v.w = __uint_as_float(__float_as_uint(ra[q].w) & mk);
             As[buf][slot(r0 + 32 * q, ch)] = v;
-            Bs[buf][slot(r0 + 32 * q, ch)] = rb[q];
+            if (q < BQ) Bs[buf][slot(r0 + 32 * q, ch)] = rb[q];
         }
     };
 
-    f32x16 acc[2][2];
+    f32x16 acc[2][UT];
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int u = 0; u < 2; ++u) acc[t][u] = (f32x16){};
+        for (int u = 0; u < UT; ++u) acc[t][u] = (f32x16){};
     const int nk = sh.KKC / kBK;
     const int fr = lane & 31, fh = lane >> 5;
     // epilogue operands, loaded before the pipeline
-    float bn[2] = {0.0f, 0.0f}, g = 1.0f;
+    float bn[UT], g = 1.0f;
+#pragma unroll
+    for (int u = 0; u < UT; ++u) bn[u] = 0.0f;
     if constexpr (EPI == kEpiBias) {
-        bn[0] = bias[n0 + wn * 64 + fr];
-        bn[1] = bias[n0 + wn * 64 + 32 + fr];
+#pragma unroll
+        for (int u = 0; u < UT; ++u) bn[u] = bias[n0 + wn * (BN / 2) + 32 * u + fr];
     }
     if constexpr (EPI == kEpiGain) g = gain[0];
     auto compute = [&](int buf) {
 #pragma unroll
         for (int kq = 0; kq < 4; ++kq) {
             const int c = 2 * kq + fh;
-            float4 a[2], b[2];
+            float4 a[2], b[UT];
 #pragma unroll
             for (int t = 0; t < 2; ++t) a[t] = As[buf][slot(wm * 64 + 32 * t + fr, c)];
 #pragma unroll
-            for (int u = 0; u < 2; ++u) b[u] = Bs[buf][slot(wn * 64 + 32 * u + fr, c)];
+            for (int u = 0; u < UT; ++u) b[u] = Bs[buf][slot(wn * (BN / 2) + 32 * u + fr, c)];
 #pragma unroll
             for (int t = 0; t < 2; ++t)
 #pragma unroll
-                for (int u = 0; u < 2; ++u) acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t].x, b[u].x, acc[t][u], 0, 0, 0);
+                for (int u = 0; u < UT; ++u) acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t].x, b[u].x, acc[t][u], 0, 0, 0);
 #pragma unroll
             for (int t = 0; t < 2; ++t)
 #pragma unroll
-                for (int u = 0; u < 2; ++u) acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t].y, b[u].y, acc[t][u], 0, 0, 0);
+                for (int u = 0; u < UT; ++u) acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t].y, b[u].y, acc[t][u], 0, 0, 0);
 #pragma unroll
             for (int t = 0; t < 2; ++t)
 #pragma unroll
-                for (int u = 0; u < 2; ++u) acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t].z, b[u].z, acc[t][u], 0, 0, 0);
+                for (int u = 0; u < UT; ++u) acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t].z, b[u].z, acc[t][u], 0, 0, 0);
 #pragma unroll
             for (int t = 0; t < 2; ++t)
 #pragma unroll
-                for (int u = 0; u < 2; ++u) acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t].w, b[u].w, acc[t][u], 0, 0, 0);
+                for (int u = 0; u < UT; ++u) acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t].w, b[u].w, acc[t][u], 0, 0, 0);
         }
     };
     // slices: prologue, a branch-free steady loop (load next, compute current,
@@ -175,10 +180,10 @@ __global__ __launch_bounds__(kTpb, 2) void igemm_fwd(float* __restrict__ Y, cons
         if constexpr (EPI == kEpiGain) v = v * g;
         return v;
     };
-    float* yb = Y + (size_t)(m0 + wm * 64 + 4 * fh) * sh.Cout + n0 + wn * 64 + fr;
+    float* yb = Y + (size_t)(m0 + wm * 64 + 4 * fh) * sh.Cout + n0 + wn * (BN / 2) + fr;
     if (m0 + kBM <= sh.M) {
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
+        for (int u = 0; u < UT; ++u)
 #pragma unroll
             for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -186,7 +191,7 @@ __global__ __launch_bounds__(kTpb, 2) void igemm_fwd(float* __restrict__ Y, cons
                     yb[(size_t)(32 * t + 8 * (r >> 2) + (r & 3)) * sh.Cout + 32 * u] = out(t, u, r);
     } else {
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
+        for (int u = 0; u < UT; ++u)
 #pragma unroll
             for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -215,38 +220,49 @@ constexpr int kWgM = 32;  // m rows per stage
 
 __device__ __forceinline__ int wslot(int m, int chunk) { return m * 32 + (chunk ^ ((m & 1) << 3)); }
 
+template <int BN>
 __global__ __launch_bounds__(kTpb, 2) void igemm_wgrad(float* __restrict__ part, const float* __restrict__ X,
     const float* __restrict__ dY, ConvShape sh, int rows_per_split) {
+    constexpr int UT = BN / 64;       // 32-column accumulator tiles per wave
+    constexpr int DCH = BN / 4;       // float4 chunks per dY row
+    constexpr int DQ = kWgM * DCH / kTpb;  // dY loads per thread
     __shared__ float4 As[2][kWgM * 32];
-    __shared__ float4 Ds[2][kWgM * 32];
+    __shared__ float4 Ds[2][kWgM * DCH];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int wk = w >> 1, wn = w & 1;
-    const int k0 = blockIdx.x * 128, n0 = blockIdx.y * 128, z = blockIdx.z;
+    const int k0 = blockIdx.x * 128, n0 = blockIdx.y * BN, z = blockIdx.z;
     const int mbeg = z * rows_per_split;
     const int mend = min(sh.M, mbeg + rows_per_split);
-    // loader role: chunk ch (fixed k = k0 + 4 ch, fixed n = n0 + 4 ch), rows r0 + 8 q
+    // loader roles: A chunk ch (fixed k = k0 + 4 ch) of rows r0 + 8 q; dY chunk
+    // dch (fixed n = n0 + 4 dch) of rows dr0 + (kTpb / DCH) q
     const int ch = tid & 31, r0 = tid >> 5;
+    const int dch = tid % DCH, dr0 = tid / DCH;
     const int kc = k0 + 4 * ch;
     const bool kok = kc < sh.KKC;
     const int tap = kok ? kc / sh.Cin : 0, ci = kok ? kc - tap * sh.Cin : 0;
     const int kh = tap / sh.K, kw = tap - kh * sh.K;
-    const float* dcol = dY + n0 + 4 * ch;
+    const float* dcol = dY + n0 + 4 * dch;
 
-    float4 ra[4], rd[4];
-    bool aok[4], mok[4];
+    float4 ra[4], rd[DQ];
+    bool aok[4], dok[DQ];
     auto load = [&](int ms) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int m = ms + r0 + 8 * q;
-            mok[q] = m < mend;
-            const int mm = mok[q] ? m : 0;
+            const bool mok = m < mend;
+            const int mm = mok ? m : 0;
             const int ow = mm % sh.Wo, t = mm / sh.Wo;
             const int oh = t % sh.Ho, b = t / sh.Ho;
             const int ih = oh * sh.stride - sh.pad + kh, iw = ow * sh.stride - sh.pad + kw;
-            aok[q] = mok[q] & kok & ((unsigned)ih < (unsigned)sh.H) & ((unsigned)iw < (unsigned)sh.W);
+            aok[q] = mok & kok & ((unsigned)ih < (unsigned)sh.H) & ((unsigned)iw < (unsigned)sh.W);
             const int p = aok[q] ? (b * sh.H + ih) * sh.W + iw : 0;
             ra[q] = ld4(X + (size_t)p * sh.Cin + ci);
-            rd[q] = ld4(dcol + (size_t)mm * sh.Cout);
+        }
+#pragma unroll
+        for (int q = 0; q < DQ; ++q) {
+            const int m = ms + dr0 + (kTpb / DCH) * q;
+            dok[q] = m < mend;
+            rd[q] = ld4(dcol + (size_t)(dok[q] ? m : 0) * sh.Cout);
         }
     };
     auto mask4 = [](float4 v, bool ok) {
@@ -257,37 +273,40 @@ __global__ __launch_bounds__(kTpb, 2) void igemm_wgrad(float* __restrict__ part,
         v.w = __uint_as_float(__float_as_uint(v.w) & mk);
         return v;
     };
+    // dY rows hold DCH chunks; the odd-row xor 8 keeps the two half-waves'
+    // rows in different bank halves as for A (DCH >= 16)
+    auto dslot = [](int m, int chunk) { return m * DCH + (chunk ^ ((m & 1) << 3)); };
     auto store = [&](int buf) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            As[buf][wslot(r0 + 8 * q, ch)] = mask4(ra[q], aok[q]);
-            Ds[buf][wslot(r0 + 8 * q, ch)] = mask4(rd[q], mok[q]);
-        }
+        for (int q = 0; q < 4; ++q) As[buf][wslot(r0 + 8 * q, ch)] = mask4(ra[q], aok[q]);
+#pragma unroll
+        for (int q = 0; q < DQ; ++q) Ds[buf][dslot(dr0 + (kTpb / DCH) * q, dch)] = mask4(rd[q], dok[q]);
     };
-    f32x16 acc[2][2];
+    f32x16 acc[2][UT];
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int u = 0; u < 2; ++u) acc[t][u] = (f32x16){};
+        for (int u = 0; u < UT; ++u) acc[t][u] = (f32x16){};
     const int fr = lane & 31, fh = lane >> 5;
     const float* Af = reinterpret_cast<const float*>(&As[0][0]);
     const float* Df = reinterpret_cast<const float*>(&Ds[0][0]);
     // element (m, col) of a staged tile: float4 slot of its chunk, then the component
     auto elem = [](int m, int col) { return wslot(m, col >> 2) * 4 + (col & 3); };
+    auto delem = [&](int m, int col) { return dslot(m, col >> 2) * 4 + (col & 3); };
     auto compute = [&](int buf) {
-        const int base = buf * kWgM * 32 * 4;
+        const int abase = buf * kWgM * 32 * 4, dbase = buf * kWgM * DCH * 4;
 #pragma unroll
         for (int p = 0; p < kWgM / 2; ++p) {
             const int m = 2 * p + fh;
-            float a[2], d[2];
+            float a[2], d[UT];
 #pragma unroll
-            for (int t = 0; t < 2; ++t) a[t] = Af[base + elem(m, wk * 64 + 32 * t + fr)];
+            for (int t = 0; t < 2; ++t) a[t] = Af[abase + elem(m, wk * 64 + 32 * t + fr)];
 #pragma unroll
-            for (int u = 0; u < 2; ++u) d[u] = Df[base + elem(m, wn * 64 + 32 * u + fr)];
+            for (int u = 0; u < UT; ++u) d[u] = Df[dbase + delem(m, wn * (BN / 2) + 32 * u + fr)];
 #pragma unroll
             for (int t = 0; t < 2; ++t)
 #pragma unroll
-                for (int u = 0; u < 2; ++u) acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t], d[u], acc[t][u], 0, 0, 0);
+                for (int u = 0; u < UT; ++u) acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t], d[u], acc[t][u], 0, 0, 0);
         }
     };
     const int nst = (mend - mbeg + kWgM - 1) / kWgM;
@@ -304,9 +323,9 @@ __global__ __launch_bounds__(kTpb, 2) void igemm_wgrad(float* __restrict__ part,
         compute((nst - 1) & 1);
     }
     // partial tile: D[k][n], rows k = k0 + wk 64 + 32 t + 8 (r / 4) + 4 h + r % 4
-    float* pb = part + (size_t)z * sh.KKC * sh.Cout + (size_t)(k0 + wk * 64 + 4 * fh) * sh.Cout + n0 + wn * 64 + fr;
+    float* pb = part + (size_t)z * sh.KKC * sh.Cout + (size_t)(k0 + wk * 64 + 4 * fh) * sh.Cout + n0 + wn * (BN / 2) + fr;
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
+    for (int u = 0; u < UT; ++u)
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -330,8 +349,10 @@ struct WgradPlan {
     int S, rows;
 };
 
+int tile_n(int Cout) { return Cout % 128 == 0 ? 128 : 64; }
+
 WgradPlan wgrad_plan(int M, int KKC, int Cout) {
-    const int tiles = ((KKC + 127) / 128) * (Cout / 128);
+    const int tiles = ((KKC + 127) / 128) * (Cout / tile_n(Cout));
     // one round of resident workgroups (two per CU on 256 CUs)
     int S = tiles >= 512 ? 1 : 512 / tiles;
     const int smax = (M + kWgM - 1) / kWgM;
@@ -382,7 +403,7 @@ __global__ __launch_bounds__(256) void transpose_kernel(float* __restrict__ out,
 extern "C" {
 
 int nnhip_conv2d_implicit_supported(int C_in, int C_out) {
-    return C_in > 0 && C_out > 0 && C_in % kBK == 0 && C_out % kBN == 0;
+    return C_in > 0 && C_out > 0 && C_in % kBK == 0 && C_out % kBNmin == 0;
 }
 
 void launch_transpose(float* out, const float* in, int rows, int cols, hipStream_t s) {
@@ -401,7 +422,7 @@ void launch_conv2d_forward_implicit(float* Y, const float* X, const float* WT, c
     const char* what = "launch_conv2d_forward_implicit";
     NNK_REQUIRE(batch >= 0 && H > 0 && W > 0 && K > 0 && stride > 0 && pad >= 0, what, "%s: bad geometry", what);
     NNK_REQUIRE(nnhip_conv2d_implicit_supported(C_in, C_out), what,
-        "%s: needs C_in %% %d == 0 and C_out %% %d == 0 (C_in=%d C_out=%d)", what, kBK, kBN, C_in, C_out);
+        "%s: needs C_in %% %d == 0 and C_out %% %d == 0 (C_in=%d C_out=%d)", what, kBK, kBNmin, C_in, C_out);
     NNK_REQUIRE(H_out == (H + 2 * pad - K) / stride + 1 && W_out == (W + 2 * pad - K) / stride + 1 && H_out > 0 &&
                     W_out > 0,
         what, "%s: output size %dx%d does not match the geometry", what, H_out, W_out);
@@ -412,10 +433,18 @@ void launch_conv2d_forward_implicit(float* Y, const float* X, const float* WT, c
     NNK_REQUIRE(Y && X && WT, what, "%s: null pointer", what);
     NNK_REQUIRE(aligned16(X) && aligned16(WT), what, "%s: X and WT must be 16-byte aligned", what);
     ConvShape sh{batch, H, W, C_in, C_out, K, stride, pad, H_out, W_out, batch * H_out * W_out, K * K * C_in};
-    const dim3 grid((unsigned)((sh.M + kBM - 1) / kBM), (unsigned)(C_out / kBN));
-    if (bias) igemm_fwd<kEpiBias><<<grid, kTpb, 0, s>>>(Y, X, WT, bias, nullptr, sh);
-    else if (gain) igemm_fwd<kEpiGain><<<grid, kTpb, 0, s>>>(Y, X, WT, nullptr, gain, sh);
-    else igemm_fwd<kEpiNone><<<grid, kTpb, 0, s>>>(Y, X, WT, nullptr, nullptr, sh);
+    const int BN = tile_n(C_out);
+    const dim3 grid((unsigned)((sh.M + kBM - 1) / kBM), (unsigned)(C_out / BN));
+#define NNK_IGEMM_FWD(BN_)                                                                    \
+    if (bias) igemm_fwd<kEpiBias, BN_><<<grid, kTpb, 0, s>>>(Y, X, WT, bias, nullptr, sh);   \
+    else if (gain) igemm_fwd<kEpiGain, BN_><<<grid, kTpb, 0, s>>>(Y, X, WT, nullptr, gain, sh); \
+    else igemm_fwd<kEpiNone, BN_><<<grid, kTpb, 0, s>>>(Y, X, WT, nullptr, nullptr, sh);
+    if (BN == 128) {
+        NNK_IGEMM_FWD(128)
+    } else {
+        NNK_IGEMM_FWD(64)
+    }
+#undef NNK_IGEMM_FWD
     nnk_after_launch(what, s);
 }
 
@@ -431,7 +460,7 @@ void launch_conv2d_flip_weights(float* WF, const float* Wt, int K, int C_in, int
 }
 
 int nnhip_conv2d_wgrad_implicit_supported(int C_in, int C_out) {
-    return C_in > 0 && C_out > 0 && C_in % 4 == 0 && C_out % kBN == 0;
+    return C_in > 0 && C_out > 0 && C_in % 4 == 0 && C_out % kBNmin == 0;
 }
 
 size_t nnhip_conv2d_wgrad_workspace(int batch, int C_in, int C_out, int K, int H_out, int W_out) {
@@ -447,7 +476,7 @@ void launch_conv2d_weight_grad_implicit(float* gW, const float* X, const float* 
     const char* what = "launch_conv2d_weight_grad_implicit";
     NNK_REQUIRE(batch >= 0 && H > 0 && W > 0 && K > 0 && stride > 0 && pad >= 0, what, "%s: bad geometry", what);
     NNK_REQUIRE(nnhip_conv2d_wgrad_implicit_supported(C_in, C_out), what,
-        "%s: needs C_in %% 4 == 0 and C_out %% %d == 0 (C_in=%d C_out=%d)", what, kBN, C_in, C_out);
+        "%s: needs C_in %% 4 == 0 and C_out %% %d == 0 (C_in=%d C_out=%d)", what, kBNmin, C_in, C_out);
     NNK_REQUIRE(H_out == (H + 2 * pad - K) / stride + 1 && W_out == (W + 2 * pad - K) / stride + 1 && H_out > 0 &&
                     W_out > 0,
         what, "%s: output size %dx%d does not match the geometry", what, H_out, W_out);
@@ -473,8 +502,10 @@ void launch_conv2d_weight_grad_implicit(float* gW, const float* X, const float* 
             pooled = true;
         }
     }
-    const dim3 grid((unsigned)((KKC + 127) / 128), (unsigned)(C_out / kBN), (unsigned)p.S);
-    igemm_wgrad<<<grid, kTpb, 0, s>>>(part, X, dY, sh, p.rows);
+    const int BN = tile_n(C_out);
+    const dim3 grid((unsigned)((KKC + 127) / 128), (unsigned)(C_out / BN), (unsigned)p.S);
+    if (BN == 128) igemm_wgrad<128><<<grid, kTpb, 0, s>>>(part, X, dY, sh, p.rows);
+    else igemm_wgrad<64><<<grid, kTpb, 0, s>>>(part, X, dY, sh, p.rows);
     if (p.S > 1) {
         const long long n = (long long)KKC * C_out;
         wgrad_reduce<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(gW, part, p.S, n);

@@ -2,12 +2,12 @@
  * weight norm + gain).  Reference: src/conv2d.c:6-145.  Weights are
  * [K*K*C_in, C_out] row-major (conv2d.c:114-115).
  * Forward: the implicit-GEMM kernel on the matrix cores when the channel counts
- * allow it (C_in % 32 == 0, C_out % 128 == 0), with the bias or gain in its
+ * allow it (C_in % 32 == 0, C_out % 64 == 0), with the bias or gain in its
  * epilogue; otherwise im2col + rocBLAS GEMM + bias/gain pass, as the reference.
  * NNHIP_CONV_PATH=gemm forces the latter.  Backward: the weight gradient as
- * an implicit GEMM too (C_in % 4 == 0, C_out % 128 == 0), the stride-1 input
+ * an implicit GEMM too (C_in % 4 == 0, C_out % 64 == 0), the stride-1 input
  * gradient as the implicit forward of grad_out with the flipped kernel
- * (C_out % 32 == 0, C_in % 128 == 0); otherwise im2col + rocBLAS GEMMs and the
+ * (C_out % 32 == 0, C_in % 64 == 0); otherwise im2col + rocBLAS GEMMs and the
  * gather col2im, which needs no memset of grad_in. */
 #include <math.h>
 #include <string.h>

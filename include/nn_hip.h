@@ -237,7 +237,7 @@ void launch_spatial_modulate_act_backward(float* grad_in, float* grad_cond,
    launch_scale_by_scalar (src/conv2d.c:17-34).  WT is the [K*K*C_in, C_out]
    weight transposed to [C_out, K*K*C_in] (launch_transpose); y [batch*H_out*W_out,
    C_out] = conv + bias[n] (bias non-NULL) or conv * gain[0] (gain non-NULL) or
-   conv.  Needs C_in % 32 == 0 and C_out % 128 == 0
+   conv.  Needs C_in % 32 == 0 and C_out % 64 == 0
    (nnhip_conv2d_implicit_supported); x and WT 16-byte aligned. */
 void launch_conv2d_forward_implicit(float* y, const float* x, const float* WT, const float* bias,
     const float* gain, int batch, int H, int W, int C_in, int C_out, int K, int stride, int pad,
@@ -249,7 +249,7 @@ int nnhip_conv2d_implicit_supported(int C_in, int C_out);
    gemm_dW (src/conv2d.c:44-47).  The reduction over the batch*H_out*W_out
    rows is split over workgroups and the partials are added in a fixed order
    (`workspace` of nnhip_conv2d_wgrad_workspace floats, or NULL: library
-   scratch).  Needs C_in % 4 == 0 and C_out % 128 == 0; x, dy 16-byte aligned. */
+   scratch).  Needs C_in % 4 == 0 and C_out % 64 == 0; x, dy 16-byte aligned. */
 void launch_conv2d_weight_grad_implicit(float* gW, const float* x, const float* dy, int batch, int H,
     int W, int C_in, int C_out, int K, int stride, int pad, int H_out, int W_out, float* workspace,
     hipStream_t s);

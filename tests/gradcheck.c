@@ -281,6 +281,7 @@ int nn_gradcheck_run(int verbose)
     fails += check_module("conv3x3_implicit_mp", conv2d_create(&g_ctx, 128, 128, 3, 1, 1, 4, 4, B, 1, 1.0f), B,
         2e-2);
     fails += check_module("conv3x3_s2_implicit", conv2d_create(&g_ctx, 32, 128, 3, 2, 1, 5, 5, B, 0, 1.0f), B, 2e-2);
+    fails += check_module("conv3x3_implicit_c64", conv2d_create(&g_ctx, 64, 64, 3, 1, 1, 4, 4, B, 1, 1.0f), B, 2e-2);
     /* diffusion blocks with an embedding slot; the EDM block's emb_lin gain is
        zero at creation (src/cond_conv_residual.c:113), so it is set to 0.7
        here to exercise the modulation path */

@@ -23,6 +23,10 @@ GEOMS = [
     (2, 8, 8, 32, 256, 1, 1, 0),       # 1x1
     (1, 9, 9, 96, 128, 5, 1, 2),       # 5x5, C_in = 3 slices of 32
     (2, 16, 16, 256, 128, 4, 2, 1),    # even kernel, stride 2
+    # 64-wide output-channel tiles (C_out % 128 != 0)
+    (2, 8, 8, 64, 64, 3, 1, 1),
+    (3, 7, 5, 32, 192, 3, 1, 1),
+    (1, 8, 8, 448, 448, 3, 1, 1),      # a DDPM-UNet width
 ]
 
 
@@ -73,10 +77,13 @@ def test_conv_forward_implicit_refuses_unsupported_channels(L, nn):
     print("[case] implicit conv refusals", flush=True)
     assert L.nnhip_conv2d_implicit_supported(128, 128) == 1
     assert L.nnhip_conv2d_implicit_supported(3, 128) == 0
-    assert L.nnhip_conv2d_implicit_supported(128, 64) == 0
+    assert L.nnhip_conv2d_implicit_supported(128, 64) == 1
+    assert L.nnhip_conv2d_implicit_supported(128, 96) == 0
     dummy = L.alloc(64)
     with pytest.raises(nn.NnHipError):
         L.launch_conv2d_forward_implicit(dummy.p, dummy.p, dummy.p, None, None, 1, 4, 4, 3, 128, 3, 1, 1, 4, 4, None)
+    with pytest.raises(nn.NnHipError):
+        L.launch_conv2d_forward_implicit(dummy.p, dummy.p, dummy.p, None, None, 1, 4, 4, 32, 96, 3, 1, 1, 4, 4, None)
     with pytest.raises(nn.NnHipError):
         L.launch_conv2d_forward_implicit(dummy.p, dummy.p, dummy.p, None, None, 1, 4, 4, 32, 128, 3, 1, 1, 5, 4, None)
 
@@ -88,6 +95,8 @@ WGRAD_GEOMS = [
     (4, 15, 15, 12, 256, 3, 2, 1),     # stride 2, C_in = 12
     (2, 8, 8, 32, 128, 1, 1, 0),       # 1x1
     (1, 9, 9, 4, 128, 5, 1, 2),        # 5x5, C_in = 4
+    (4, 8, 8, 64, 64, 3, 1, 1),        # 64-wide output-channel tiles
+    (2, 6, 6, 12, 192, 3, 1, 1),
 ]
 
 
