@@ -132,6 +132,13 @@ def cpu_baseline(x, dy, gamma, beta, G, sample_b, reps=1):
         orc.groupnorm_backward_f32(dys, xs, gamma, beta, mu, rs, G, 3)
     dt = (time.perf_counter() - t0) / reps
     n = xs.size
+    # the same maths on one core, over one sample
+    orc.set_threads(1)
+    t0 = time.perf_counter()
+    y1, mu1, rs1 = orc.groupnorm_forward_f32(xs[:1], gamma, beta, G, 1e-5, 3)
+    orc.groupnorm_backward_f32(dys[:1], xs[:1], gamma, beta, mu1, rs1, G, 3)
+    dt1 = time.perf_counter() - t0
+    orc.set_threads(threads)
     return {
         "value": round(20.0 * n / dt / 1e9, 3),
         "unit": "GB/s",
@@ -141,6 +148,8 @@ def cpu_baseline(x, dy, gamma, beta, G, sample_b, reps=1):
                   f"{reps} rep(s), {dt * 1e3:.1f} ms per fwd+bwd, fp32 OpenMP transcription of "
                   f"src/kernels.cu:622-717 + Pade SiLU",
         "us_per_sample_step": round(dt / sample_b * 1e6, 1),
+        "value_1_thread": round(20.0 * xs[:1].size / dt1 / 1e9, 3),
+        "sample_1_thread": f"the same on 1 of the 256 samples with 1 thread, {dt1 * 1e3:.1f} ms",
     }
 
 

@@ -110,18 +110,21 @@ bool nnk_gns_launch(const void* fn, int P, void** args, hipStream_t s, const cha
 // (cached per device and kernel), capped and rounded down to whole units.
 int nnk_gns_grid(const void* fn, int key, size_t lds, int unit) {
     constexpr int kDev = 16, kKeys = 256;
-    static int occ_cache[kDev][kKeys];
-    static int cu_cache[kDev];
+    // per device and kernel: 0 = not yet queried, -1 = unusable, else the
+    // resident workgroups per CU (relaxed atomics: concurrent callers may both
+    // query, and store the same value)
+    static std::atomic<int> occ_cache[kDev][kKeys];
+    static std::atomic<int> cu_cache[kDev];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kDev || key < 0 || key >= kKeys) return 0;
-    if (occ_cache[dev][key] == 0) {
+    if (occ_cache[dev][key].load(std::memory_order_relaxed) == 0) {
         const hipError_t ea =
             lds ? hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) : hipSuccess;
         if (ea != hipSuccess) {
             (void)hipGetLastError();
             nnk_path_note("streaming GroupNorm kernel %d: LDS attribute of %zu bytes: %s", key, lds,
                 hipGetErrorString(ea));
-            occ_cache[dev][key] = -1;
+            occ_cache[dev][key].store(-1, std::memory_order_relaxed);
             return 0;
         }
         int occ = 0;
@@ -129,25 +132,27 @@ int nnk_gns_grid(const void* fn, int key, size_t lds, int unit) {
         if (eo != hipSuccess || occ <= 0) {
             (void)hipGetLastError();
             nnk_path_note("streaming GroupNorm kernel %d: occupancy %d (%s)", key, occ, hipGetErrorString(eo));
-            occ_cache[dev][key] = -1;
+            occ_cache[dev][key].store(-1, std::memory_order_relaxed);
             return 0;
         }
-        occ_cache[dev][key] = occ;
+        occ_cache[dev][key].store(occ, std::memory_order_relaxed);
     }
-    if (occ_cache[dev][key] < 0) return 0;
-    if (cu_cache[dev] == 0) {
+    const int occ = occ_cache[dev][key].load(std::memory_order_relaxed);
+    if (occ < 0) return 0;
+    if (cu_cache[dev].load(std::memory_order_relaxed) == 0) {
         int cus = 0;
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) {
             (void)hipGetLastError();
             return 0;
         }
-        cu_cache[dev] = cus;
+        cu_cache[dev].store(cus, std::memory_order_relaxed);
     }
-    long long P = (long long)occ_cache[dev][key] * cu_cache[dev];
+    const int cus = cu_cache[dev].load(std::memory_order_relaxed);
+    long long P = (long long)occ * cus;
     if (P > nnk::gns::kMaxGrid) P = nnk::gns::kMaxGrid;
     P = P / unit * unit;
     if (P <= 0)
         nnk_path_note("streaming GroupNorm kernel %d: %d resident workgroups < %d tiles per sample row", key,
-            occ_cache[dev][key] * cu_cache[dev], unit);
+            occ * cus, unit);
     return (int)P;
 }

@@ -20,12 +20,11 @@ struct ErrorRecord {
 thread_local ErrorRecord g_err;
 
 bool check_mode() {
-    static int mode = -1;
-    if (mode < 0) {
+    static const bool on = [] {  // read once (thread-safe static initialisation)
         const char* e = getenv("NNHIP_CHECK");
-        mode = (e && e[0] == '1') ? 1 : 0;
-    }
-    return mode == 1;
+        return e && e[0] == '1';
+    }();
+    return on;
 }
 
 }  // namespace
@@ -46,11 +45,10 @@ void nnk_set_error(int code, const char* fmt, ...) {
 
 // NNHIP_VERBOSE=1: report on stderr why a launcher left its fast path.
 void nnk_path_note(const char* fmt, ...) {
-    static int verbose = -1;
-    if (verbose < 0) {
+    static const bool verbose = [] {
         const char* e = getenv("NNHIP_VERBOSE");
-        verbose = (e && e[0] == '1') ? 1 : 0;
-    }
+        return e && e[0] == '1';
+    }();
     if (!verbose) return;
     va_list ap;
     va_start(ap, fmt);
