@@ -16,9 +16,9 @@
 // thread loads 4 float4 of A and 4 of WT into registers, the slice before it
 // computes from LDS, then the registers go to the other LDS buffer (two
 // buffers of 2 x 16 KB; two workgroups fit a CU).  LDS tiles are [128 rows][8
-// float4 chunks] with the chunk index xor-swizzled by the row, so the 128-bit
-// fragment reads of a wave (32 rows, one chunk per half-wave) and the tile
-// writes are both free of bank conflicts.
+// float4 chunks] with the chunk index xor-swizzled by the row (slot()), so the
+// 128-bit fragment reads of a wave (32 rows, one chunk per half-wave) and the
+// tile writes are both free of bank conflicts.
 //
 // Lane layout of v_mfma_f32_32x32x2f32 (checked on the device): lane l supplies
 // A[l % 32][l / 32] and B[l / 32][l % 32]; accumulator register r of lane l
@@ -47,8 +47,13 @@ struct ConvShape {
     int KKC;  // K * K * Cin
 };
 
-// float4 slot of (row, chunk) in a [128][8] tile.
-__device__ __forceinline__ int slot(int row, int chunk) { return row * 8 + (chunk ^ (row & 7)); }
+// float4 slot of (row, chunk) in a [128][8] tile.  The xor spreads any 8
+// consecutive rows of one chunk over the 8 chunk positions, and any 16
+// consecutive rows over distinct (row parity, position) pairs, so 128-bit
+// accesses whose lane groups cover 128 or 256 bytes of banks do not conflict.
+__device__ __forceinline__ int slot(int row, int chunk) {
+    return row * 8 + (chunk ^ (row & 7) ^ ((row >> 3) & 1));
+}
 
 enum { kEpiNone = 0, kEpiBias = 1, kEpiGain = 2 };
 
@@ -84,34 +89,39 @@ __global__ __launch_bounds__(kTpb, 2) void igemm_fwd(float* __restrict__ Y, cons
     // zeroed when stored): a branch around a load would make the compiler's
     // later waits drain the whole vector-memory counter, i.e. wait for the
     // next slice's loads before the current slice's MFMAs.
-    float4 ra[4], rb[BQ];
-    bool aok[4];
-    auto load = [&](int kt) {
+    // Two register sets: the slice two ahead is loaded while the next one is
+    // written to LDS, so a load has two slices of MFMA work to arrive.
+    struct Regs {
+        float4 a[4], b[BQ];
+        bool ok[4];
+    };
+    Regs R0, R1;
+    auto load = [&](int kt, Regs& R) {
         const int k0 = kt * kBK;
         const int khw = k0 / sh.Cin, ci = k0 - khw * sh.Cin + ch * 4;
         const int kh = khw / sh.K, kw = khw - kh * sh.K;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int ih = ihb[q] + kh, iw = iwb[q] + kw;
-            aok[q] = rok[q] & ((unsigned)ih < (unsigned)sh.H) & ((unsigned)iw < (unsigned)sh.W);
-            const int p = aok[q] ? pix[q] + ih * sh.W + iw : 0;
-            ra[q] = ld4(X + (size_t)p * sh.Cin + ci);
-            if (q < BQ) rb[q] = ld4(wrow + q * wstep + k0);
+            R.ok[q] = rok[q] & ((unsigned)ih < (unsigned)sh.H) & ((unsigned)iw < (unsigned)sh.W);
+            const int p = R.ok[q] ? pix[q] + ih * sh.W + iw : 0;
+            R.a[q] = ld4(X + (size_t)p * sh.Cin + ci);
+            if (q < BQ) R.b[q] = ld4(wrow + q * wstep + k0);
         }
     };
     // Padding is zeroed by masking the bits (a select of whole float4 values
     // becomes a select of their addresses, which puts them in scratch memory).
-    auto store = [&](int buf) {
+    auto store = [&](int buf, const Regs& R) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const unsigned mk = aok[q] ? 0xffffffffu : 0u;
+            const unsigned mk = R.ok[q] ? 0xffffffffu : 0u;
             float4 v;
-            v.x = __uint_as_float(__float_as_uint(ra[q].x) & mk);
-            v.y = __uint_as_float(__float_as_uint(ra[q].y) & mk);
-            v.z = __uint_as_float(__float_as_uint(ra[q].z) & mk);
-            v.w = __uint_as_float(__float_as_uint(ra[q].w) & mk);
+            v.x = __uint_as_float(__float_as_uint(R.a[q].x) & mk);
+            v.y = __uint_as_float(__float_as_uint(R.a[q].y) & mk);
+            v.z = __uint_as_float(__float_as_uint(R.a[q].z) & mk);
+            v.w = __uint_as_float(__float_as_uint(R.a[q].w) & mk);
             As[buf][slot(r0 + 32 * q, ch)] = v;
-            if (q < BQ) Bs[buf][slot(r0 + 32 * q, ch)] = rb[q];
+            if (q < BQ) Bs[buf][slot(r0 + 32 * q, ch)] = R.b[q];
         }
     };
 
@@ -131,45 +141,79 @@ __global__ __launch_bounds__(kTpb, 2) void igemm_fwd(float* __restrict__ Y, cons
         for (int u = 0; u < UT; ++u) bn[u] = bias[n0 + wn * (BN / 2) + 32 * u + fr];
     }
     if constexpr (EPI == kEpiGain) g = gain[0];
-    auto compute = [&](int buf) {
+    // Fragments of a k quarter (8 k: one 128-bit read per row tile) and the
+    // 16 MFMAs on them.  The next quarter's reads are issued before the
+    // current quarter's MFMAs (two fragment register sets; the scheduling
+    // barriers keep the compiler from sinking the reads below the MFMAs, which
+    // would leave the matrix core idle for the LDS latency of every quarter).
+    auto frag = [&](int buf, int kq, float4 (&a)[2], float4 (&b)[UT]) {
+        const int c = 2 * kq + fh;
 #pragma unroll
-        for (int kq = 0; kq < 4; ++kq) {
-            const int c = 2 * kq + fh;
-            float4 a[2], b[UT];
+        for (int t = 0; t < 2; ++t) a[t] = As[buf][slot(wm * 64 + 32 * t + fr, c)];
 #pragma unroll
-            for (int t = 0; t < 2; ++t) a[t] = As[buf][slot(wm * 64 + 32 * t + fr, c)];
-#pragma unroll
-            for (int u = 0; u < UT; ++u) b[u] = Bs[buf][slot(wn * (BN / 2) + 32 * u + fr, c)];
-#pragma unroll
-            for (int t = 0; t < 2; ++t)
-#pragma unroll
-                for (int u = 0; u < UT; ++u) acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t].x, b[u].x, acc[t][u], 0, 0, 0);
-#pragma unroll
-            for (int t = 0; t < 2; ++t)
-#pragma unroll
-                for (int u = 0; u < UT; ++u) acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t].y, b[u].y, acc[t][u], 0, 0, 0);
-#pragma unroll
-            for (int t = 0; t < 2; ++t)
-#pragma unroll
-                for (int u = 0; u < UT; ++u) acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t].z, b[u].z, acc[t][u], 0, 0, 0);
-#pragma unroll
-            for (int t = 0; t < 2; ++t)
-#pragma unroll
-                for (int u = 0; u < UT; ++u) acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t].w, b[u].w, acc[t][u], 0, 0, 0);
-        }
+        for (int u = 0; u < UT; ++u) b[u] = Bs[buf][slot(wn * (BN / 2) + 32 * u + fr, c)];
     };
-    // slices: prologue, a branch-free steady loop (load next, compute current,
-    // store next), last slice
-    load(0);
-    store(0);
+    auto mfmas = [&](const float4 (&a)[2], const float4 (&b)[UT]) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int u = 0; u < UT; ++u) acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t].x, b[u].x, acc[t][u], 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int u = 0; u < UT; ++u) acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t].y, b[u].y, acc[t][u], 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int u = 0; u < UT; ++u) acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t].z, b[u].z, acc[t][u], 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int u = 0; u < UT; ++u) acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t].w, b[u].w, acc[t][u], 0, 0, 0);
+    };
+    auto compute = [&](int buf) {
+        float4 a0[2], b0[UT], a1[2], b1[UT];
+        frag(buf, 0, a0, b0);
+        frag(buf, 1, a1, b1);
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(a0, b0);
+        __builtin_amdgcn_sched_barrier(0);
+        frag(buf, 2, a0, b0);
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(a1, b1);
+        __builtin_amdgcn_sched_barrier(0);
+        frag(buf, 3, a1, b1);
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(a0, b0);
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(a1, b1);
+    };
+    // Slices: prologue, a branch-free steady loop over pairs of slices (slice
+    // kt computes from LDS buffer kt % 2 while R[kt % 2] receives slice kt + 2
+    // and R[(kt + 1) % 2] goes to the other buffer; the second load of a pair
+    // is clamped to the last slice, a harmless reload), then the one or two
+    // slices left.
+    load(0, R0);
+    if (nk > 1) load(1, R1);
+    store(0, R0);
     __syncthreads();
-    for (int kt = 0; kt + 1 < nk; ++kt) {
-        load(kt + 1);
-        compute(kt & 1);
-        store((kt + 1) & 1);
+    int kt = 0;
+    for (; kt + 2 < nk; kt += 2) {
+        load(kt + 2, R0);
+        compute(0);
+        store(1, R1);
+        __syncthreads();
+        load(min(kt + 3, nk - 1), R1);
+        compute(1);
+        store(0, R0);
         __syncthreads();
     }
-    compute((nk - 1) & 1);
+    compute(0);
+    if (kt + 1 < nk) {
+        store(1, R1);
+        __syncthreads();
+        compute(1);
+    }
 
     // epilogue: lanes 0-31 and 32-63 each write 32 consecutive outputs of a
     // row.  A full row tile stores with no per-row test (a branch per store
@@ -293,20 +337,39 @@ __global__ __launch_bounds__(kTpb, 2) void igemm_wgrad(float* __restrict__ part,
     // element (m, col) of a staged tile: float4 slot of its chunk, then the component
     auto elem = [](int m, int col) { return wslot(m, col >> 2) * 4 + (col & 3); };
     auto delem = [&](int m, int col) { return dslot(m, col >> 2) * 4 + (col & 3); };
-    auto compute = [&](int buf) {
+    // Operands of m pair p, and their MFMAs.  Two operand register sets: the
+    // reads of pair p + 2 are issued right after the MFMAs of pair p (the
+    // scheduling barriers keep them there), so each pair's reads have the
+    // next pair's MFMAs to arrive.
+    auto wfrag = [&](int buf, int p, float (&a)[2], float (&d)[UT]) {
         const int abase = buf * kWgM * 32 * 4, dbase = buf * kWgM * DCH * 4;
+        const int m = 2 * p + fh;
 #pragma unroll
-        for (int p = 0; p < kWgM / 2; ++p) {
-            const int m = 2 * p + fh;
-            float a[2], d[UT];
+        for (int t = 0; t < 2; ++t) a[t] = Af[abase + elem(m, wk * 64 + 32 * t + fr)];
 #pragma unroll
-            for (int t = 0; t < 2; ++t) a[t] = Af[abase + elem(m, wk * 64 + 32 * t + fr)];
+        for (int u = 0; u < UT; ++u) d[u] = Df[dbase + delem(m, wn * (BN / 2) + 32 * u + fr)];
+    };
+    auto wmfma = [&](const float (&a)[2], const float (&d)[UT]) {
 #pragma unroll
-            for (int u = 0; u < UT; ++u) d[u] = Df[dbase + delem(m, wn * (BN / 2) + 32 * u + fr)];
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
-            for (int t = 0; t < 2; ++t)
+            for (int u = 0; u < UT; ++u) acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t], d[u], acc[t][u], 0, 0, 0);
+    };
+    auto compute = [&](int buf) {
+        float a0[2], d0[UT], a1[2], d1[UT];
+        wfrag(buf, 0, a0, d0);
+        wfrag(buf, 1, a1, d1);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int u = 0; u < UT; ++u) acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t], d[u], acc[t][u], 0, 0, 0);
+        for (int p = 0; p < kWgM / 2; p += 2) {
+            wmfma(a0, d0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (p + 2 < kWgM / 2) wfrag(buf, p + 2, a0, d0);
+            __builtin_amdgcn_sched_barrier(0);
+            wmfma(a1, d1);
+            __builtin_amdgcn_sched_barrier(0);
+            if (p + 3 < kWgM / 2) wfrag(buf, p + 3, a1, d1);
+            __builtin_amdgcn_sched_barrier(0);
         }
     };
     const int nst = (mend - mbeg + kWgM - 1) / kWgM;
