@@ -221,6 +221,48 @@ def test_cooperative_launch_matches_plain(L, rng, monkeypatch):
         assert_bits_equal(a, b, what)
 
 
+def test_cooperative_launches_on_two_streams(L, orc, rng, monkeypatch):
+    """Streaming GroupNorms issued on two streams at once, each with its own
+    workspace, in the cooperative mode that such callers select
+    (NNHIP_GN_COOPERATIVE=1): both results match the oracle and no wait ran
+    out of polls."""
+    print("[case] stream groupnorm cooperative, two streams", flush=True)
+    monkeypatch.setenv("NNHIP_GN_PATH", "stream")
+    monkeypatch.setenv("NNHIP_GN_COOPERATIVE", "1")
+    B, H, W, C, G = 2, 64, 64, 256, 32
+    HW = H * W
+    streams = [L.dll.nnhip_stream_create() for _ in range(2)]
+    try:
+        cases = []
+        for s in streams:
+            x, gamma, beta, dy = make_inputs(rng, B, H, W, C)
+            d = {"x": L.to_device(x), "dy": L.to_device(dy), "g": L.to_device(gamma), "b": L.to_device(beta),
+                 "y": L.alloc(x.size), "dx": L.alloc(x.size), "mu": L.alloc(B * G), "rs": L.alloc(B * G),
+                 "gg": L.alloc(C), "gb": L.alloc(C),
+                 "ws": zeroed(L, L.nnhip_groupnorm_backward_workspace(B, HW, C, G)), "s": s}
+            cases.append((x, gamma, beta, dy, d))
+        for _ in range(3):  # interleaved issue on the two streams
+            for *_, d in cases:
+                L.launch_groupnorm_act_forward_ws(d["y"].p, d["mu"].p, d["rs"].p, d["x"].p, d["g"].p, d["b"].p, B, HW,
+                                                  C, G, 1e-5, 3, d["ws"].p, d["s"])
+            for *_, d in cases:
+                L.launch_groupnorm_act_backward_ws(d["dx"].p, d["gg"].p, d["gb"].p, d["dy"].p, d["x"].p, d["g"].p,
+                                                   d["b"].p, d["mu"].p, d["rs"].p, B, HW, C, G, 3, d["ws"].p, d["s"])
+        for s in streams:
+            L.dll.nnhip_stream_synchronize(s)
+        L.sync()
+        for x, gamma, beta, dy, d in cases:
+            assert L.nnhip_groupnorm_workspace_status(d["ws"].p) == 0
+            y_ref, mu_ref, rs_ref = orc.groupnorm_forward(x, gamma, beta, G, 1e-5, 3)
+            assert rel_err(d["y"].download(shape=x.shape), y_ref) <= TOL
+            dx_ref, _, _ = orc.groupnorm_backward(dy, x, gamma, beta, mu_ref, rs_ref, G, 3)
+            assert rel_err(d["dx"].download(shape=x.shape), dx_ref) <= TOL
+    finally:
+        for s in streams:
+            L.dll.nnhip_stream_synchronize(s)
+            L.dll.nnhip_stream_destroy(s)
+
+
 def test_reg_path_switch_matches_stream(L, rng, monkeypatch):
     """NNHIP_GN_PATH=reg and =stream agree to the parity bar on a shape both take."""
     print("[case] stream vs register path", flush=True)
