@@ -185,12 +185,27 @@ class _Timer:
 FP32_MFMA_PEAK_TFLOPS = 157.3
 
 
-def _row(name, cfg, us, algo_bytes, note="", flops=None):
+def _cpu_us(cpu):
+    """Time a CPU restatement of the row once: cpu = (fn, scale, what); the
+    result is scaled from the bounded sample fn processes to the row's full
+    workload."""
+    fn, scale, what = cpu
+    t0 = time.perf_counter()
+    fn()
+    return (time.perf_counter() - t0) * 1e6 * scale, what
+
+
+def _row(name, cfg, us, algo_bytes, note="", flops=None, cpu=None):
     """One suite line.  HBM-bound rows report algorithmic GB/s against 8 TB/s;
-    matrix-core rows (flops given) report TFLOP/s against the fp32 MFMA peak."""
+    matrix-core rows (flops given) report TFLOP/s against the fp32 MFMA peak.
+    cpu: the oracle's restatement of the row on one host core (or numpy for a
+    GEMM), timed on a bounded sample and scaled to the row's workload."""
     gbs = algo_bytes / (us * 1e-6) / 1e9 if algo_bytes else None
     rec = {"row": name, "config": cfg, "us": round(us, 2), "algorithmic_bytes": int(algo_bytes),
            "GB_s": round(gbs, 1) if gbs else None, "hbm_frac": round(gbs / HBM_PEAK_GBS, 4) if gbs else None}
+    if cpu is not None:
+        cus, what = _cpu_us(cpu)
+        rec.update({"cpu_us": round(cus, 1), "cpu_sample": what, "gpu_speedup": round(cus / us, 1)})
     if flops:
         tf = flops / (us * 1e-6) / 1e12
         rec.update({"flops": int(flops), "TFLOP_s": round(tf, 1), "mfma_frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)})
@@ -203,11 +218,20 @@ def _row(name, cfg, us, algo_bytes, note="", flops=None):
         log(f"[suite] {name:34s} {us:9.2f} us  " + (f"{gbs:7.0f} GB/s ({gbs / HBM_PEAK_GBS:.3f})" if gbs else ""))
 
 
-def run_suite(L, nn, reps):
+def run_suite(L, nn, reps, with_cpu=True):
     rng = np.random.default_rng(SEED)
     stream = L.dll.nnhip_stream_create()
     T = _Timer(L, stream)
     f32 = np.float32
+    from oracle import oracle as orc
+    orc.set_threads(1)
+    hr = np.random.default_rng(SEED + 1)  # host-side samples for the CPU timings
+
+    def hn(*shape):
+        return hr.standard_normal(shape, dtype=f32)
+
+    def cpu(fn, scale, what):
+        return (fn, scale, what) if with_cpu else None
 
     def dev(a):
         return L.to_device(np.ascontiguousarray(a, dtype=f32))
@@ -224,29 +248,42 @@ def run_suite(L, nn, reps):
         L.launch_groupnorm_act_forward(y.p, mu.p, rs.p, x.p, g.p, bt.p, B, HW, C, G, 1e-5, 3, stream)
         L.launch_groupnorm_act_backward_ws(dx.p, gg.p, gb.p, dy.p, x.p, g.p, bt.p, mu.p, rs.p, B, HW, C, G, 3,
                                            ws.p, stream)
+    hx, hdy, hg, hb = hn(B, HW, C), hn(B, HW, C), (1 + 0.1 * hn(C)).astype(f32), (0.1 * hn(C)).astype(f32)
+
+    def gn1_cpu():
+        y_, m_, r_ = orc.groupnorm_forward_f32(hx, hg, hb, G, 1e-5, 3)
+        orc.groupnorm_backward_f32(hdy, hx, hg, hb, m_, r_, G, 3)
     _row("gn_silu_fwd_bwd", "cfg1 [8,32,32,128] G32", T.median_us(gn1, reps), 20 * B * HW * C,
-         "cache-resident: GB/s are not an HBM roofline claim")
+         "cache-resident: GB/s are not an HBM roofline claim",
+         cpu=cpu(gn1_cpu, 1.0, "full cfg1, fp32 transcription of src/kernels.cu:622-717 + SiLU, 1 thread"))
     del x, dy, y, dx
 
     # cfg2: EDM MP ops
     R, Cc = 128 * 32 * 32, 128
     a, b_ = dev(rng.standard_normal(R * Cc)), dev(rng.standard_normal(R * Cc))
     o = L.alloc(R * Cc)
+    ha, hb2 = hn(R // 8, Cc), hn(R // 8, Cc)  # one eighth of cfg2 on the CPU
+    wa, wb = orc.mp_sum_weights(0.3)
     _row("mp_sum", "cfg2 [128,32,32,128] t=0.3",
-         T.median_us(lambda: L.launch_mp_sum(o.p, a.p, b_.p, 0.3, R * Cc, stream), reps), 12 * R * Cc)
+         T.median_us(lambda: L.launch_mp_sum(o.p, a.p, b_.p, 0.3, R * Cc, stream), reps), 12 * R * Cc,
+         cpu=cpu(lambda: orc.weighted_sum(ha, hb2, wa, wb), 8.0, "1/8 of cfg2 x 8, 1 thread"))
     o2 = L.alloc(R * 2 * Cc)
     _row("mp_cat", "cfg2 -> [128,32,32,256]",
-         T.median_us(lambda: L.launch_mp_channel_cat(o2.p, a.p, b_.p, 0.3, R, Cc, Cc, stream), reps), 16 * R * Cc)
+         T.median_us(lambda: L.launch_mp_channel_cat(o2.p, a.p, b_.p, 0.3, R, Cc, Cc, stream), reps), 16 * R * Cc,
+         cpu=cpu(lambda: orc.mp_cat(ha, hb2, 0.3), 8.0, "1/8 of cfg2 x 8, 1 thread"))
+    hcat = hn(R // 8, 2 * Cc)
     _row("mp_channel_split", "cfg2 [128,32,32,256] -> 2x128",
          T.median_us(lambda: L.launch_mp_channel_split(a.p, b_.p, o2.p, 0.3, R, Cc, Cc, stream), reps),
-         16 * R * Cc)
+         16 * R * Cc, cpu=cpu(lambda: orc.mp_split(hcat, Cc, Cc, 0.3), 8.0, "1/8 of cfg2 x 8, 1 thread"))
     # EDM block neighbours at the cfg2 shape (src/cond_conv_residual.c:30-33, 46-49)
     cnd = dev(0.5 * rng.standard_normal(128 * Cc))
     gcd = L.alloc(128 * Cc)
     tmp = L.alloc(R * Cc)
+    hx16, hc16, hg16 = hn(16, 1024, Cc), (0.5 * hn(16, Cc)).astype(f32), hn(16, 1024, Cc)
     _row("spatial_modulate_mp_silu_fwd", "EDM block [128,32,32,128] fused",
          T.median_us(lambda: L.launch_spatial_modulate_act_forward(o.p, a.p, cnd.p, 128, 32, 32, Cc, 5, stream),
-                     reps), 8 * R * Cc)
+                     reps), 8 * R * Cc,
+         cpu=cpu(lambda: orc.spatial_modulate_act_forward(hx16, hc16, 5), 8.0, "16 of 128 samples x 8, 1 thread"))
 
     def ref_fwd():
         L.launch_spatial_modulate(tmp.p, a.p, cnd.p, 128, 32, 32, Cc, stream)
@@ -255,7 +292,9 @@ def run_suite(L, nn, reps):
          8 * R * Cc, "same algorithmic bytes as the fused row")
     _row("spatial_modulate_mp_silu_bwd", "EDM block [128,32,32,128] fused",
          T.median_us(lambda: L.launch_spatial_modulate_act_backward(o.p, gcd.p, b_.p, a.p, cnd.p, 128, 32, 32, Cc, 5,
-                                                                    None, stream), reps), 12 * R * Cc)
+                                                                    None, stream), reps), 12 * R * Cc,
+         cpu=cpu(lambda: orc.spatial_modulate_act_backward(hg16, hx16, hc16, 5), 8.0,
+                 "16 of 128 samples x 8, 1 thread"))
 
     def ref_bwd():
         L.launch_activation_backward(tmp.p, b_.p, o2.p, R * Cc, 5, stream)
@@ -266,13 +305,16 @@ def run_suite(L, nn, reps):
     del o2
     Kg, Co = 1152, 128
     W = dev(rng.standard_normal(Kg * Co))
+    hW, hM = hn(Kg, Co), hn(Kg, Co)
+    hWn = orc.weight_normalize(hW, 1e-4)
     _row("weight_normalize", "cfg2 W[1152,128] eps 1e-4",
          T.median_us(lambda: L.launch_weight_normalize(W.p, Kg, Co, 1e-4, stream), reps), 8 * Kg * Co,
-         "latency-bound")
+         "latency-bound", cpu=cpu(lambda: orc.weight_normalize(hW, 1e-4), 1.0, "full cfg2 weight, 1 thread"))
     M, gain, ggn = dev(rng.standard_normal(Kg * Co)), dev(np.ones(1)), L.alloc(1)
     _row("weight_normalize_backward", "cfg2 W[1152,128]",
          T.median_us(lambda: L.launch_weight_normalize_backward(M.p, W.p, gain.p, ggn.p, Kg, Co, stream), reps),
-         12 * Kg * Co, "latency-bound")
+         12 * Kg * Co, "latency-bound",
+         cpu=cpu(lambda: orc.weight_normalize_backward(hM, hWn, 1.0), 1.0, "full cfg2 weight, 1 thread"))
     wn_ws = L.alloc(int(L.nnhip_weight_normalize_backward_workspace(Co)))
     wn_ws.fill_bytes(0)
     _row("weight_normalize_backward_ws", "cfg2 W[1152,128], lent workspace",
@@ -282,14 +324,18 @@ def run_suite(L, nn, reps):
     sig = np.exp(-1.2 + 1.2 * rng.standard_normal(128)).clip(0.002, 80)
     xs, fr, ph = dev(np.log(sig) / 4), dev(rng.standard_normal(256)), dev(rng.uniform(0, 1, 256))
     emb = L.alloc(128 * 256)
+    hxs, hfr, hph = (np.log(sig) / 4).astype(f32), hn(256), hr.uniform(0, 1, 256).astype(f32)
     _row("mp_fourier", "cfg2 [128 x 256]",
          T.median_us(lambda: L.launch_mp_fourier(emb.p, xs.p, fr.p, ph.p, 128, 256, stream), reps),
-         4 * (128 + 512 + 128 * 256), "latency-bound")
+         4 * (128 + 512 + 128 * 256), "latency-bound",
+         cpu=cpu(lambda: orc.mp_fourier(hxs, hfr, hph), 1.0, "full cfg2, 1 thread"))
     act_a, act_o = a, o
     _row("mp_silu_fwd", "cfg2 [128,32,32,128]",
-         T.median_us(lambda: L.launch_activation_forward(act_o.p, act_a.p, R * Cc, 5, stream), reps), 8 * R * Cc)
+         T.median_us(lambda: L.launch_activation_forward(act_o.p, act_a.p, R * Cc, 5, stream), reps), 8 * R * Cc,
+         cpu=cpu(lambda: orc.act_forward(ha, 5), 8.0, "1/8 of cfg2 x 8, 1 thread"))
     _row("scale_by_scalar", "cfg2 GEMM out [131072,128]",
-         T.median_us(lambda: L.launch_scale_by_scalar(act_o.p, gain.p, R * Cc, stream), reps), 8 * R * Cc)
+         T.median_us(lambda: L.launch_scale_by_scalar(act_o.p, gain.p, R * Cc, stream), reps), 8 * R * Cc,
+         cpu=cpu(lambda: orc.scale_by_scalar(ha, 1.0), 8.0, "1/8 of cfg2 x 8, 1 thread"))
     del a, b_, o
 
     # cfg3: im2col / col2im 3x3 s1 p1, N=128, 32x32x128
@@ -297,12 +343,15 @@ def run_suite(L, nn, reps):
     ncol = Bn * H * Wd * K * K * Ci
     im = dev(rng.uniform(-1, 1, Bn * H * Wd * Ci))
     col = L.alloc(ncol)
+    him = hr.uniform(-1, 1, (16, H, Wd, Ci)).astype(f32)  # 16 of 128 images on the CPU
+    hcol = orc.im2col(him, K, 1, 1)
     _row("im2col", "cfg3 [128,32,32,128] 3x3 s1 p1",
          T.median_us(lambda: L.launch_im2col(col.p, im.p, Bn, H, Wd, Ci, K, 1, 1, H, Wd, stream), reps),
-         4 * (ncol + Bn * H * Wd * Ci))
+         4 * (ncol + Bn * H * Wd * Ci), cpu=cpu(lambda: orc.im2col(him, K, 1, 1), 8.0, "16 of 128 images x 8, 1 thread"))
     _row("col2im_set", "cfg3 (gather, no memset)",
          T.median_us(lambda: L.launch_col2im_set(im.p, col.p, Bn, H, Wd, Ci, K, 1, 1, H, Wd, stream), reps),
-         4 * (ncol + Bn * H * Wd * Ci))
+         4 * (ncol + Bn * H * Wd * Ci),
+         cpu=cpu(lambda: orc.col2im(hcol, him.shape, K, 1, 1), 8.0, "16 of 128 images x 8, 1 thread"))
     _row("col2im", "cfg3 (reference pair: memset + accumulate)",
          T.median_us(lambda: (L.dll.nnhip_memset_async(im.p, 0, 4 * Bn * H * Wd * Ci, stream),
                               L.launch_col2im(im.p, col.p, Bn, H, Wd, Ci, K, 1, 1, H, Wd, stream)), reps),
@@ -322,56 +371,74 @@ def run_suite(L, nn, reps):
         L.launch_transpose(WTt.p, Wt.p, KKC, Co, stream)
         L.launch_conv2d_forward_implicit(yc.p, im.p, WTt.p, bias_c.p, None, Bn, H, Wd, Ci, Co, K, 1, 1, H, Wd,
                                          stream)
+    hWt = (hn(KKC, Co) / np.sqrt(KKC)).astype(f32)
+    hgy = hn(16 * H * Wd, Co)
+    conv_cpu_note = f"16 of 128 images x 8: oracle im2col + numpy float32 matmul ({os.cpu_count()} host cores)"
     _row("conv_fwd_implicit", "cfg3 3x3 128->128, + bias (transpose + implicit GEMM)", T.median_us(conv_fwd, reps),
-         4 * (Bn * H * Wd * (Ci + Co) + KKC * Co), "matrix-core bound", flops=conv_flops)
+         4 * (Bn * H * Wd * (Ci + Co) + KKC * Co), "matrix-core bound", flops=conv_flops,
+         cpu=cpu(lambda: orc.im2col(him, K, 1, 1) @ hWt, 8.0, conv_cpu_note))
     _row("conv_wgrad_implicit", "cfg3 dW = im2col(x)^T dy (split-M + fixed-order sum)",
          T.median_us(lambda: L.launch_conv2d_weight_grad_implicit(gwc.p, im.p, gyc.p, Bn, H, Wd, Ci, Co, K, 1, 1, H,
                                                                   Wd, wgws.p, stream), reps),
-         4 * (Bn * H * Wd * (Ci + Co) + KKC * Co), "matrix-core bound", flops=conv_flops)
+         4 * (Bn * H * Wd * (Ci + Co) + KKC * Co), "matrix-core bound", flops=conv_flops,
+         cpu=cpu(lambda: orc.im2col(him, K, 1, 1).T @ hgy, 8.0, conv_cpu_note))
 
     def conv_dgrad():
         L.launch_conv2d_flip_weights(WTt.p, Wt.p, K, Ci, Co, stream)
         L.launch_conv2d_forward_implicit(gxc.p, gyc.p, WTt.p, None, None, Bn, H, Wd, Co, Ci, K, 1, 1, H, Wd, stream)
     _row("conv_dgrad_implicit", "cfg3 dx = conv(dy, flipped kernel) (flip + implicit GEMM)", T.median_us(conv_dgrad, reps),
-         4 * (Bn * H * Wd * (Ci + Co) + KKC * Co), "matrix-core bound", flops=conv_flops)
+         4 * (Bn * H * Wd * (Ci + Co) + KKC * Co), "matrix-core bound", flops=conv_flops,
+         cpu=cpu(lambda: orc.col2im(hgy @ hWt.T, him.shape, K, 1, 1), 8.0,
+                 f"16 of 128 images x 8: numpy float32 matmul + oracle col2im ({os.cpu_count()} host cores)"))
     del im, yc, gyc, gxc
 
     # cfg4: sinusoidal, LayerNorm, SiLU over the DDPM stack
     t = dev(rng.integers(0, 1000, 256))
     semb = L.alloc(256 * 256)
     lmp = float(f32(np.log(f32(10000.0))))
+    ht = hr.integers(0, 1000, 256).astype(f32)
     _row("sinusoidal", "cfg4 [256 x 256]",
          T.median_us(lambda: L.launch_sinusoidal(semb.p, t.p, 256, 256, lmp, stream), reps), 4 * (256 + 65536),
-         "latency-bound")
+         "latency-bound", cpu=cpu(lambda: orc.sinusoidal(ht, 256, lmp), 1.0, "full cfg4, 1 thread"))
     Rl, Cl = 65536, 256
     xl, dyl = dev(rng.standard_normal(Rl * Cl)), dev(rng.standard_normal(Rl * Cl))
     yl, dxl = L.alloc(Rl * Cl), L.alloc(Rl * Cl)
     gl, bl = dev(1 + 0.1 * rng.standard_normal(Cl)), dev(0.1 * rng.standard_normal(Cl))
     mul, rsl, ggl, gbl = L.alloc(Rl), L.alloc(Rl), L.alloc(Cl), L.alloc(Cl)
     wsl = L.alloc(L.nnhip_layernorm_backward_workspace(Rl, Cl))
+    hxl, hdyl = hn(Rl // 8, Cl), hn(Rl // 8, Cl)
+    hgl, hbl = (1 + 0.1 * hn(Cl)).astype(f32), (0.1 * hn(Cl)).astype(f32)
+    _, hmul, hrsl = orc.layernorm_forward(hxl, hgl, hbl, 1e-5)
     _row("layernorm_fwd", "cfg4 [65536, 256]",
          T.median_us(lambda: L.launch_layernorm_forward(yl.p, mul.p, rsl.p, xl.p, gl.p, bl.p, Rl, Cl, 1e-5, stream),
-                     reps), 8 * Rl * Cl)
+                     reps), 8 * Rl * Cl,
+         cpu=cpu(lambda: orc.layernorm_forward(hxl, hgl, hbl, 1e-5), 8.0, "1/8 of the rows x 8, 1 thread"))
     _row("layernorm_bwd", "cfg4 [65536, 256]",
          T.median_us(lambda: L.launch_layernorm_backward_ws(dxl.p, ggl.p, gbl.p, dyl.p, xl.p, gl.p, mul.p, rsl.p, Rl,
-                                                            Cl, wsl.p, stream), reps), 12 * Rl * Cl)
+                                                            Cl, wsl.p, stream), reps), 12 * Rl * Cl,
+         cpu=cpu(lambda: orc.layernorm_backward(hdyl, hxl, hgl, hmul, hrsl), 8.0, "1/8 of the rows x 8, 1 thread"))
     del xl, dyl, yl, dxl
     n4 = 256 * 64 * 64 * 256
     xa, ga = dev(rng.standard_normal(n4, dtype=f32)), L.alloc(n4)
     ya = L.alloc(n4)
+    h16 = hn(16, 4096, 256)  # 16 of 256 samples on the CPU
+    h16b = hn(16, 4096, 256)
     _row("silu_fwd", "cfg4 [256,64,64,256]",
-         T.median_us(lambda: L.launch_activation_forward(ya.p, xa.p, n4, 3, stream), max(5, reps // 4)), 8 * n4)
+         T.median_us(lambda: L.launch_activation_forward(ya.p, xa.p, n4, 3, stream), max(5, reps // 4)), 8 * n4,
+         cpu=cpu(lambda: orc.act_forward(h16, 3), 16.0, "16 of 256 samples x 16, 1 thread"))
     _row("silu_bwd", "cfg4 [256,64,64,256]",
          T.median_us(lambda: L.launch_activation_backward(ga.p, ya.p, xa.p, n4, 3, stream), max(5, reps // 4)),
-         12 * n4)
+         12 * n4, cpu=cpu(lambda: orc.act_backward(h16b, h16, 3), 16.0, "16 of 256 samples x 16, 1 thread"))
     # DDPM block neighbours at the cfg4 shape (src/conv_residual.c:33, 44-45)
     emb = dev(rng.standard_normal(256 * 256))
     gemb = L.alloc(256 * 256)
+    hemb = hn(16, 256)
     _row("spatial_add", "DDPM block [256,64,64,256] += [256,256]",
-         T.median_us(lambda: L.launch_spatial_add(ya.p, emb.p, 256, 64, 64, 256, stream), max(5, reps // 4)), 8 * n4)
+         T.median_us(lambda: L.launch_spatial_add(ya.p, emb.p, 256, 64, 64, 256, stream), max(5, reps // 4)), 8 * n4,
+         cpu=cpu(lambda: orc.spatial_add(h16, hemb), 16.0, "16 of 256 samples x 16, 1 thread"))
     _row("spatial_reduce_sum", "DDPM block [256,64,64,256] -> [256,256]",
          T.median_us(lambda: L.launch_spatial_reduce_sum(gemb.p, xa.p, 256, 64 * 64, 256, stream), max(5, reps // 4)),
-         4 * n4)
+         4 * n4, cpu=cpu(lambda: orc.spatial_reduce_sum(h16), 16.0, "16 of 256 samples x 16, 1 thread"))
     del xa, ga, ya
 
     # cfg5: fused Adam + EMA over the DDPM-UNet-like list
@@ -389,9 +456,16 @@ def run_suite(L, nn, reps):
         off += (n + 3) // 4 * 4  # keep every tensor 16-byte aligned
     plan = nn.make_plan(L, slots)
     w1 = float(f32(1) - f32(0.9999))
+    nsm = 1 << 22  # 4 Mi of the 35.1 M parameters on the CPU
+    hp, hgr, hm, hv, hsh = hn(nsm), hn(nsm), np.zeros(nsm, f32), np.zeros(nsm, f32), hn(nsm)
+
+    def adam_cpu():
+        p_, m_, v_ = orc.adam_step(hp, hm, hv, hgr, 1e-4, 0.9, 0.999, 1e-8, 0.1, 0.001)
+        orc.weighted_sum(hsh, p_, 0.9999, w1)
     _row("adam_ema_fused", f"cfg5 {len(sizes)} tensors / {total} params",
          T.median_us(lambda: L.launch_adam_ema_step(plan, 1e-4, 0.9, 0.999, 1e-8, 0.1, 0.001, 0.9999, w1, stream),
-                     reps), 36 * total)
+                     reps), 36 * total,
+         cpu=cpu(adam_cpu, total / nsm, "4 Mi parameters scaled to the list, Adam then EMA, 1 thread"))
 
     def per_tensor():
         for s_ in slots:
@@ -457,7 +531,7 @@ def main() -> int:
     info = L.device_info()
     if args.suite:
         log(f"[suite] device {info}")
-        run_suite(L, nn, max(5, args.steps))
+        run_suite(L, nn, max(5, args.steps), with_cpu=not args.no_cpu)
         return 0
     if args.calibrate:
         run_calibration(L, max(1, args.steps))
