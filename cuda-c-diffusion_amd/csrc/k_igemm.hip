@@ -45,6 +45,7 @@ struct ConvShape {
     int B, H, W, Cin, Cout, K, stride, pad, Ho, Wo;
     int M;    // B * Ho * Wo
     int KKC;  // K * K * Cin
+    FastDiv wo, ho;  // output pixel decode m -> (b, oh, ow)
 };
 
 // float4 slot of (row, chunk) in a [128][8] tile.  The xor spreads any 8
@@ -76,11 +77,12 @@ __global__ __launch_bounds__(kTpb, 2) void igemm_fwd(float* __restrict__ Y, cons
         const int m = m0 + r0 + 32 * q;
         rok[q] = m < sh.M;
         const int mm = rok[q] ? m : 0;
-        const int ow = mm % sh.Wo, t = mm / sh.Wo;
-        const int oh = t % sh.Ho, b = t / sh.Ho;
-        pix[q] = b * sh.H * sh.W;
-        ihb[q] = oh * sh.stride - sh.pad;
-        iwb[q] = ow * sh.stride - sh.pad;
+        uint32_t t, ow, b, oh;
+        sh.wo.divmod((uint32_t)mm, t, ow);
+        sh.ho.divmod(t, b, oh);
+        pix[q] = (int)b * sh.H * sh.W;
+        ihb[q] = (int)oh * sh.stride - sh.pad;
+        iwb[q] = (int)ow * sh.stride - sh.pad;
     }
     const float* wrow = WT + (size_t)(n0 + r0) * sh.KKC + ch * 4;
     const size_t wstep = (size_t)32 * sh.KKC;
@@ -295,11 +297,12 @@ __global__ __launch_bounds__(kTpb, 2) void igemm_wgrad(float* __restrict__ part,
             const int m = ms + r0 + 8 * q;
             const bool mok = m < mend;
             const int mm = mok ? m : 0;
-            const int ow = mm % sh.Wo, t = mm / sh.Wo;
-            const int oh = t % sh.Ho, b = t / sh.Ho;
-            const int ih = oh * sh.stride - sh.pad + kh, iw = ow * sh.stride - sh.pad + kw;
+            uint32_t t, ow, b, oh;
+            sh.wo.divmod((uint32_t)mm, t, ow);
+            sh.ho.divmod(t, b, oh);
+            const int ih = (int)oh * sh.stride - sh.pad + kh, iw = (int)ow * sh.stride - sh.pad + kw;
             aok[q] = mok & kok & ((unsigned)ih < (unsigned)sh.H) & ((unsigned)iw < (unsigned)sh.W);
-            const int p = aok[q] ? (b * sh.H + ih) * sh.W + iw : 0;
+            const int p = aok[q] ? ((int)b * sh.H + ih) * sh.W + iw : 0;
             ra[q] = ld4(X + (size_t)p * sh.Cin + ci);
         }
 #pragma unroll
@@ -495,7 +498,8 @@ void launch_conv2d_forward_implicit(float* Y, const float* X, const float* WT, c
     if (batch == 0) return;
     NNK_REQUIRE(Y && X && WT, what, "%s: null pointer", what);
     NNK_REQUIRE(aligned16(X) && aligned16(WT), what, "%s: X and WT must be 16-byte aligned", what);
-    ConvShape sh{batch, H, W, C_in, C_out, K, stride, pad, H_out, W_out, batch * H_out * W_out, K * K * C_in};
+    ConvShape sh{batch, H, W, C_in, C_out, K, stride, pad, H_out, W_out, batch * H_out * W_out, K * K * C_in,
+        FastDiv((uint32_t)W_out), FastDiv((uint32_t)H_out)};
     const int BN = tile_n(C_out);
     const dim3 grid((unsigned)((sh.M + kBM - 1) / kBM), (unsigned)(C_out / BN));
 #define NNK_IGEMM_FWD(BN_)                                                                    \
@@ -552,7 +556,8 @@ void launch_conv2d_weight_grad_implicit(float* gW, const float* X, const float* 
         return;
     }
     NNK_REQUIRE(aligned16(X) && aligned16(dY), what, "%s: X and dY must be 16-byte aligned", what);
-    ConvShape sh{batch, H, W, C_in, C_out, K, stride, pad, H_out, W_out, batch * H_out * W_out, KKC};
+    ConvShape sh{batch, H, W, C_in, C_out, K, stride, pad, H_out, W_out, batch * H_out * W_out, KKC,
+        FastDiv((uint32_t)W_out), FastDiv((uint32_t)H_out)};
     const WgradPlan p = wgrad_plan(sh.M, KKC, C_out);
     float* part = gW;
     bool pooled = false;
