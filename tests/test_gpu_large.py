@@ -95,3 +95,54 @@ def test_large_layernorm(L, orc, rng):
     assert rel_err(dxd.download(shape=x.shape), dx_ref) <= TOL
     assert rel_err(ggd.download(), gg_ref, floor=fg) <= TOL
     assert rel_err(gbd.download(), gb_ref, floor=fb) <= TOL
+
+
+def test_north_star_full_size_groupnorm_silu(L, orc):
+    """The bench workload at its full size, GN(32)+SiLU forward and backward on
+    [256, 64, 64, 256] (1 GiB per tensor) through the bench's launchers and
+    lent workspaces: y and dx of three samples against the oracle, and
+    dgamma/dbeta against the oracle's per-sample backward summed over all 256
+    samples (the batch sum is linear), at the 1e-5 bar."""
+    print("[case] north-star full size GN(32)+SiLU", flush=True)
+    B, HW, C, G = 256, 64 * 64, 256, 32
+    rng = np.random.default_rng(410293)
+    x = rng.standard_normal((B, HW, C), dtype=np.float32)
+    dy = rng.standard_normal((B, HW, C), dtype=np.float32)
+    gamma = (1.0 + 0.1 * rng.standard_normal(C)).astype(np.float32)
+    beta = (0.1 * rng.standard_normal(C)).astype(np.float32)
+    xd, dyd = L.to_device(x), L.to_device(dy)
+    yd, dxd = L.alloc(x.size), L.alloc(x.size)
+    gd, bd, ggd, gbd = L.to_device(gamma), L.to_device(beta), L.alloc(C), L.alloc(C)
+    mud, rsd = L.alloc(B * G), L.alloc(B * G)
+    fws = L.to_device(np.zeros(max(1, L.nnhip_groupnorm_forward_workspace(B, HW, C, G)), np.float32))
+    bws = L.to_device(np.zeros(L.nnhip_groupnorm_backward_workspace(B, HW, C, G), np.float32))
+    L.launch_groupnorm_act_forward_ws(yd.p, mud.p, rsd.p, xd.p, gd.p, bd.p, B, HW, C, G, 1e-5, 3, fws.p, None)
+    L.launch_groupnorm_act_backward_ws(dxd.p, ggd.p, gbd.p, dyd.p, xd.p, gd.p, bd.p, mud.p, rsd.p, B, HW, C, G, 3,
+                                       bws.p, None)
+    L.sync()
+    assert L.nnhip_groupnorm_workspace_status(fws.p) == 0
+    assert L.nnhip_groupnorm_workspace_status(bws.p) == 0
+    n = HW * C
+    for b in (0, 131, 255):
+        y_ref, mu_ref, rs_ref = orc.groupnorm_forward(x[b:b + 1], gamma, beta, G, 1e-5, 3)
+        y = np.empty(n, np.float32)
+        L.dll.nnhip_memcpy_dtoh(y.ctypes.data, yd.offset(b * n), 4 * n)
+        assert rel_err(y.reshape(y_ref.shape), y_ref) <= TOL
+        dx_ref, _, _ = orc.groupnorm_backward(dy[b:b + 1], x[b:b + 1], gamma, beta, mu_ref, rs_ref, G, 3)
+        dxs = np.empty(n, np.float32)
+        L.dll.nnhip_memcpy_dtoh(dxs.ctypes.data, dxd.offset(b * n), 4 * n)
+        assert rel_err(dxs.reshape(dx_ref.shape), dx_ref) <= TOL
+    gg_ref = np.zeros(C, np.float64)
+    gb_ref = np.zeros(C, np.float64)
+    sq_g = np.zeros(C, np.float64)
+    sq_b = np.zeros(C, np.float64)
+    for b in range(B):
+        _, mu_b, rs_b = orc.groupnorm_forward(x[b:b + 1], gamma, beta, G, 1e-5, 3)
+        _, gg_b, gb_b = orc.groupnorm_backward(dy[b:b + 1], x[b:b + 1], gamma, beta, mu_b, rs_b, G, 3)
+        gg_ref += gg_b
+        gb_ref += gb_b
+        sq_g += gg_b.astype(np.float64) ** 2
+        sq_b += gb_b.astype(np.float64) ** 2
+    # floor: the root of the summed squared per-sample terms bounds the sums' scale
+    assert rel_err(ggd.download(), gg_ref, floor=np.sqrt(sq_g)) <= TOL
+    assert rel_err(gbd.download(), gb_ref, floor=np.sqrt(sq_b)) <= TOL
