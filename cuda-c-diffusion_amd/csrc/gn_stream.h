@@ -648,8 +648,12 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
         meanA = meanN;
         rsA = rsN;
         pb ^= 1;
+        // The records of tile tB are requested as soon as this workgroup's
+        // own phase A of it is done, a whole round before phase B needs them
+        // (with a short phase A, as for the identity, a request at the top of
+        // the round would still be in flight at phase B).
+        records_prefetch(tB, r0, r1);
         while (tA + P < nt) {
-            records_prefetch(tB, r0, r1);
             take();
             lds_reads_done();
             issue_with_stats(tA + P, meanN, rsN);
@@ -662,9 +666,9 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
             meanA = meanN;
             rsA = rsN;
             pb ^= 1;
+            records_prefetch(tB, r0, r1);
         }
         if (tA < nt) {
-            records_prefetch(tB, r0, r1);
             take();
             phase_a(xv, gv, tA, meanA, rsA, pb);
             phase_b(tB, r0, r1, rsB, pb);
@@ -672,8 +676,8 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
             tB = tA;
             rsB = rsA;
             pb ^= 1;
+            records_prefetch(tB, r0, r1);
         }
-        records_prefetch(tB, r0, r1);
         phase_b(tB, r0, r1, rsB, pb);
     }
 
