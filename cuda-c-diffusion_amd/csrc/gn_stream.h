@@ -405,8 +405,10 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
     int tB = tA;
     tA += P;
     pb ^= 1;
+    // Tile tB's records are requested right after this workgroup's own
+    // phase A of it, a round before phase B reads them.
+    records_prefetch(tB, r0, r1);
     while (tA + P < nt) {
-        records_prefetch(tB, r0, r1);
         take();
         lds_reads_done();
         issue(tA + P);
@@ -416,17 +418,17 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
         tB = tA;
         tA += P;
         pb ^= 1;
+        records_prefetch(tB, r0, r1);
     }
     if (tA < nt) {
-        records_prefetch(tB, r0, r1);
         take();
         phase_a(v, tA, pb);
         phase_b(tB, r0, r1, pb);
         park();
         tB = tA;
         pb ^= 1;
+        records_prefetch(tB, r0, r1);
     }
-    records_prefetch(tB, r0, r1);
     phase_b(tB, r0, r1, pb);
 }
 
