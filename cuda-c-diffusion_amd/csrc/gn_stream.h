@@ -217,6 +217,19 @@ __device__ __forceinline__ void for_group_xor(F f) {
     for (int o = Gm::CW4; o < kWave; o <<= 1) f(o);
 }
 
+// Slot of wave w's partial pair of group g in the per-tile exchange
+// float2 [GT][NW].  The LDS has 64 four-byte banks, so a group's NW = 16
+// pairs cover 32 banks and groups g, g + 1 together cover all 64.  The
+// group leaders of one wave store at once (one lane per group); xoring the
+// slot with g / 2 sends them to distinct banks (at the plain index w every
+// even group would hit the same two banks).  The NW lanes that read one
+// group back still read a permutation of its 16 pairs.
+template <class Gm>
+__device__ __forceinline__ int wave_slot(int g, int w) {
+    static_assert((Gm::NW & (Gm::NW - 1)) == 0, "the slot xor needs a power-of-two wave count");
+    return w ^ ((g >> 1) & (Gm::NW - 1));
+}
+
 // ---------------------------------------------------------------------------
 // Forward.
 // ---------------------------------------------------------------------------
@@ -231,8 +244,8 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
     // Double-buffered by loop parity pb: consecutive phase A's (and phase B's)
     // may run with no barrier between them (first and last rounds), so a
     // buffer is rewritten only two phases later, past the other phase's barrier.
-    __shared__ float wred[2][GT][NW][2];        // [parity][group][wave][mean, M2]
-    __shared__ float stat[2][GT][2];
+    __shared__ float2 wred[2][GT][NW];          // [parity][group][wave slot] (mean, M2)
+    __shared__ float2 stat[2][GT];              // (mean, rstd)
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
     const int col = lane % CW4, row0 = wid * Gm::RW + lane / CW4;
     const int gl = col / Gm::CPG4;              // group of this lane within the tile
@@ -281,10 +294,7 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
             chan_merge_eq(m, q, __shfl_xor(m, o, kWave), __shfl_xor(q, o, kWave), cnt);
             cnt *= 2.0f;
         });
-        if (lane % CW4 % Gm::CPG4 == 0 && lane < CW4) {
-            wred[pb][gl][wid][0] = m;
-            wred[pb][gl][wid][1] = q;
-        }
+        if (lane % CW4 % Gm::CPG4 == 0 && lane < CW4) wred[pb][gl][wave_slot<Gm>(gl, wid)] = make_float2(m, q);
         lds_barrier();
         // the NW wave partials of group g merge on lanes (g, i = 0..NW-1) of
         // one wave in a fixed xor tree (the merge is symmetric, so every lane
@@ -292,7 +302,8 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
         static_assert(kWave % NW == 0, "a group's wave partials share a wave");
         if (tid < GT * NW) {
             const int g = tid / NW, i = tid % NW;
-            float mm = wred[pb][g][i][0], qq = wred[pb][g][i][1];
+            const float2 pq = wred[pb][g][wave_slot<Gm>(g, i)];
+            float mm = pq.x, qq = pq.y;
 #pragma unroll
             for (int o = 1; o < NW; o <<= 1) {
                 chan_merge_eq(mm, qq, __shfl_xor(mm, o, kWave), __shfl_xor(qq, o, kWave), cnt);
@@ -342,16 +353,15 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
                 chan_merge_eq(m, q, __shfl_xor(m, o, kWave), __shfl_xor(q, o, kWave), n);
                 n *= 2.0f;
             }
-            if (rj == 0) {
-                stat[pb][rg][0] = m;
-                stat[pb][rg][1] = rsqrtf(q / n + eps);
-            }
+            if (rj == 0) stat[pb][rg] = make_float2(m, rsqrtf(q / n + eps));
         }
         lds_barrier();
-        const float mean = stat[pb][gl][0], rs = stat[pb][gl][1];
+        const float2 st = stat[pb][gl];
+        const float mean = st.x, rs = st.y;
         if (t == 0 && tid < GT) {
-            mu_out[b * sh.G + cb * GT + tid] = stat[pb][tid][0];
-            rstd_out[b * sh.G + cb * GT + tid] = stat[pb][tid][1];
+            const float2 sg = stat[pb][tid];
+            mu_out[b * sh.G + cb * GT + tid] = sg.x;
+            rstd_out[b * sh.G + cb * GT + tid] = sg.y;
         }
         // gamma * (v - mean) * rs + beta = v * sc + sh0 per channel
         float4 sc, s0;
@@ -446,8 +456,8 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
     constexpr int NW = Gm::NW, NV = Gm::NV, GT = Gm::GT, TPB = Gm::TPB, CW4 = Gm::CW4;
     __shared__ float4 stage[2 * NV * TPB];      // x then dy of the next tile (direct-to-LDS loads)
     __shared__ float4 parked[2 * NV * TPB];     // xhat then g of the tile awaiting phase B
-    __shared__ float wred[2][GT][NW][2];        // double-buffered by loop parity, as in the forward
-    __shared__ float stat[2][GT][2];
+    __shared__ float2 wred[2][GT][NW];          // (S1, S2) partials, laid out as in the forward
+    __shared__ float2 stat[2][GT];              // group means of g and g * xhat
     __shared__ float cred[NW][CW4][8];          // per-wave dgamma/dbeta sums at the end (then the reducer's)
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
     const int col = lane % CW4, row0 = wid * Gm::RW + lane / CW4;
@@ -535,16 +545,14 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
             s1 += __shfl_xor(s1, o, kWave);
             s2 += __shfl_xor(s2, o, kWave);
         });
-        if (lane % CW4 % Gm::CPG4 == 0 && lane < CW4) {
-            wred[pb][gl][wid][0] = s1;
-            wred[pb][gl][wid][1] = s2;
-        }
+        if (lane % CW4 % Gm::CPG4 == 0 && lane < CW4) wred[pb][gl][wave_slot<Gm>(gl, wid)] = make_float2(s1, s2);
         lds_barrier();
         // wave partials of group g summed on lanes (g, i) in a fixed xor tree
         static_assert(kWave % NW == 0, "a group's wave partials share a wave");
         if (tid < GT * NW) {
             const int g = tid / NW, i = tid % NW;
-            float a = wred[pb][g][i][0], c = wred[pb][g][i][1];
+            const float2 ac = wred[pb][g][wave_slot<Gm>(g, i)];
+            float a = ac.x, c = ac.y;
 #pragma unroll
             for (int o = 1; o < NW; o <<= 1) {
                 a += __shfl_xor(a, o, kWave);
@@ -586,14 +594,12 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
                 a += __shfl_xor(a, o, kWave);
                 c += __shfl_xor(c, o, kWave);
             }
-            if (rj == 0) {
-                stat[pb][rg][0] = a * sh.inv_n;
-                stat[pb][rg][1] = c * sh.inv_n;
-            }
+            if (rj == 0) stat[pb][rg] = make_float2(a * sh.inv_n, c * sh.inv_n);
         }
         lds_barrier();
         // dx = rs * ((g - m1) - xhat * m2) = g * rs + (xhat * (-rs m2) + (-rs m1))
-        const float a1 = -rs * stat[pb][gl][0], a2 = -rs * stat[pb][gl][1];
+        const float2 st = stat[pb][gl];
+        const float a1 = -rs * st.x, a2 = -rs * st.y;
         float* dxs = dx + (size_t)b * sh.HW * sh.C + (size_t)(t * Gm::TP + row0) * sh.C + c0;
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
