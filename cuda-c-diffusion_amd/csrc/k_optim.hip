@@ -21,6 +21,7 @@ using namespace nnk;
 
 constexpr int kTpb = 256;
 constexpr int kChunk = 4096;  // elements per workgroup: 4 float4 per thread
+static_assert(kChunk % (4 * kTpb) == 0, "a full chunk is whole float4 slices of the workgroup");
 
 struct DevSlot {
     float* p;
@@ -46,41 +47,53 @@ __device__ __forceinline__ float adam_one(float& p, float& m, float& v, float g,
     return p;
 }
 
-template <bool NT>
-__global__ __launch_bounds__(kTpb) void adam_kernel(float* __restrict__ p, float* __restrict__ m,
-    float* __restrict__ v, const float* __restrict__ g, AdamArgs a, long long n, int vec) {
-    const long long start = (long long)blockIdx.x * kChunk;
-    const long long end = min(start + (long long)kChunk, n);
-    if (vec) {
-        const long long nv = (end - start) / 4;
-        for (long long q = threadIdx.x; q < nv; q += kTpb) {
-            const long long i = start + 4 * q;
-            float4 pp = ldS<NT>(p + i), mm = ldS<NT>(m + i), vv = ldS<NT>(v + i);
-            const float4 gg = ldS<NT>(g + i);
-            adam_one(pp.x, mm.x, vv.x, gg.x, a);
-            adam_one(pp.y, mm.y, vv.y, gg.y, a);
-            adam_one(pp.z, mm.z, vv.z, gg.z, a);
-            adam_one(pp.w, mm.w, vv.w, gg.w, a);
-            stS<NT>(p + i, pp);
-            stS<NT>(m + i, mm);
-            stS<NT>(v + i, vv);
+// One full chunk (kChunk elements, 16-byte aligned): every thread loads its
+// U float4 of each tensor before any arithmetic, so all of the chunk's loads
+// are in flight at once (a loop that stores p, m, v before loading the next
+// slice keeps one slice in flight, since the tensors may alias as far as the
+// compiler knows).  p_new feeds the EMA from registers.
+template <int MODE, bool NT, bool EMA>
+__device__ __forceinline__ void chunk_full(const DevSlot& t, long long start, const AdamArgs& a, float w0, float w1) {
+    constexpr int U = kChunk / 4 / kTpb;
+    float4 pp[U], mm[U], vv[U], gg[U], sh[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const long long i = start + 4LL * (threadIdx.x + u * kTpb);
+        pp[u] = ldS<NT>(t.p + i);
+        if constexpr (MODE != 2) {
+            mm[u] = ldS<NT>(t.m + i);
+            vv[u] = ldS<NT>(t.v + i);
+            gg[u] = ldS<NT>(t.g + i);
         }
-        const long long t = start + 4 * nv + threadIdx.x;
-        if (t < end) adam_one(p[t], m[t], v[t], g[t], a);
-    } else {
-        for (long long i = start + threadIdx.x; i < end; i += kTpb) adam_one(p[i], m[i], v[i], g[i], a);
+        if constexpr (EMA) sh[u] = ldS<NT>(t.shadow + i);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const long long i = start + 4LL * (threadIdx.x + u * kTpb);
+        if constexpr (MODE != 2) {
+            adam_one(pp[u].x, mm[u].x, vv[u].x, gg[u].x, a);
+            adam_one(pp[u].y, mm[u].y, vv[u].y, gg[u].y, a);
+            adam_one(pp[u].z, mm[u].z, vv[u].z, gg[u].z, a);
+            adam_one(pp[u].w, mm[u].w, vv[u].w, gg[u].w, a);
+            stS<NT>(t.p + i, pp[u]);
+            stS<NT>(t.m + i, mm[u]);
+            stS<NT>(t.v + i, vv[u]);
+        }
+        if constexpr (EMA) {
+            sh[u].x = w0 * sh[u].x + w1 * pp[u].x;
+            sh[u].y = w0 * sh[u].y + w1 * pp[u].y;
+            sh[u].z = w0 * sh[u].z + w1 * pp[u].z;
+            sh[u].w = w0 * sh[u].w + w1 * pp[u].w;
+            stS<NT>(t.shadow + i, sh[u]);
+        }
     }
 }
 
-// mode 0: Adam only, 1: Adam then EMA, 2: EMA only (shadow = w0*shadow + w1*p)
+// A chunk that is a tensor's last and partial, or of a tensor that is not
+// 16-byte aligned.
 template <int MODE, bool NT>
-__global__ __launch_bounds__(kTpb) void multi_tensor_kernel(const DevSlot* __restrict__ slots,
-    const int2* __restrict__ chunks, AdamArgs a, float w0, float w1) {
-    const int2 ch = chunks[blockIdx.x];
-    const DevSlot t = slots[ch.x];
-    const long long start = (long long)ch.y * kChunk;
-    const long long end = min(start + (long long)kChunk, t.n);
-    const bool ema = MODE != 0 && t.shadow != nullptr;
+__device__ __forceinline__ void chunk_any(const DevSlot& t, long long start, long long end, bool ema,
+    const AdamArgs& a, float w0, float w1) {
     if (t.vec) {
         const long long nv = (end - start) / 4;
         for (long long q = threadIdx.x; q < nv; q += kTpb) {
@@ -118,6 +131,34 @@ __global__ __launch_bounds__(kTpb) void multi_tensor_kernel(const DevSlot* __res
             if constexpr (MODE != 2) pn = adam_one(t.p[i], t.m[i], t.v[i], t.g[i], a);
             if (ema) t.shadow[i] = w0 * t.shadow[i] + w1 * pn;
         }
+    }
+}
+
+// Single tensor (the reference launcher): one chunk per workgroup.
+template <bool NT>
+__global__ __launch_bounds__(kTpb) void adam_kernel(float* __restrict__ p, float* __restrict__ m,
+    float* __restrict__ v, const float* __restrict__ g, AdamArgs a, long long n, int vec) {
+    const DevSlot t{p, m, v, g, nullptr, n, vec, 0};
+    const long long start = (long long)blockIdx.x * kChunk;
+    const long long end = min(start + (long long)kChunk, n);
+    if (vec && end - start == kChunk) chunk_full<0, NT, false>(t, start, a, 0.0f, 0.0f);
+    else chunk_any<0, NT>(t, start, end, false, a, 0.0f, 0.0f);
+}
+
+// mode 0: Adam only, 1: Adam then EMA, 2: EMA only (shadow = w0*shadow + w1*p)
+template <int MODE, bool NT>
+__global__ __launch_bounds__(kTpb) void multi_tensor_kernel(const DevSlot* __restrict__ slots,
+    const int2* __restrict__ chunks, AdamArgs a, float w0, float w1) {
+    const int2 ch = chunks[blockIdx.x];
+    const DevSlot t = slots[ch.x];
+    const long long start = (long long)ch.y * kChunk;
+    const long long end = min(start + (long long)kChunk, t.n);
+    const bool ema = MODE != 0 && t.shadow != nullptr;
+    if (t.vec && end - start == kChunk) {
+        if (ema) chunk_full<MODE, NT, MODE != 0>(t, start, a, w0, w1);
+        else if constexpr (MODE != 2) chunk_full<MODE, NT, false>(t, start, a, w0, w1);
+    } else {
+        chunk_any<MODE, NT>(t, start, end, ema, a, w0, w1);
     }
 }
 
