@@ -406,6 +406,7 @@ def run_suite(L, nn, reps, with_cpu=True):
     gl, bl = dev(1 + 0.1 * rng.standard_normal(Cl)), dev(0.1 * rng.standard_normal(Cl))
     mul, rsl, ggl, gbl = L.alloc(Rl), L.alloc(Rl), L.alloc(Cl), L.alloc(Cl)
     wsl = L.alloc(L.nnhip_layernorm_backward_workspace(Rl, Cl))
+    wsl.fill_bytes(0)
     hxl, hdyl = hn(Rl // 8, Cl), hn(Rl // 8, Cl)
     hgl, hbl = (1 + 0.1 * hn(Cl)).astype(f32), (0.1 * hn(Cl)).astype(f32)
     _, hmul, hrsl = orc.layernorm_forward(hxl, hgl, hbl, 1e-5)

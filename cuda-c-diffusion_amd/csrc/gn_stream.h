@@ -121,31 +121,6 @@ __device__ __forceinline__ void settle(const unsigned long long (&r)[N]) {
     for (int u = 0; u < N; ++u) asm volatile("" ::"v"(r[u]));
 }
 
-__device__ __forceinline__ unsigned long long tagged(unsigned long long tag, float v) {
-    return tag | (unsigned long long)__builtin_bit_cast(unsigned, v);
-}
-__device__ __forceinline__ void rec_store(unsigned long long* p, unsigned long long v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ unsigned long long rec_load(const unsigned long long* p) {
-    return __hip_atomic_load(const_cast<unsigned long long*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Poll one record until it carries `epoch`; bounded.
-__device__ __forceinline__ float rec_wait(const unsigned long long* p, unsigned long long r, unsigned epoch,
-    unsigned spin_limit, unsigned* err) {
-    unsigned n = 0;
-    while ((unsigned)(r >> 32) != epoch) {
-        if (++n > spin_limit) {
-            atomicOr(err, 1u);
-            break;
-        }
-        __builtin_amdgcn_s_sleep(1);
-        r = rec_load(p);
-    }
-    return __builtin_bit_cast(float, (unsigned)r);
-}
-
 // Chan merge of (na, ma, qa) with (nb, mb, qb).
 __device__ __forceinline__ void chan_merge(float& n, float& m, float& q, float nb, float mb, float qb) {
     const float nn = n + nb;
@@ -812,7 +787,6 @@ struct Plan {
 
 // Applicability and sizes; `bwd` selects the backward geometry.
 Plan make_plan(bool bwd, int B, int HW, int C, int G);
-unsigned next_epoch();
 }  // namespace gns
 }  // namespace nnk
 

@@ -62,13 +62,6 @@ Plan make_plan(bool bwd, int B, int HW, int C, int G) {
     return p;
 }
 
-unsigned next_epoch() {
-    static std::atomic<unsigned> epoch{0};
-    unsigned e = ++epoch;
-    if (e == 0) e = ++epoch;  // 0 is the value of a zero-filled workspace
-    return e;
-}
-
 }  // namespace gns
 }  // namespace nnk
 
@@ -82,7 +75,14 @@ __global__ void gns_clear(unsigned* p, size_t n) {
 
 }  // namespace
 
-void nnk_gns_clear_workspace(float* ws, size_t n_floats, hipStream_t s) {
+unsigned nnk_next_epoch() {
+    static std::atomic<unsigned> epoch{0};
+    unsigned e = ++epoch;
+    if (e == 0) e = ++epoch;  // 0 is the value of a zero-filled workspace
+    return e;
+}
+
+void nnk_clear_workspace(float* ws, size_t n_floats, hipStream_t s) {
     if (n_floats == 0) return;
     const size_t blocks = (n_floats + 255) / 256 < 4096 ? (n_floats + 255) / 256 : 4096;
     gns_clear<<<dim3((unsigned)blocks), dim3(256), 0, s>>>(reinterpret_cast<unsigned*>(ws), n_floats);

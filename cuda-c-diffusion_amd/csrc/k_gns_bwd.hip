@@ -26,7 +26,7 @@ bool launch(const Plan& p, float* dx, float* ggamma, float* gbeta, const float* 
     wk.rec = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(ws) + p.rec_offset);
     wk.part = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(ws) + p.part_offset);
     wk.tpart = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(ws) + p.tpart_offset);
-    unsigned epoch = next_epoch();
+    unsigned epoch = nnk_next_epoch();
     unsigned limit = kSpinLimit;
     void* args[] = {&dx, &ggamma, &gbeta, const_cast<float**>(&dy), const_cast<float**>(&x), const_cast<float**>(&gamma),
         const_cast<float**>(&beta), const_cast<float**>(&mu), const_cast<float**>(&rstd), &sh, &wk, &epoch,

@@ -26,7 +26,7 @@ bool launch(const Plan& p, float* y, float* mu, float* rstd, const float* x, con
     wk.rec = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(ws) + p.rec_offset);
     wk.part = nullptr;
     wk.tpart = nullptr;
-    unsigned epoch = next_epoch();
+    unsigned epoch = nnk_next_epoch();
     unsigned limit = kSpinLimit;
     void* args[] = {&y, &mu, &rstd, const_cast<float**>(&x), const_cast<float**>(&gamma),
         const_cast<float**>(&beta), &sh, &wk, &eps, &epoch, &limit};

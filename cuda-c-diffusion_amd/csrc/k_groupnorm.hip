@@ -13,7 +13,6 @@
 #include "gn_kernels.h"
 #include "gn_stream.h"
 
-void nnk_gns_clear_workspace(float* ws, size_t n_floats, hipStream_t s);
 
 namespace {
 
@@ -271,7 +270,7 @@ bool try_stream(bool bwd, int B, int HW, int C, int G, bool reg_ok, float* ws, h
     if (!w) {
         w = nnk_scratch_acquire(p.ws_floats, s, what);
         if (!w) return false;
-        nnk_gns_clear_workspace(w, p.ws_floats, s);
+        nnk_clear_workspace(w, p.ws_floats, s);
     }
     const bool ok = launch(w);
     if (!ws) nnk_scratch_release(w, s);

@@ -406,8 +406,18 @@ __global__ __launch_bounds__(256) void wgrad_reduce(float* __restrict__ gW, cons
     long long n) {
     const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
     if (i >= n) return;
+    // kB slices in flight, added in slice order
+    constexpr int kB = 8;
     float t = part[i];
-    for (int z = 1; z < S; ++z) t += part[(size_t)z * n + i];
+    int z = 1;
+    for (; z + kB <= S; z += kB) {
+        float v[kB];
+#pragma unroll
+        for (int u = 0; u < kB; ++u) v[u] = part[(size_t)(z + u) * n + i];
+#pragma unroll
+        for (int u = 0; u < kB; ++u) t += v[u];
+    }
+    for (; z < S; ++z) t += part[(size_t)z * n + i];
     gW[i] = t;
 }
 

@@ -335,7 +335,23 @@ __global__ __launch_bounds__(kTpb) void ln_colsum2(float* __restrict__ og, float
     const int c = blockIdx.x * kWave + lane;
     float sg = 0.0f, sb = 0.0f;
     if (c < C) {
-        for (int p = wid; p < P; p += kNw) {
+        // kB rows of each in flight, added in row order
+        constexpr int kB = 8;
+        int p = wid;
+        for (; p + (kB - 1) * kNw < P; p += kB * kNw) {
+            float vg[kB], vb[kB];
+#pragma unroll
+            for (int u = 0; u < kB; ++u) {
+                vg[u] = pg[(size_t)(p + u * kNw) * C + c];
+                vb[u] = pb[(size_t)(p + u * kNw) * C + c];
+            }
+#pragma unroll
+            for (int u = 0; u < kB; ++u) {
+                sg += vg[u];
+                sb += vb[u];
+            }
+        }
+        for (; p < P; p += kNw) {
             sg += pg[(size_t)p * C + c];
             sb += pb[(size_t)p * C + c];
         }

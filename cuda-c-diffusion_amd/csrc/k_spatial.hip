@@ -163,8 +163,18 @@ __global__ __launch_bounds__(kTpb) void spatial_segments_sum(float* __restrict__
     if (i >= (long long)B * C) return;
     const long long b = i / C, c = i % C;
     const float* p = part + b * S * C + c;
+    // kB segments in flight, added in segment order
+    constexpr int kB = 8;
     float t = p[0];
-    for (int s = 1; s < S; ++s) t += p[(size_t)s * C];
+    int s = 1;
+    for (; s + kB <= S; s += kB) {
+        float v[kB];
+#pragma unroll
+        for (int u = 0; u < kB; ++u) v[u] = p[(size_t)(s + u) * C];
+#pragma unroll
+        for (int u = 0; u < kB; ++u) t += v[u];
+    }
+    for (; s < S; ++s) t += p[(size_t)s * C];
     out[i] = t;
 }
 

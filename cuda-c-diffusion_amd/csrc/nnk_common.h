@@ -347,6 +347,43 @@ __host__ __device__ __forceinline__ bool aligned16(const void* p) {
     return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
 }
 
+// ---------------------------------------------------------------------------
+// Epoch-tagged 64-bit records: the exchange between workgroups of one launch.
+// A record is (launch epoch << 32 | float bits), stored and loaded with
+// relaxed agent-scope atomics (coherent across the XCDs' L2s).  A reader
+// accepts a record only when it carries its own launch's epoch, so no fence
+// has to order the writer's record before the writer's arrival count (an
+// agent-scope release writes back the whole L2).  The epoch is unique in the
+// process and never 0, so a zero-filled workspace, or one holding records of
+// earlier launches only, never passes for this launch's data.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ unsigned long long tagged(unsigned long long tag, float v) {
+    return tag | (unsigned long long)__builtin_bit_cast(unsigned, v);
+}
+__device__ __forceinline__ void rec_store(unsigned long long* p, unsigned long long v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned long long rec_load(const unsigned long long* p) {
+    return __hip_atomic_load(const_cast<unsigned long long*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Poll one record until it carries `epoch`, at most spin_limit times (each
+// poll sleeps first); past that set *err and return what is there.
+__device__ __forceinline__ float rec_wait(const unsigned long long* p, unsigned long long r, unsigned epoch,
+    unsigned spin_limit, unsigned* err) {
+    unsigned n = 0;
+    while ((unsigned)(r >> 32) != epoch) {
+        if (++n > spin_limit) {
+            atomicOr(err, 1u);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+        r = rec_load(p);
+    }
+    return __builtin_bit_cast(float, (unsigned)r);
+}
+
+
 }  // namespace nnk
 
 // ---------------------------------------------------------------------------
@@ -362,6 +399,11 @@ void nnk_path_note(const char* fmt, ...);
 // Stream-ordered scratch for launchers that need partial sums.
 float* nnk_scratch_acquire(size_t n_floats, hipStream_t s, const char* what);
 void nnk_scratch_release(float* p, hipStream_t s);
+// Launch epoch for tagged records: unique in the process, never 0.
+unsigned nnk_next_epoch();
+// Zero n_floats words of a workspace drawn from the scratch pool (a fill
+// kernel, so that the sequence can be captured in a graph).
+void nnk_clear_workspace(float* ws, size_t n_floats, hipStream_t s);
 
 #define NNK_REQUIRE(cond, what, ...)                         \
     do {                                                     \

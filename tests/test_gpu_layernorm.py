@@ -11,7 +11,9 @@ from helpers import TOL, rel_err
 
 pytestmark = pytest.mark.gpu
 
-SHAPES = [(256 * 16 * 16, 256), (2, 16), (37, 48), (5, 1000), (3, 1030), (64, 4), (1, 7), (130, 2048), (1, 1)]
+# (64 * 70 + 5, 64): 71 partial rows of 64 rows each, a last partial segment
+SHAPES = [(256 * 16 * 16, 256), (2, 16), (37, 48), (5, 1000), (3, 1030), (64, 4), (1, 7), (130, 2048), (1, 1),
+          (64 * 70 + 5, 64)]
 
 
 def _inputs(rng, R, C):
@@ -52,14 +54,17 @@ def test_layernorm_forward_backward(L, orc, rng, shape):
     assert rel_err(ggd.download(), gg_ref, floor=fg) <= TOL
     assert rel_err(gbd.download(), gb_ref, floor=fb) <= TOL
 
-    # workspace variant: identical results
+    # workspace variant: identical results, also from a second launch on the
+    # same workspace
     ws = L.alloc(max(1, L.nnhip_layernorm_backward_workspace(R, C)))
-    dx2, gg2, gb2 = L.alloc(x.size), L.alloc(C), L.alloc(C)
-    L.launch_layernorm_backward_ws(dx2.p, gg2.p, gb2.p, dyd.p, xd.p, gd.p, mud.p, rsd.p, R, C, ws.p, None)
-    L.sync()
-    assert np.array_equal(dx2.download(), dxd.download())
-    assert np.array_equal(gg2.download(), ggd.download())
-    assert np.array_equal(gb2.download(), gbd.download())
+    ws.fill_bytes(0)
+    for rep in range(2):
+        dx2, gg2, gb2 = L.alloc(x.size), L.alloc(C), L.alloc(C)
+        L.launch_layernorm_backward_ws(dx2.p, gg2.p, gb2.p, dyd.p, xd.p, gd.p, mud.p, rsd.p, R, C, ws.p, None)
+        L.sync()
+        assert np.array_equal(dx2.download(), dxd.download()), rep
+        assert np.array_equal(gg2.download(), ggd.download()), rep
+        assert np.array_equal(gb2.download(), gbd.download()), rep
 
 
 def test_layernorm_misaligned(L, orc, rng):
