@@ -166,10 +166,19 @@ class _Timer:
         self.L, self.stream = L, stream
         self.ev = [L.dll.nnhip_event_create() for _ in range(2)]
 
-    def median_us(self, fn, reps=20, warmup=3):
+    def median_us(self, fn, reps=20, warmup=3, warm_s=0.03):
+        """Median over `reps` launch sequences, each bracketed by events and
+        waited for.  The row first runs back to back for at least `warm_s`
+        seconds (and `warmup` times): after idle the device needs some
+        milliseconds of load to reach its steady clock, which a 300 us
+        matrix-core launch measured cold misses by up to ~20 %."""
         L = self.L
-        for _ in range(warmup):
+        t0, n = time.perf_counter(), 0
+        while n < warmup or time.perf_counter() - t0 < warm_s:
             fn()
+            n += 1
+            if n % 8 == 0:
+                L.dll.nnhip_stream_synchronize(self.stream)
         L.dll.nnhip_stream_synchronize(self.stream)
         out = []
         for _ in range(reps):
