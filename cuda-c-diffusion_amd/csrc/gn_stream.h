@@ -760,13 +760,16 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
 // Host side (k_gns_fwd.hip / k_gns_bwd.hip).
 // ---------------------------------------------------------------------------
 // Streaming geometry: 1024 threads, tiles of 32 float4 columns (128
-// channels); forward tiles of 128 pixel rows, backward of 64 (one tile of
-// each input tensor is 64 KB: the staged and the parked tile fill 128 KB of
-// the workgroup's LDS).
+// channels); forward tiles of 128 pixel rows (64 KB), backward of 64 (32 KB of
+// x and 32 KB of dy): the staged and the parked tile fill 128 KB of the
+// workgroup's LDS either way.  Measured alternative: forward tiles of whole
+// 256-channel rows (64 float4 columns x 64 rows, teams of 64) ran 411 us
+// against 372 us at the north-star shape.
 namespace nnk {
 namespace gns {
 constexpr int kTpb = 1024;
-constexpr int kCw4 = 32;
+constexpr int kFwdCw4 = 32;
+constexpr int kBwdCw4 = 32;
 constexpr int kFwdTp = 128;
 constexpr int kBwdTp = 64;
 constexpr int kMaxGrid = 1024;        // persistent workgroups at most

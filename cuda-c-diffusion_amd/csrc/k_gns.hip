@@ -20,6 +20,7 @@ Plan make_plan(bool bwd, int B, int HW, int C, int G) {
     if (cpg % 4 != 0) return p;
     const int cpg4 = cpg / 4;
     if (cpg4 != 1 && cpg4 != 2 && cpg4 != 4) return p;
+    const int kCw4 = bwd ? kBwdCw4 : kFwdCw4;
     if (C % (4 * kCw4) != 0) return p;
     const int TP = bwd ? kBwdTp : kFwdTp;
     if (HW % TP != 0) return p;

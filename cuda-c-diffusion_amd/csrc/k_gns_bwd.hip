@@ -13,7 +13,7 @@ using namespace nnk::gns;
 template <int ACT, int CPG4, int RPL, bool NT>
 bool launch(const Plan& p, float* dx, float* ggamma, float* gbeta, const float* dy, const float* x,
     const float* gamma, const float* beta, const float* mu, const float* rstd, float* ws, hipStream_t s) {
-    using Gm = Geom<kTpb, kBwdTp, kCw4, CPG4>;
+    using Gm = Geom<kTpb, kBwdTp, kBwdCw4, CPG4>;
     const void* fn = reinterpret_cast<const void*>(&gns_bwd<Gm, ACT, RPL, NT>);
     const size_t lds = 0;  // all LDS is static (stage, parked, reduction buffers)
     const int key = 128 + ((ACT * 3 + (CPG4 == 1 ? 0 : CPG4 == 2 ? 1 : 2)) * 2 + (RPL - 1)) * 2 + (NT ? 1 : 0);

@@ -13,7 +13,7 @@ using namespace nnk::gns;
 template <int ACT, int CPG4, int RPL, bool NT>
 bool launch(const Plan& p, float* y, float* mu, float* rstd, const float* x, const float* gamma,
     const float* beta, float eps, float* ws, hipStream_t s) {
-    using Gm = Geom<kTpb, kFwdTp, kCw4, CPG4>;
+    using Gm = Geom<kTpb, kFwdTp, kFwdCw4, CPG4>;
     const void* fn = reinterpret_cast<const void*>(&gns_fwd<Gm, ACT, RPL, NT>);
     const size_t lds = 0;  // all LDS is static (stage, parked, reduction buffers)
     const int key = ((ACT * 3 + (CPG4 == 1 ? 0 : CPG4 == 2 ? 1 : 2)) * 2 + (RPL - 1)) * 2 + (NT ? 1 : 0);
