@@ -264,6 +264,17 @@ __global__ __launch_bounds__(kTpb, 2) void igemm_fwd(float* __restrict__ Y, cons
 // ---------------------------------------------------------------------------
 constexpr int kWgM = 32;  // m rows per stage
 
+// XCD-aware tile order.  Workgroups are dispatched round-robin over the
+// device's 8 XCDs (workgroup L on XCD L % 8), each with its own L2.  Tile
+// L' = xcd_order(L) gives XCD x a contiguous range of tiles, so the k tiles
+// of one m split, which read the same X and dY rows, run in the same L2
+// instead of on different XCDs.  A bijection of [0, total) for any total.
+constexpr int kXcds = 8;
+__device__ __forceinline__ int xcd_order(int L, int total) {
+    const int x = L % kXcds, j = L / kXcds, q = total / kXcds, r = total % kXcds;
+    return x * q + min(x, r) + j;
+}
+
 __device__ __forceinline__ int wslot(int m, int chunk) { return m * 32 + (chunk ^ ((m & 1) << 3)); }
 
 template <int BN>
@@ -276,7 +287,10 @@ __global__ __launch_bounds__(kTpb, 2) void igemm_wgrad(float* __restrict__ part,
     __shared__ float4 Ds[2][kWgM * DCH];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int wk = w >> 1, wn = w & 1;
-    const int k0 = blockIdx.x * 128, n0 = blockIdx.y * BN, z = blockIdx.z;
+    // tile (k tile, n tile, split z), k tile fastest, in XCD-aware order
+    const int KT = (sh.KKC + 127) / 128, NT = sh.Cout / BN;
+    const int tl = xcd_order((int)blockIdx.x, (int)gridDim.x);
+    const int k0 = (tl % KT) * 128, n0 = ((tl / KT) % NT) * BN, z = tl / (KT * NT);
     const int mbeg = z * rows_per_split;
     const int mend = min(sh.M, mbeg + rows_per_split);
     // loader roles: A chunk ch (fixed k = k0 + 4 ch) of rows r0 + 8 q; dY chunk
@@ -581,7 +595,7 @@ void launch_conv2d_weight_grad_implicit(float* gW, const float* X, const float* 
         }
     }
     const int BN = tile_n(C_out);
-    const dim3 grid((unsigned)((KKC + 127) / 128), (unsigned)(C_out / BN), (unsigned)p.S);
+    const dim3 grid((unsigned)((KKC + 127) / 128) * (unsigned)(C_out / BN) * (unsigned)p.S);
     if (BN == 128) igemm_wgrad<128><<<grid, kTpb, 0, s>>>(part, X, dY, sh, p.rows);
     else igemm_wgrad<64><<<grid, kTpb, 0, s>>>(part, X, dY, sh, p.rows);
     if (p.S > 1) {
