@@ -703,24 +703,9 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
     constexpr int Q = TPB / NVAL;
     float(*chain)[NVAL] = reinterpret_cast<float(*)[NVAL]>(&cred[0][0][0]);
     {
-        const int v = tid % NVAL, q = tid / NVAL;
-        const unsigned long long* src = wk.part + (size_t)team * T * NVAL + v;
-        float acc = 0.0f;
-        int m = q;
-        constexpr int kBatch = 8;
-        for (; m + (kBatch - 1) * Q < T; m += kBatch * Q) {
-            unsigned long long r8[kBatch];
-#pragma unroll
-            for (int u = 0; u < kBatch; ++u) r8[u] = rec_load(src + (size_t)(m + u * Q) * NVAL);
-#pragma unroll
-            for (int u = 0; u < kBatch; ++u)
-                acc += rec_wait(src + (size_t)(m + u * Q) * NVAL, r8[u], epoch, spin_limit, wk.err);
-        }
-        for (; m < T; m += Q) {
-            const unsigned long long* p = src + (size_t)m * NVAL;
-            acc += rec_wait(p, rec_load(p), epoch, spin_limit, wk.err);
-        }
-        chain[q][v] = acc;
+        const int v = tid % NVAL, q = tid / NVAL;  // q is uniform over the wave (NVAL >= 64)
+        const unsigned long long* src = wk.part + ((size_t)team * T + q) * NVAL + v;
+        chain[q][v] = rec_sum<16>(src, (size_t)Q * NVAL, (T - q + Q - 1) / Q, epoch, spin_limit, wk.err);
     }
     __syncthreads();
     for (int v = tid; v < NVAL; v += TPB) {
@@ -743,12 +728,9 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
     for (int i = tid; i < 2 * sh.C; i += TPB) {
         const int d = i / sh.C, c = i % sh.C;
         const int cbc = c / (CW4 * 4), cl = c % (CW4 * 4);
-        float acc = 0.0f;
-        for (int k = cbc; k < nteams; k += NCB) {
-            const unsigned long long* p = wk.tpart + (size_t)k * NVAL + d * (CW4 * 4) + cl;
-            acc += rec_wait(p, rec_load(p), epoch, spin_limit, wk.err);
-        }
-        (d ? gbeta : ggamma)[c] = acc;
+        const unsigned long long* p = wk.tpart + (size_t)cbc * NVAL + d * (CW4 * 4) + cl;
+        (d ? gbeta : ggamma)[c] = rec_sum<4>(p, (size_t)NCB * NVAL, (nteams - cbc + NCB - 1) / NCB, epoch,
+                                             spin_limit, wk.err);
     }
     if (tid == 0) __hip_atomic_store(wk.count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

@@ -383,6 +383,42 @@ __device__ __forceinline__ float rec_wait(const unsigned long long* p, unsigned 
     return __builtin_bit_cast(float, (unsigned)r);
 }
 
+// Sum of the n tagged records p[0], p[stride], ... in index order, KB loads
+// in flight.  The records of a batch that do not carry `epoch` yet are loaded
+// again together, so a batch costs one round trip per poll rather than one
+// per late record; past spin_limit polls *err is set and the sum is taken as
+// it stands.  n must be uniform over the wave.
+template <int KB>
+__device__ __forceinline__ float rec_sum(const unsigned long long* p, size_t stride, int n, unsigned epoch,
+    unsigned spin_limit, unsigned* err) {
+    float acc = 0.0f;
+    for (int m = 0; m < n; m += KB) {
+        const int nb = n - m < KB ? n - m : KB;
+        unsigned long long r[KB];
+#pragma unroll
+        for (int u = 0; u < KB; ++u)
+            if (u < nb) r[u] = rec_load(p + (size_t)(m + u) * stride);
+        for (unsigned polls = 0;; ++polls) {
+            bool late = false;
+#pragma unroll
+            for (int u = 0; u < KB; ++u) late |= u < nb && (unsigned)(r[u] >> 32) != epoch;
+            if (!late) break;
+            if (polls >= spin_limit) {
+                atomicOr(err, 1u);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+            for (int u = 0; u < KB; ++u)
+                if (u < nb && (unsigned)(r[u] >> 32) != epoch) r[u] = rec_load(p + (size_t)(m + u) * stride);
+        }
+#pragma unroll
+        for (int u = 0; u < KB; ++u)
+            if (u < nb) acc += __builtin_bit_cast(float, (unsigned)r[u]);
+    }
+    return acc;
+}
+
 
 }  // namespace nnk
 
