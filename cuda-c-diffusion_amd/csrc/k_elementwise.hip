@@ -16,8 +16,13 @@ namespace {
 
 using namespace nnk;
 
+// One float4 per thread and one-shot workgroups: measured at 1 GiB per tensor,
+// this streams 1-read/1-write at 0.79-0.83 of the HBM peak against 0.70-0.77
+// with four float4 per thread, and a grid-stride loop over a capped grid was
+// slower still (0.57-0.70): new workgroups are dispatched in address order,
+// which keeps the set of open DRAM pages small.
 constexpr int kTpb = 256;
-constexpr int kUnroll = 4;
+constexpr int kUnroll = 1;
 constexpr long long kPerBlock = (long long)kTpb * kUnroll;
 
 inline unsigned blocks_for(long long units) {

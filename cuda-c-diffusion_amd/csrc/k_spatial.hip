@@ -31,7 +31,7 @@ namespace {
 using namespace nnk;
 
 constexpr int kTpb = 256;
-constexpr int kUnroll = 4;
+constexpr int kUnroll = 1;  // one float4 per thread, one-shot grid (as k_elementwise.hip)
 
 enum { kOpAdd = 0, kOpMod = 1 };
 
@@ -185,9 +185,10 @@ bool shape_ok(const char* what, int B, int HW, int C) {
     return true;
 }
 
+// One-shot grid (the kernels keep a grid-stride loop, so any grid is correct).
 unsigned ew_grid(long long units, int per_block) {
     long long g = (units + per_block - 1) / per_block;
-    if (g > 8192) g = 8192;
+    if (g > (1LL << 30)) g = 1LL << 30;
     return (unsigned)(g < 1 ? 1 : g);
 }
 
