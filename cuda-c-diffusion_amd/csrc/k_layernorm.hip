@@ -445,7 +445,7 @@ void launch_layernorm_forward(float* y, float* mu, float* rstd, const float* x, 
     NNK_REQUIRE(y && mu && rstd && x && gamma && beta, what, "%s: null pointer", what);
     const int nv = fast_nv(C, y, x, gamma, beta);
     if (nv == 1) {
-        constexpr int RB = 4;
+        constexpr int RB = 1;
         if (use_nt(8LL * batch * C))
             ln_fwd_wave<1, RB, true><<<(unsigned)((batch + kNw * RB - 1) / (kNw * RB)), kTpb, 0, s>>>(y, mu, rstd, x, gamma, beta, batch, C, eps);
         else

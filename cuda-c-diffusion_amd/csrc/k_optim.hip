@@ -5,7 +5,7 @@
 // src/ema.c:29-35 (weighted_sum with decay, 1-decay).
 //
 // Multi-tensor form: the plan holds a device table of tensors and a list of
-// 4096-element chunks (tensor, chunk index); one workgroup updates one chunk,
+// 1024-element chunks (tensor, chunk index); one workgroup updates one chunk,
 // so a whole parameter list is one launch instead of one per tensor.  Per
 // parameter the fused step moves 36 bytes (read p, g, m, v, shadow; write p,
 // m, v, shadow); p_new feeds the EMA from registers.  Large plans stream all
@@ -20,7 +20,7 @@ namespace {
 using namespace nnk;
 
 constexpr int kTpb = 256;
-constexpr int kChunk = 4096;  // elements per workgroup: 4 float4 per thread
+constexpr int kChunk = 1024;  // elements per workgroup: one float4 per thread
 static_assert(kChunk % (4 * kTpb) == 0, "a full chunk is whole float4 slices of the workgroup");
 
 struct DevSlot {
