@@ -21,7 +21,14 @@ namespace {
 using namespace nnk;
 
 constexpr int kTpb = 256;
-constexpr int kUnroll = 4;
+// One unit per thread on a one-shot grid for the generic im2col and for
+// col2im (col2im_set at cfg3: 113 -> 105 us against four units per thread).
+constexpr int kUnroll = 1;
+// Passes in flight per thread in im2col_rows_kernel for K != 3.  The rows
+// kernel keeps all passes of a tile in one workgroup: one pass per workgroup
+// (one float4 per thread) measured 142 us against 113 us at cfg3, its nine
+// taps of an image row then being read on different XCDs.
+constexpr int kRowsBatch = 4;
 constexpr long long kPerBlock = (long long)kTpb * kUnroll;
 
 struct ConvGeom {
@@ -67,7 +74,7 @@ __global__ __launch_bounds__(kTpb) void im2col_kernel(float* __restrict__ col,
 // (b, oh*stride - pad, ow*stride - pad) comes from an LDS table.  Bit-exact.
 constexpr int kMaxRowsPerTile = 64;
 // NB = passes whose loads are in flight together: K*K for the common 3x3
-// kernel (all nine), kUnroll otherwise.
+// kernel (all nine), kRowsBatch otherwise.
 template <int NB, bool NT>
 __global__ __launch_bounds__(kTpb) void im2col_rows_kernel(float* __restrict__ col,
     const float* __restrict__ im, ConvGeom g, int rows, int CV, FastDiv div_k, FastDiv div_kk,
@@ -243,8 +250,8 @@ void launch_im2col(float* col, const float* im, int batch, int H, int W, int C, 
         const FastDiv dkk((uint32_t)(K * K));
         if (K == 3 && nt) im2col_rows_kernel<9, true><<<tiles, kTpb, 0, s>>>(col, im, g, (int)rows, CV, dk, dkk, dwo, dho);
         else if (K == 3) im2col_rows_kernel<9, false><<<tiles, kTpb, 0, s>>>(col, im, g, (int)rows, CV, dk, dkk, dwo, dho);
-        else if (nt) im2col_rows_kernel<kUnroll, true><<<tiles, kTpb, 0, s>>>(col, im, g, (int)rows, CV, dk, dkk, dwo, dho);
-        else im2col_rows_kernel<kUnroll, false><<<tiles, kTpb, 0, s>>>(col, im, g, (int)rows, CV, dk, dkk, dwo, dho);
+        else if (nt) im2col_rows_kernel<kRowsBatch, true><<<tiles, kTpb, 0, s>>>(col, im, g, (int)rows, CV, dk, dkk, dwo, dho);
+        else im2col_rows_kernel<kRowsBatch, false><<<tiles, kTpb, 0, s>>>(col, im, g, (int)rows, CV, dk, dkk, dwo, dho);
     } else if (vec) {
         if (nt) im2col_kernel<4, true><<<blocks_for(units), kTpb, 0, s>>>(col, im, g, units, drow, dcv, dk, dwo, dho);
         else im2col_kernel<4, false><<<blocks_for(units), kTpb, 0, s>>>(col, im, g, units, drow, dcv, dk, dwo, dho);
