@@ -59,6 +59,7 @@ _SIGS = {
     "nnhip_device_synchronize": (I, [], False),
     "nnhip_stream_create": (P, [], False),
     "nnhip_stream_destroy": (I, [P], False),
+    "nnhip_stream_scratch_release": (None, [P], False),
     "nnhip_stream_synchronize": (I, [P], False),
     "nnhip_event_create": (P, [], False),
     "nnhip_event_destroy": (I, [P], False),

@@ -435,6 +435,7 @@ void nnk_path_note(const char* fmt, ...);
 // Stream-ordered scratch for launchers that need partial sums.
 float* nnk_scratch_acquire(size_t n_floats, hipStream_t s, const char* what);
 void nnk_scratch_release(float* p, hipStream_t s);
+void nnk_scratch_forget_stream(hipStream_t s);
 // Launch epoch for tagged records: unique in the process, never 0.
 unsigned nnk_next_epoch();
 // Zero n_floats words of a workspace drawn from the scratch pool (a fill

@@ -154,6 +154,20 @@ float* nnk_scratch_acquire(size_t n_floats, hipStream_t s, const char* what) {
     return static_cast<float*>(slot->p);
 }
 
+// Drop stream s's cached block (freed in stream order).  Called before the
+// stream goes away: a later stream could otherwise be handed the same handle
+// value, find the slot and use the block while the old stream's work on it is
+// still pending.
+void nnk_scratch_forget_stream(hipStream_t s) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    for (int i = 0; i < g_nslots; ++i) {
+        if (g_slots[i].stream != s) continue;
+        if (g_slots[i].p) (void)hipFreeAsync(g_slots[i].p, s);
+        g_slots[i] = g_slots[--g_nslots];
+        --i;
+    }
+}
+
 void nnk_scratch_release(float* p, hipStream_t s) {
     if (!p) return;
     std::lock_guard<std::mutex> lock(g_scratch_mu);
@@ -172,8 +186,9 @@ __global__ __launch_bounds__(256) void fill_f32_kernel(float* __restrict__ p, fl
 }
 
 // ---------------------------------------------------------------------------
-// Calibration copy: the same 4 x float4 per thread access pattern as the
-// streaming elementwise kernels.
+// Calibration copy for the HBM byte counters: a plain streaming copy, four
+// float4 per thread.  What the counters read per byte moved does not depend
+// on the access pattern, only that every byte is read and written once.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void copy_f32_kernel(float* __restrict__ dst,
     const float* __restrict__ src, long long n4, long long n) {
@@ -256,7 +271,12 @@ hipStream_t nnhip_stream_create(void) {
     return s;
 }
 
-int nnhip_stream_destroy(hipStream_t s) { return (int)hipStreamDestroy(s); }
+int nnhip_stream_destroy(hipStream_t s) {
+    if (s) nnk_scratch_forget_stream(s);
+    return (int)hipStreamDestroy(s);
+}
+
+void nnhip_stream_scratch_release(hipStream_t s) { nnk_scratch_forget_stream(s); }
 int nnhip_stream_synchronize(hipStream_t s) { return (int)hipStreamSynchronize(s); }
 
 hipEvent_t nnhip_event_create(void) {

@@ -45,7 +45,13 @@ int nnhip_device_synchronize(void);
 
 /* ---- streams and events ---- */
 hipStream_t nnhip_stream_create(void); /* NULL stream on failure */
+/* Also drops the launch layer's cached scratch block of s. */
 int nnhip_stream_destroy(hipStream_t s);
+/* The launchers without a workspace argument keep one scratch block per
+   (device, stream) until the process ends.  Call this (it frees the block in
+   stream order) before destroying a stream with hipStreamDestroy directly;
+   nnhip_stream_destroy does it itself. */
+void nnhip_stream_scratch_release(hipStream_t s);
 int nnhip_stream_synchronize(hipStream_t s);
 hipEvent_t nnhip_event_create(void);
 int nnhip_event_destroy(hipEvent_t e);

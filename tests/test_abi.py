@@ -85,20 +85,28 @@ def test_launchers_keep_reference_argument_order(nn):
 
 def test_host_refusals_record_an_error(nn):
     """Shapes the kernels cannot take are refused on the host and recorded in
-    the error record (the reference would launch and read out of bounds)."""
+    the error record (the reference would launch and read out of bounds).
+    Each case must be refused by the host check itself, before any launch:
+    the pointers are dummies that a kernel would fault on, so the test checks
+    for the refusal's own code and message (a launch that failed for another
+    reason, such as no device here, would not match)."""
     L = nn.lib()
     L.last_error()  # clear
     dummy = ctypes.c_void_p(16)  # never dereferenced: the shape check comes first
     cases = [
-        ("launch_groupnorm_forward", (dummy, dummy, dummy, dummy, dummy, dummy, 1, 4, 10, 4, 1e-5, None)),
-        ("launch_groupnorm_act_forward", (dummy, dummy, dummy, dummy, dummy, dummy, 1, 4, 8, 4, 1e-5, 99, None)),
-        ("launch_layernorm_forward", (dummy, dummy, dummy, dummy, dummy, dummy, 2, 0, 1e-5, None)),
-        ("launch_im2col", (dummy, dummy, 1, 4, 4, 2, 3, 1, 1, 5, 4, None)),
-        ("launch_sinusoidal", (dummy, dummy, 2, 1, 9.2, None)),
-        ("launch_weight_normalize", (dummy, -1, 4, 1e-4, None)),
+        ("launch_groupnorm_forward", (dummy, dummy, dummy, dummy, dummy, dummy, 1, 4, 10, 4, 1e-5, None),
+         "is not divisible by G"),
+        ("launch_groupnorm_act_forward", (dummy, dummy, dummy, dummy, dummy, dummy, 1, 4, 8, 4, 1e-5, 99, None),
+         "unknown activation 99"),
+        ("launch_layernorm_forward", (dummy, dummy, dummy, dummy, dummy, dummy, 2, 0, 1e-5, None), "bad shape"),
+        # K = 0 (an H_out that does not match H, K, stride and pad is not refused:
+        # the reference trusts it too, and the kernels bounds-check the image side)
+        ("launch_im2col", (dummy, dummy, 1, 4, 4, 2, 0, 1, 1, 4, 4, None), "bad geometry"),
+        ("launch_sinusoidal", (dummy, dummy, 2, 1, 9.2, None), "bad shape"),
+        ("launch_weight_normalize", (dummy, -1, 4, 1e-4, None), "bad shape"),
     ]
-    for name, args in cases:
-        with pytest.raises(nn.NnHipError):
+    for name, args, text in cases:
+        with pytest.raises(nn.NnHipError, match=f"{name}: error 1: {name}: .*{text}"):
             L.call(name, *args)
     code, _ = L.last_error()
     assert code == 0  # the record is cleared by each read

@@ -167,3 +167,40 @@ def test_launcher_scratch_reuse_across_sizes_and_streams(L, orc, rng):
     finally:
         L.dll.nnhip_stream_synchronize(s1)
         L.dll.nnhip_stream_destroy(s1)
+
+
+def test_launcher_scratch_dropped_with_its_stream(L, orc, rng):
+    """Destroying a stream drops its cached scratch block: streams created,
+    used by a launcher without a workspace argument and destroyed in turn (a
+    new stream may get a recycled handle) keep matching the lent-workspace
+    launcher, and nnhip_stream_scratch_release on a live stream is harmless."""
+    print("[case] scratch dropped with its stream", flush=True)
+    ni, no = 1152, 128
+    W = orc.weight_normalize(rng.standard_normal((ni, no)).astype(np.float32), 1e-4)
+    M = rng.standard_normal((ni, no)).astype(np.float32)
+    Wd, gain = L.to_device(W), L.to_device(np.array([0.9], np.float32))
+    ws = L.alloc(int(L.nnhip_weight_normalize_backward_workspace(no)))
+    ws.fill_bytes(0)
+    gB, ggB = L.to_device(M), L.to_device(np.zeros(1, np.float32))
+    L.launch_weight_normalize_backward_ws(gB.p, Wd.p, gain.p, ggB.p, ni, no, ws.p, None)
+    L.sync()
+    for k in range(4):
+        s = L.dll.nnhip_stream_create()
+        assert s
+        try:
+            gA, ggA = L.to_device(M), L.to_device(np.zeros(1, np.float32))
+            L.launch_weight_normalize_backward(gA.p, Wd.p, gain.p, ggA.p, ni, no, s)
+            if k == 1:
+                L.dll.nnhip_stream_scratch_release(s)
+                L.launch_weight_normalize_backward(gA.p, Wd.p, gain.p, ggA.p, ni, no, s)
+                L.dll.nnhip_stream_synchronize(s)  # the uploads below are not ordered with s
+                gA.upload(M)
+                ggA.upload(np.zeros(1, np.float32))
+                L.launch_weight_normalize_backward(gA.p, Wd.p, gain.p, ggA.p, ni, no, s)
+            L.dll.nnhip_stream_synchronize(s)
+            L.sync()
+            assert_bits_equal(gA.download(shape=M.shape), gB.download(shape=M.shape), f"gW stream {k}")
+            assert_bits_equal(ggA.download(), ggB.download(), f"g_gain stream {k}")
+        finally:
+            L.dll.nnhip_stream_synchronize(s)
+            assert L.dll.nnhip_stream_destroy(s) == 0
