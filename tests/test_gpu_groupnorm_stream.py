@@ -151,13 +151,16 @@ def test_stream_groupnorm_other_activations(L, orc, rng, monkeypatch, act):
     check_case(L, orc, rng, (2, 32, 32, 256, 32), act)
 
 
-def test_stream_groupnorm_auto_multi_round(L, orc, rng, monkeypatch):
+@pytest.mark.parametrize("act", [3, 0, 1], ids=["silu", "identity", "relu"])
+def test_stream_groupnorm_auto_multi_round(L, orc, rng, monkeypatch, act):
     """Auto policy at 64 samples of the north-star sample shape: every
     workgroup walks several samples (16 forward rounds, 32 backward), and both
-    directions move >= 512 MB, so the nontemporal instantiations run."""
-    print("[case] stream groupnorm auto B=64 64x64x256", flush=True)
+    directions move >= 512 MB, so the nontemporal instantiations run.  Identity
+    and ReLU run the steady loop that issues part of the next tile after
+    phase A."""
+    print(f"[case] stream groupnorm auto B=64 64x64x256 act={act}", flush=True)
     monkeypatch.delenv("NNHIP_GN_PATH", raising=False)
-    check_case(L, orc, rng, (64, 64, 64, 256, 32), 3)
+    check_case(L, orc, rng, (64, 64, 64, 256, 32), act)
 
 
 def test_stream_groupnorm_pool_workspace_and_determinism(L, orc, rng, monkeypatch):
