@@ -145,6 +145,20 @@ constexpr bool split_prefetch() {
     return ACT == ACT_IDENTITY || ACT == ACT_RELU;
 }
 
+// Backward: s_sleep 1 periods (~64 clocks each) that a workgroup waits in
+// phase B before it writes the tile's dx.  Measured A/B on one GPU at the
+// north-star shape, SiLU backward: none 573-575 us, 8 -> 563-566, 12 ->
+// 558-561, 16 -> 556-559, a single s_sleep 12 -> 566-568; a vmcnt(0) wait
+// there instead (dx only after this workgroup's next-tile reads have landed)
+// gave 578 us, and a scheduling barrier alone changed nothing, so it is the
+// delay that helps: the round's writes start once more of the device's
+// reads are done.  GELU measured slower with the pause (543 -> 552 us), and
+// the identity and ReLU kernels split their prefetch instead.
+template <int ACT>
+constexpr int store_pause() {
+    return ACT == ACT_SILU || ACT == ACT_MP_SILU ? 16 : 0;
+}
+
 // ---------------------------------------------------------------------------
 // Geometry shared by the forward and backward kernels.
 // ---------------------------------------------------------------------------
@@ -600,6 +614,9 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
         const float2 st = stat[pb][gl];
         const float a1 = -rs * st.x, a2 = -rs * st.y;
         float* dxs = dx + (size_t)b * sh.HW * sh.C + (size_t)(t * Gm::TP + row0) * sh.C + c0;
+        // A short pause before the tile's dx stores (see store_pause).
+#pragma unroll
+        for (int ip = 0; ip < store_pause<ACT>(); ++ip) __builtin_amdgcn_s_sleep(1);
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
             const float4 xh = parked[k * TPB + tid];
