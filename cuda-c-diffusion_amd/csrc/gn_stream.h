@@ -152,11 +152,11 @@ constexpr bool split_prefetch() {
 // there instead (dx only after this workgroup's next-tile reads have landed)
 // gave 578 us, and a scheduling barrier alone changed nothing, so it is the
 // delay that helps: the round's writes start once more of the device's
-// reads are done.  GELU measured slower with the pause (543 -> 552 us), and
-// the identity and ReLU kernels split their prefetch instead.
+// reads are done.  Identity (with its split prefetch): 583 -> 570 us with 8
+// or 16.  GELU measured slower with the pause (543 -> 552 us).
 template <int ACT>
 constexpr int store_pause() {
-    return ACT == ACT_SILU || ACT == ACT_MP_SILU ? 16 : 0;
+    return ACT == ACT_SILU || ACT == ACT_MP_SILU ? 16 : (ACT == ACT_IDENTITY || ACT == ACT_RELU ? 8 : 0);
 }
 
 // ---------------------------------------------------------------------------
