@@ -153,10 +153,19 @@ constexpr bool split_prefetch() {
 // gave 578 us, and a scheduling barrier alone changed nothing, so it is the
 // delay that helps: the round's writes start once more of the device's
 // reads are done.  Identity (with its split prefetch): 583 -> 570 us with 8
-// or 16.  GELU measured slower with the pause (543 -> 552 us).
+// or 16; tanh 577 -> 560 with 16 (568 with 8); GELU 541-556 -> 533-535 with 4
+// but 552-554 with 16; ReLU 580 with 8, 577 with 16.
 template <int ACT>
 constexpr int store_pause() {
-    return ACT == ACT_SILU || ACT == ACT_MP_SILU ? 16 : (ACT == ACT_IDENTITY || ACT == ACT_RELU ? 8 : 0);
+    switch (ACT) {
+    case ACT_SILU:
+    case ACT_MP_SILU:
+    case ACT_TANH: return 16;
+    case ACT_IDENTITY:
+    case ACT_RELU: return 8;
+    case ACT_GELU: return 4;
+    default: return 0;
+    }
 }
 
 // ---------------------------------------------------------------------------
