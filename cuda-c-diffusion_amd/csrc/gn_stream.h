@@ -150,7 +150,9 @@ constexpr bool split_prefetch() {
 // north-star shape, SiLU backward: none 573-575 us, 8 -> 563-566, 12 ->
 // 558-561, 16 -> 556-559, a single s_sleep 12 -> 566-568; a vmcnt(0) wait
 // there instead (dx only after this workgroup's next-tile reads have landed)
-// gave 578 us, and a scheduling barrier alone changed nothing, so it is the
+// gave 578 us, the same pause at the start of phase B or before its barrier
+// 563-575 us, a pause staggered over waves or workgroups 582-622 us, and a
+// scheduling barrier alone changed nothing, so it is the
 // delay that helps: the round's writes start once more of the device's
 // reads are done.  Identity (with its split prefetch): 583 -> 570 us with 8
 // or 16; tanh 577 -> 560 with 16 (568 with 8); GELU 541-556 -> 533-535 with 4
