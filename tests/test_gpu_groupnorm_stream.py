@@ -163,6 +163,16 @@ def test_stream_groupnorm_auto_multi_round(L, orc, rng, monkeypatch, act):
     check_case(L, orc, rng, (64, 64, 64, 256, 32), act)
 
 
+@pytest.mark.parametrize("shape", [(32, 64, 64, 128, 32), (32, 32, 32, 512, 32)], ids=["cpg4", "cpg16"])
+@pytest.mark.parametrize("act", [3, 0], ids=["silu", "identity"])
+def test_stream_groupnorm_multi_round_other_group_widths(L, orc, rng, monkeypatch, shape, act):
+    """Several rounds per workgroup at group widths 4 (one column block) and 16
+    (four column blocks), forced streaming: 1024 tiles each way."""
+    print(f"[case] stream groupnorm multi-round {shape} act={act}", flush=True)
+    monkeypatch.setenv("NNHIP_GN_PATH", "stream")
+    check_case(L, orc, rng, shape, act)
+
+
 def test_stream_groupnorm_pool_workspace_and_determinism(L, orc, rng, monkeypatch):
     """No caller workspace (pool-drawn, cleared per launch); two launches give
     bit-identical results (fixed merge and reduction order)."""
