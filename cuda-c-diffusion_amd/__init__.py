@@ -60,6 +60,10 @@ _SIGS = {
     "nnhip_stream_create": (P, [], False),
     "nnhip_stream_destroy": (I, [P], False),
     "nnhip_stream_scratch_release": (None, [P], False),
+    "nnhip_graph_capture_begin": (I, [P], False),
+    "nnhip_graph_capture_end": (P, [P], False),
+    "nnhip_graph_launch": (I, [P, P], False),
+    "nnhip_graph_destroy": (I, [P], False),
     "nnhip_stream_synchronize": (I, [P], False),
     "nnhip_event_create": (P, [], False),
     "nnhip_event_destroy": (I, [P], False),

@@ -201,8 +201,11 @@ struct Shape {
 
 // Workspace layout (device), byte offsets:
 //   0      err u32 (sticky wait-timeout flag)
-//   256    arrival counters u32: [0] teams done, [1 + team] members done;
-//          zero between launches (each launch re-arms what it counted)
+//   4      epoch u32: the tag of the last launch on this workspace, advanced by
+//          that launch's last workgroup (see launch_epoch)
+//   256    arrival counters u32: [0] teams (backward) or workgroups (forward)
+//          done, [1 + team] members done; zero between launches (each launch
+//          re-arms what it counted)
 //   8192   records u64, then (backward) the dgamma/dbeta partials.
 // The header has a fixed size, so a workspace lent for one shape and then
 // another never finds a counter where records were.
@@ -210,11 +213,26 @@ constexpr size_t kHeaderBytes = 8192;
 constexpr size_t kCountOffset = 256;
 struct Work {
     unsigned* err;
+    unsigned* ep;              // the epoch of the last launch on this workspace (0: none yet)
     unsigned* count;
     unsigned long long* rec;   // ntiles * GT * 2, [sample, column block][group][value][pixel tile]
     unsigned long long* part;  // bwd: [P][2][4 * CW4] per-workgroup dgamma/dbeta partials (tagged)
     unsigned long long* tpart; // bwd: [P / T][2][4 * CW4] per-team sums (tagged)
 };
+
+// The tag of this launch: one more than the last launch's on this workspace
+// (never 0, the value of a zero-filled workspace).  Every workgroup reads the
+// word at its start; only the launch's last workgroup, once every workgroup
+// has arrived at the end (and so has read it), stores the new value.  The
+// tag is therefore unique per launch on the workspace also when the launch
+// is replayed from a captured graph with the same arguments.
+__device__ __forceinline__ unsigned launch_epoch(const Work& wk) {
+    const unsigned e = __hip_atomic_load(wk.ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    return e ? e : 1u;
+}
+__device__ __forceinline__ void publish_epoch(const Work& wk, unsigned epoch) {
+    __hip_atomic_store(wk.ep, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // Lanes that share this lane's group inside a wave: xor over the column bits
 // inside the group and over the row bits of the wave.
@@ -245,7 +263,7 @@ __device__ __forceinline__ int wave_slot(int g, int w) {
 template <class Gm, int ACT, int RPL, bool NT>
 __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float* __restrict__ mu_out,
     float* __restrict__ rstd_out, const float* __restrict__ x, const float* __restrict__ gamma,
-    const float* __restrict__ beta, Shape sh, Work wk, float eps, unsigned epoch, unsigned spin_limit) {
+    const float* __restrict__ beta, Shape sh, Work wk, float eps, unsigned spin_limit) {
 #pragma clang fp contract(fast)
     constexpr int NW = Gm::NW, NV = Gm::NV, GT = Gm::GT, TPB = Gm::TPB, CW4 = Gm::CW4;
     __shared__ float4 stage[NV * TPB];          // next tile, written by direct-to-LDS loads
@@ -269,6 +287,7 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
     settle(gm);
     settle(bt);
     const float nthr = (float)(NV * 4);
+    const unsigned epoch = launch_epoch(wk);
     const unsigned long long tag = (unsigned long long)epoch << 32;
     // merge role in phase B: LPG = T / RPL lanes per group (a power of two, at
     // most one wave and TPB / GT, so a group's mergers share a wave); lane rj
@@ -458,6 +477,17 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
         records_prefetch(tB, r0, r1);
     }
     phase_b(tB, r0, r1, pb);
+    // the last active workgroup to finish advances the workspace's epoch
+    __shared__ unsigned arrived;
+    __syncthreads();
+    if (tid == 0) {
+        const unsigned active = (unsigned)(nt < P ? nt : P);
+        arrived = __hip_atomic_fetch_add(wk.count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (arrived == active - 1) {
+            publish_epoch(wk, epoch);
+            __hip_atomic_store(wk.count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // re-arm
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -468,7 +498,7 @@ template <class Gm, int ACT, int RPL, bool NT>
 __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float* __restrict__ ggamma,
     float* __restrict__ gbeta, const float* __restrict__ dy,
     const float* __restrict__ x, const float* __restrict__ gamma, const float* __restrict__ beta,
-    const float* __restrict__ mu, const float* __restrict__ rstd, Shape sh, Work wk, unsigned epoch,
+    const float* __restrict__ mu, const float* __restrict__ rstd, Shape sh, Work wk,
     unsigned spin_limit) {
 #pragma clang fp contract(fast)
     constexpr int NW = Gm::NW, NV = Gm::NV, GT = Gm::GT, TPB = Gm::TPB, CW4 = Gm::CW4;
@@ -493,6 +523,7 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
     if constexpr (ACT != ACT_IDENTITY) bt = ld4(beta + c0);
     settle(gm);
     settle(bt);
+    const unsigned epoch = launch_epoch(wk);
     const unsigned long long tag = (unsigned long long)epoch << 32;
     const int LPG = T / RPL;
     const int rg = tid / LPG, rj = tid % LPG;
@@ -795,7 +826,10 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
         (d ? gbeta : ggamma)[c] = rec_sum<4>(p, (size_t)NCB * NVAL, (nteams - cbc + NCB - 1) / NCB, epoch,
                                              spin_limit, wk.err);
     }
-    if (tid == 0) __hip_atomic_store(wk.count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) {
+        publish_epoch(wk, epoch);  // every workgroup has arrived, so all have read the old one
+        __hip_atomic_store(wk.count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
 }  // namespace gns

@@ -1,5 +1,5 @@
 // k_gns.hip -- host side shared by the streaming GroupNorm launchers
-// (k_gns_fwd.hip, k_gns_bwd.hip): shape plan, launch epochs, workspace clear
+// (k_gns_fwd.hip, k_gns_bwd.hip): shape plan, workspace clear
 // and the persistent grid size.
 #include <stdlib.h>
 
@@ -75,13 +75,6 @@ __global__ void gns_clear(unsigned* p, size_t n) {
 }
 
 }  // namespace
-
-unsigned nnk_next_epoch() {
-    static std::atomic<unsigned> epoch{0};
-    unsigned e = ++epoch;
-    if (e == 0) e = ++epoch;  // 0 is the value of a zero-filled workspace
-    return e;
-}
 
 void nnk_clear_workspace(float* ws, size_t n_floats, hipStream_t s) {
     if (n_floats == 0) return;

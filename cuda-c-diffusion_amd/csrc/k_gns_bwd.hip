@@ -22,14 +22,14 @@ bool launch(const Plan& p, float* dx, float* ggamma, float* gbeta, const float* 
     Shape sh = p.sh;
     Work wk;
     wk.err = reinterpret_cast<unsigned*>(ws);
+    wk.ep = reinterpret_cast<unsigned*>(ws) + 1;
     wk.count = reinterpret_cast<unsigned*>(reinterpret_cast<char*>(ws) + kCountOffset);
     wk.rec = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(ws) + p.rec_offset);
     wk.part = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(ws) + p.part_offset);
     wk.tpart = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(ws) + p.tpart_offset);
-    unsigned epoch = nnk_next_epoch();
     unsigned limit = kSpinLimit;
     void* args[] = {&dx, &ggamma, &gbeta, const_cast<float**>(&dy), const_cast<float**>(&x), const_cast<float**>(&gamma),
-        const_cast<float**>(&beta), const_cast<float**>(&mu), const_cast<float**>(&rstd), &sh, &wk, &epoch,
+        const_cast<float**>(&beta), const_cast<float**>(&mu), const_cast<float**>(&rstd), &sh, &wk,
         &limit};
     return nnk_gns_launch(fn, P, args, s, "streaming GroupNorm backward");
 }

@@ -22,14 +22,14 @@ bool launch(const Plan& p, float* y, float* mu, float* rstd, const float* x, con
     Shape sh = p.sh;
     Work wk;
     wk.err = reinterpret_cast<unsigned*>(ws);
+    wk.ep = reinterpret_cast<unsigned*>(ws) + 1;
     wk.count = reinterpret_cast<unsigned*>(reinterpret_cast<char*>(ws) + kCountOffset);
     wk.rec = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(ws) + p.rec_offset);
     wk.part = nullptr;
     wk.tpart = nullptr;
-    unsigned epoch = nnk_next_epoch();
     unsigned limit = kSpinLimit;
     void* args[] = {&y, &mu, &rstd, const_cast<float**>(&x), const_cast<float**>(&gamma),
-        const_cast<float**>(&beta), &sh, &wk, &eps, &epoch, &limit};
+        const_cast<float**>(&beta), &sh, &wk, &eps, &limit};
     return nnk_gns_launch(fn, P, args, s, "streaming GroupNorm forward");
 }
 

@@ -257,10 +257,11 @@ bool want_stream(bool bwd, int B, int HW, int C, int G, bool reg_ok) {
 
 // Streaming launch on the caller's workspace or on one drawn from the
 // stream-ordered pool.  The kernels accept a statistics record only when it
-// carries the launch's epoch (unique in the process, never 0).  A lent
-// workspace is zero-filled by its owner before first use and written only by
-// these launchers, so it can hold only zeros and older epochs; a pool block
-// may hold anything and is zeroed first.
+// carries the launch's epoch, which the workspace itself keeps (one more than
+// the last launch's on it, never 0; advanced on the device, so a graph replay
+// gets a new one).  A lent workspace is zero-filled by its owner before first
+// use and written only by these launchers, so it can hold only zeros and older
+// epochs; a pool block may hold anything and is zeroed first.
 template <class F>
 bool try_stream(bool bwd, int B, int HW, int C, int G, bool reg_ok, float* ws, hipStream_t s, const char* what,
     F launch) {

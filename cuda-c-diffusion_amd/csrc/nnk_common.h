@@ -353,9 +353,10 @@ __host__ __device__ __forceinline__ bool aligned16(const void* p) {
 // relaxed agent-scope atomics (coherent across the XCDs' L2s).  A reader
 // accepts a record only when it carries its own launch's epoch, so no fence
 // has to order the writer's record before the writer's arrival count (an
-// agent-scope release writes back the whole L2).  The epoch is unique in the
-// process and never 0, so a zero-filled workspace, or one holding records of
-// earlier launches only, never passes for this launch's data.
+// agent-scope release writes back the whole L2).  The epoch is never 0 and
+// differs from every earlier launch's on the same workspace, so a
+// zero-filled workspace, or one holding records of earlier launches only,
+// never passes for this launch's data.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ unsigned long long tagged(unsigned long long tag, float v) {
     return tag | (unsigned long long)__builtin_bit_cast(unsigned, v);
@@ -436,8 +437,6 @@ void nnk_path_note(const char* fmt, ...);
 float* nnk_scratch_acquire(size_t n_floats, hipStream_t s, const char* what);
 void nnk_scratch_release(float* p, hipStream_t s);
 void nnk_scratch_forget_stream(hipStream_t s);
-// Launch epoch for tagged records: unique in the process, never 0.
-unsigned nnk_next_epoch();
 // Zero n_floats words of a workspace drawn from the scratch pool (a fill
 // kernel, so that the sequence can be captured in a graph).
 void nnk_clear_workspace(float* ws, size_t n_floats, hipStream_t s);

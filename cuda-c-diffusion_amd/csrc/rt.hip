@@ -295,6 +295,23 @@ float nnhip_event_elapsed_ms(hipEvent_t start, hipEvent_t stop) {
     return ms;
 }
 
+int nnhip_graph_capture_begin(hipStream_t s) {
+    if (!s) return (int)hipErrorInvalidValue;
+    return (int)hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+}
+
+hipGraphExec_t nnhip_graph_capture_end(hipStream_t s) {
+    hipGraph_t g = nullptr;
+    if (!s || hipStreamEndCapture(s, &g) != hipSuccess || !g) return nullptr;
+    hipGraphExec_t e = nullptr;
+    const hipError_t r = hipGraphInstantiate(&e, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    return r == hipSuccess ? e : nullptr;
+}
+
+int nnhip_graph_launch(hipGraphExec_t g, hipStream_t s) { return (int)hipGraphLaunch(g, s); }
+int nnhip_graph_destroy(hipGraphExec_t g) { return (int)hipGraphExecDestroy(g); }
+
 void nnhip_fill_f32(float* p, float value, size_t n, hipStream_t s) {
     if (n == 0) return;
     NNK_REQUIRE(p, "fill", "nnhip_fill_f32: null pointer");

@@ -59,6 +59,19 @@ int nnhip_event_record(hipEvent_t e, hipStream_t s);
 int nnhip_event_synchronize(hipEvent_t e);
 float nnhip_event_elapsed_ms(hipEvent_t start, hipEvent_t stop); /* < 0 on error */
 
+/* ---- graphs ---- */
+/* Capture the work issued to stream s (not the null stream) from this thread
+   into a graph, then instantiate it: begin, issue launchers, end.  The
+   launchers with a lent workspace issue kernels only (no memset, no
+   allocation), so their sequences can be captured; the streaming GroupNorm
+   keeps its launch tag in the workspace and advances it on the device, so
+   each replay of a captured launch gets a tag of its own.  end returns NULL
+   on failure. */
+int nnhip_graph_capture_begin(hipStream_t s);
+hipGraphExec_t nnhip_graph_capture_end(hipStream_t s);
+int nnhip_graph_launch(hipGraphExec_t g, hipStream_t s);
+int nnhip_graph_destroy(hipGraphExec_t g);
+
 /* ---- calibration ---- */
 /* dst[i] = src[i] for n floats with the same 128-bit vector access pattern
    as the path's streaming kernels; used to scale HBM counters. */

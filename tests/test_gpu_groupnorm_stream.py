@@ -306,3 +306,77 @@ def test_workspace_status_untouched_by_register_path(L, orc, rng, monkeypatch):
     assert rel_err(dx, dx_ref) <= TOL
     assert rel_err(gg, gg_ref, floor=fg) <= TOL
     assert L.nnhip_groupnorm_workspace_status(ws.p) == 0
+
+
+def test_stream_groupnorm_graph_replay(L, orc, rng, monkeypatch):
+    """The streaming forward + backward captured into a HIP graph and
+    replayed with new inputs each time: every replay matches the eager launch
+    on the same inputs bit for bit (each replay gets a fresh record tag from
+    the workspace), with eager launches on the same workspaces in between."""
+    print("[case] stream groupnorm graph capture and replay", flush=True)
+    monkeypatch.setenv("NNHIP_GN_PATH", "stream")
+    B, H, W, C, G = 16, 64, 64, 256, 32
+    HW, act = H * W, 3
+    sets = [make_inputs(rng, B, H, W, C) for _ in range(2)]
+    xd, dyd = L.alloc(B * HW * C), L.alloc(B * HW * C)
+    gd, bd = L.to_device(sets[0][1]), L.to_device(sets[0][2])
+    yd, dxd = L.alloc(B * HW * C), L.alloc(B * HW * C)
+    mud, rsd, ggd, gbd = L.alloc(B * G), L.alloc(B * G), L.alloc(C), L.alloc(C)
+    fws = L.alloc(L.nnhip_groupnorm_forward_workspace(B, HW, C, G))
+    bws = L.alloc(L.nnhip_groupnorm_backward_workspace(B, HW, C, G))
+    fws.fill_bytes(0)
+    bws.fill_bytes(0)
+    s = L.dll.nnhip_stream_create()
+    assert s
+    outs = (yd, mud, rsd, dxd, ggd, gbd)
+
+    def issue():
+        L.launch_groupnorm_act_forward_ws(yd.p, mud.p, rsd.p, xd.p, gd.p, bd.p, B, HW, C, G, 1e-5, act, fws.p, s)
+        L.launch_groupnorm_act_backward_ws(dxd.p, ggd.p, gbd.p, dyd.p, xd.p, gd.p, bd.p, mud.p, rsd.p, B, HW, C, G,
+                                           act, bws.p, s)
+
+    def load(k):
+        L.dll.nnhip_stream_synchronize(s)  # the uploads are not ordered with s
+        xd.upload(sets[k][0])
+        dyd.upload(sets[k][3])
+
+    def results():
+        L.dll.nnhip_stream_synchronize(s)
+        L.sync()
+        return [o.download() for o in outs]
+
+    graph = None
+    try:
+        refs = []
+        for k in range(2):
+            load(k)
+            issue()
+            refs.append(results())
+        assert L.dll.nnhip_graph_capture_begin(s) == 0
+        issue()
+        graph = L.dll.nnhip_graph_capture_end(s)
+        assert graph, "graph capture failed"
+        names = ("y", "mu", "rstd", "dx", "dgamma", "dbeta")
+        for replay in range(6):
+            k = replay % 2
+            load(k)
+            for o in outs:
+                o.fill_bytes(0)
+            L.sync()
+            assert L.dll.nnhip_graph_launch(graph, s) == 0
+            for got, ref, name in zip(results(), refs[k], names):
+                assert_bits_equal(got, ref, f"replay {replay} {name}")
+            issue()  # eager launch on the same workspaces between replays
+            for got, ref, name in zip(results(), refs[k], names):
+                assert_bits_equal(got, ref, f"eager after replay {replay} {name}")
+        assert L.nnhip_groupnorm_workspace_status(fws.p) == 0
+        assert L.nnhip_groupnorm_workspace_status(bws.p) == 0
+        # the eager reference itself against the oracle (gamma, beta of set 0)
+        x, gamma, beta = sets[1][0], sets[0][1], sets[0][2]
+        y_ref, mu_ref, rs_ref = orc.groupnorm_forward(x, gamma, beta, G, 1e-5, act)
+        assert rel_err(refs[1][0].reshape(x.shape), y_ref) <= TOL
+    finally:
+        if graph:
+            L.dll.nnhip_graph_destroy(graph)
+        L.dll.nnhip_stream_synchronize(s)
+        L.dll.nnhip_stream_destroy(s)
