@@ -387,24 +387,16 @@ double nn_convcheck(int B, int H, int W, int Cin, int Cout, int K, int stride, i
     return d;
 }
 
-/* The fused DDPM block's forward + backward captured into a HIP graph on a
-   created stream (nnhip_graph_capture_begin/end) and replayed `reps` times.
-   Every replay must reproduce the eager output, input gradient and
-   embedding gradient bit for bit (returned: number of mismatching replays,
-   -1 if the capture failed).  out_ms[0]: eager forward+backward, out_ms[1]:
-   one graph replay (best of reps, each timed alone). */
-int nn_blockcheck_ddpm_graph(int B, int H, int W, int C, int G, int emb, int reps, float* out_ms)
+/* A block's forward + backward captured into a HIP graph on a created stream
+   (nnhip_graph_capture_begin/end) and replayed `reps` times.  Every replay
+   must reproduce the eager output, input gradient and embedding gradient bit
+   for bit (returned: number of mismatching replays, -1 if the capture
+   failed).  out_ms[0]: eager forward+backward, out_ms[1]: one graph replay
+   (best of reps, each timed alone). */
+static int graph_replays(Context* cg, Module* blk, int slot, int B, int n, int emb, float* x, float* gout, int reps,
+    float* out_ms)
 {
-    hipStream_t s = nnhip_stream_create();
-    Context cg;
-    nn_context_init(&cg, 13ull, s);
-    const int n = B * H * W * C;
-    const int slot = ctx_add_cond(&cg, emb, B);
-    float* e = dev_normal((size_t)B * emb, 1.0f);
-    ctx_set_cond(&cg, slot, e);
-    Module* blk = conv_residual_create(&cg, C, emb, H, W, B, G, slot);
-    float* x = dev_normal((size_t)n, 1.0f);
-    float* gout = dev_normal((size_t)n, 1.0f);
+    hipStream_t s = cg->stream;
     float *y = nn_device_alloc((size_t)n), *gx = nn_device_alloc((size_t)n);
     float *y0 = nn_device_alloc((size_t)n), *gx0 = nn_device_alloc((size_t)n);
     float* ge0 = nn_device_alloc((size_t)B * emb);
@@ -415,9 +407,9 @@ int nn_blockcheck_ddpm_graph(int B, int H, int W, int C, int G, int emb, int rep
     /* eager runs (the first also sizes every cached scratch block) */
     for (int rep = 0; rep < 3; ++rep) {
         NN_HIP_CHECK(hipEventRecord(t0, s));
-        blk->forward(blk, x, y, B, &cg);
-        ctx_zero_cond_grad(&cg, B);
-        blk->backward(blk, x, y, gout, gx, B, &cg);
+        blk->forward(blk, x, y, B, cg);
+        ctx_zero_cond_grad(cg, B);
+        blk->backward(blk, x, y, gout, gx, B, cg);
         NN_HIP_CHECK(hipEventRecord(t1, s));
         NN_HIP_CHECK(hipEventSynchronize(t1));
         NN_HIP_CHECK(hipEventElapsedTime(&ms, t0, t1));
@@ -425,14 +417,14 @@ int nn_blockcheck_ddpm_graph(int B, int H, int W, int C, int G, int emb, int rep
     }
     NN_HIP_CHECK(hipMemcpy(y0, y, (size_t)n * sizeof(float), hipMemcpyDeviceToDevice));
     NN_HIP_CHECK(hipMemcpy(gx0, gx, (size_t)n * sizeof(float), hipMemcpyDeviceToDevice));
-    NN_HIP_CHECK(hipMemcpy(ge0, cg.cond[slot].grad, (size_t)B * emb * sizeof(float), hipMemcpyDeviceToDevice));
+    NN_HIP_CHECK(hipMemcpy(ge0, cg->cond[slot].grad, (size_t)B * emb * sizeof(float), hipMemcpyDeviceToDevice));
 
     int bad = -1;
     hipGraphExec_t graph = NULL;
     if (nnhip_graph_capture_begin(s) == 0) {
-        blk->forward(blk, x, y, B, &cg);
-        ctx_zero_cond_grad(&cg, B);
-        blk->backward(blk, x, y, gout, gx, B, &cg);
+        blk->forward(blk, x, y, B, cg);
+        ctx_zero_cond_grad(cg, B);
+        blk->backward(blk, x, y, gout, gx, B, cg);
         graph = nnhip_graph_capture_end(s);
     }
     if (graph) {
@@ -448,21 +440,72 @@ int nn_blockcheck_ddpm_graph(int B, int H, int W, int C, int G, int emb, int rep
             NN_HIP_CHECK(hipEventElapsedTime(&ms, t0, t1));
             if (ms < best_g) best_g = ms;
             if (rel_diff(y, y0, (size_t)n) != 0.0 || rel_diff(gx, gx0, (size_t)n) != 0.0 ||
-                rel_diff(cg.cond[slot].grad, ge0, (size_t)B * emb) != 0.0)
+                rel_diff(cg->cond[slot].grad, ge0, (size_t)B * emb) != 0.0)
                 ++bad;
             /* eager work on the same buffers and workspaces between replays */
-            blk->forward(blk, x, y, B, &cg);
+            blk->forward(blk, x, y, B, cg);
             NN_HIP_CHECK(hipStreamSynchronize(s));
         }
         (void)nnhip_graph_destroy(graph);
     }
     out_ms[0] = best_e;
     out_ms[1] = best_g;
-    blk->free(blk);
-    float* more[] = {x, gout, y, gx, y0, gx0, ge0, e};
+    float* more[] = {y, gx, y0, gx0, ge0};
     for (size_t i = 0; i < sizeof more / sizeof more[0]; ++i) (void)hipFree(more[i]);
     (void)hipEventDestroy(t0);
     (void)hipEventDestroy(t1);
+    return bad;
+}
+
+/* The fused DDPM block (src/conv_residual.c) as a graph; see graph_replays. */
+int nn_blockcheck_ddpm_graph(int B, int H, int W, int C, int G, int emb, int reps, float* out_ms)
+{
+    hipStream_t s = nnhip_stream_create();
+    Context cg;
+    nn_context_init(&cg, 13ull, s);
+    const int n = B * H * W * C;
+    const int slot = ctx_add_cond(&cg, emb, B);
+    float* e = dev_normal((size_t)B * emb, 1.0f);
+    ctx_set_cond(&cg, slot, e);
+    Module* blk = conv_residual_create(&cg, C, emb, H, W, B, G, slot);
+    float* x = dev_normal((size_t)n, 1.0f);
+    float* gout = dev_normal((size_t)n, 1.0f);
+    const int bad = graph_replays(&cg, blk, slot, B, n, emb, x, gout, reps, out_ms);
+    blk->free(blk);
+    (void)hipFree(x);
+    (void)hipFree(gout);
+    (void)hipFree(e);
+    nn_context_destroy(&cg);
+    (void)nnhip_stream_destroy(s);
+    return bad;
+}
+
+/* The fused EDM block (src/cond_conv_residual.c) as a graph, with a non-zero
+   embedding gain so that the conditioning path carries gradient. */
+int nn_blockcheck_edm_graph(int B, int H, int W, int C, int emb, float t, int reps, float* out_ms)
+{
+    hipStream_t s = nnhip_stream_create();
+    Context cg;
+    nn_context_init(&cg, 17ull, s);
+    const int n = B * H * W * C;
+    const int slot = ctx_add_cond(&cg, emb, B);
+    float* e = dev_normal((size_t)B * emb, 1.0f);
+    ctx_set_cond(&cg, slot, e);
+    Module* blk = cond_conv_residual_create(&cg, C, emb, H, W, B, t, slot);
+    {
+        ParamList pl;
+        param_list_init(&pl);
+        blk->parameters(blk, &pl);
+        if (pl.count > 3 && pl.items[3].size == 1) nnhip_fill_f32(pl.items[3].param, 0.7f, 1, s);
+        param_list_free(&pl);
+    }
+    float* x = dev_normal((size_t)n, 1.0f);
+    float* gout = dev_normal((size_t)n, 1.0f);
+    const int bad = graph_replays(&cg, blk, slot, B, n, emb, x, gout, reps, out_ms);
+    blk->free(blk);
+    (void)hipFree(x);
+    (void)hipFree(gout);
+    (void)hipFree(e);
     nn_context_destroy(&cg);
     (void)nnhip_stream_destroy(s);
     return bad;

@@ -31,6 +31,8 @@ def bc(L):
     lib.nn_blockcheck_edm.restype = C.c_double
     lib.nn_blockcheck_ddpm_graph.argtypes = [C.c_int] * 7 + [C.POINTER(C.c_float)]
     lib.nn_blockcheck_ddpm_graph.restype = C.c_int
+    lib.nn_blockcheck_edm_graph.argtypes = [C.c_int] * 5 + [C.c_float, C.c_int, C.POINTER(C.c_float)]
+    lib.nn_blockcheck_edm_graph.restype = C.c_int
     return lib
 
 
@@ -46,6 +48,18 @@ def test_ddpm_block_graph_replay(bc, shape):
     ms = (C.c_float * 2)()
     bad = bc.nn_blockcheck_ddpm_graph(*shape, 4, ms)
     print(f"DDPM block {shape} as a graph: eager fwd+bwd {ms[0]:.3f} ms, graph replay {ms[1]:.3f} ms", flush=True)
+    assert bad == 0, "capture failed" if bad < 0 else f"{bad} replays differ from eager"
+
+
+@pytest.mark.parametrize("shape", [(2, 8, 8, 16, 12), (128, 32, 32, 128, 512)], ids=["small", "cfg2"])
+def test_edm_block_graph_replay(bc, shape):
+    """The fused EDM block (weight-normalised convolutions with a lent
+    workspace, the modulate + MP-SiLU pair, mp_sum) as one HIP graph: every
+    replay bit-identical to eager."""
+    print(f"[case] EDM block graph {shape}", flush=True)
+    ms = (C.c_float * 2)()
+    bad = bc.nn_blockcheck_edm_graph(*shape, 0.3, 4, ms)
+    print(f"EDM block {shape} as a graph: eager fwd+bwd {ms[0]:.3f} ms, graph replay {ms[1]:.3f} ms", flush=True)
     assert bad == 0, "capture failed" if bad < 0 else f"{bad} replays differ from eager"
 
 
