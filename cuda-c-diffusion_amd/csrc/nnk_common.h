@@ -432,6 +432,8 @@ void nnk_set_error(int code, const char* fmt, ...);
 // Check the launch just made on `s` (and, in NNHIP_CHECK=1 mode, synchronise
 // the stream and abort on failure).  `what` names the launcher.
 void nnk_after_launch(const char* what, hipStream_t s);
+// Whether stream s is capturing a graph (no synchronisation or allocation then).
+bool nnk_capturing(hipStream_t s);
 void nnk_path_note(const char* fmt, ...);
 // Stream-ordered scratch for launchers that need partial sums.
 float* nnk_scratch_acquire(size_t n_floats, hipStream_t s, const char* what);

@@ -6,6 +6,7 @@
 #include <string.h>
 
 #include <mutex>
+#include <vector>
 
 #include "nn_hip_rt.h"
 #include "nnk_common.h"
@@ -58,9 +59,14 @@ void nnk_path_note(const char* fmt, ...) {
     va_end(ap);
 }
 
+bool nnk_capturing(hipStream_t s) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    return s && hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+}
+
 void nnk_after_launch(const char* what, hipStream_t s) {
     hipError_t e = hipGetLastError();
-    if (e == hipSuccess && check_mode()) e = hipStreamSynchronize(s);
+    if (e == hipSuccess && check_mode() && !nnk_capturing(s)) e = hipStreamSynchronize(s);
     if (e != hipSuccess) nnk_set_error((int)e, "%s: %s", what, hipGetErrorString(e));
 }
 
@@ -73,6 +79,13 @@ void nnk_after_launch(const char* what, hipStream_t s) {
 // Blocks come from a memory pool the library owns, one per device, whose
 // release threshold keeps freed memory cached; the process's default pool is
 // left as it is.  Cached blocks are held until the process ends.
+//
+// Under stream capture a launcher may only take the stream's cached block as
+// it is (the graph keeps its address): a capture that would need a new or
+// larger block is refused with an error, so run the sequence once eagerly
+// before capturing it.  A block that a capture has used is never freed: when
+// the slot later grows or its stream is dropped, the old block is retired
+// (kept until the process ends) because graphs may still replay on it.
 namespace {
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
@@ -84,9 +97,22 @@ struct Slot {
     void* p;
     size_t bytes;
     bool busy;
+    bool captured;  // a captured graph refers to p
 };
 Slot g_slots[256];
 int g_nslots = 0;
+std::vector<void*> g_retired;  // blocks graphs may still use
+
+// Caller holds g_scratch_mu.  Give up slot's block: free it in stream order,
+// or retire it if a captured graph refers to it.
+void drop_block(Slot& slot) {
+    if (!slot.p) return;
+    if (slot.captured) g_retired.push_back(slot.p);
+    else (void)hipFreeAsync(slot.p, slot.stream);
+    slot.p = nullptr;
+    slot.bytes = 0;
+    slot.captured = false;
+}
 
 // Caller holds g_scratch_mu.
 hipMemPool_t scratch_pool(int dev, const char* what) {
@@ -130,6 +156,7 @@ float* nnk_scratch_acquire(size_t n_floats, hipStream_t s, const char* what) {
         return nullptr;
     }
     size_t need = n_floats * sizeof(float) + 256;
+    const bool capturing = nnk_capturing(s);
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     hipMemPool_t pool = scratch_pool(dev, what);
     if (!pool) return nullptr;
@@ -138,7 +165,13 @@ float* nnk_scratch_acquire(size_t n_floats, hipStream_t s, const char* what) {
         if (g_slots[i].dev == dev && g_slots[i].stream == s) slot = &g_slots[i];
     if (!slot && g_nslots < (int)(sizeof g_slots / sizeof g_slots[0])) {
         slot = &g_slots[g_nslots++];
-        *slot = Slot{dev, s, nullptr, 0, false};
+        *slot = Slot{dev, s, nullptr, 0, false, false};
+    }
+    if (capturing && (!slot || slot->busy || slot->bytes < need)) {
+        nnk_set_error((int)hipErrorStreamCaptureUnsupported,
+            "%s: scratch of %zu bytes is not cached for the capturing stream (run the sequence once before "
+            "capturing it)", what, need);
+        return nullptr;
     }
     if (!slot || slot->busy) return static_cast<float*>(pool_alloc(pool, need, s, what));
     if (slot->bytes < need) {
@@ -146,10 +179,11 @@ float* nnk_scratch_acquire(size_t n_floats, hipStream_t s, const char* what) {
         while (bytes < need) bytes <<= 1;
         void* p = pool_alloc(pool, bytes, s, what);
         if (!p) return nullptr;
-        if (slot->p) (void)hipFreeAsync(slot->p, s);
+        drop_block(*slot);
         slot->p = p;
         slot->bytes = bytes;
     }
+    if (capturing) slot->captured = true;
     slot->busy = true;
     return static_cast<float*>(slot->p);
 }
@@ -162,7 +196,7 @@ void nnk_scratch_forget_stream(hipStream_t s) {
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     for (int i = 0; i < g_nslots; ++i) {
         if (g_slots[i].stream != s) continue;
-        if (g_slots[i].p) (void)hipFreeAsync(g_slots[i].p, s);
+        drop_block(g_slots[i]);
         g_slots[i] = g_slots[--g_nslots];
         --i;
     }

@@ -169,6 +169,59 @@ def test_launcher_scratch_reuse_across_sizes_and_streams(L, orc, rng):
         L.dll.nnhip_stream_destroy(s1)
 
 
+def test_launcher_scratch_under_graph_capture(L, orc, rng, nn):
+    """A launcher without a workspace argument inside a captured graph uses its
+    stream's cached scratch block.  The replays keep matching eager after the
+    stream's block has grown for a larger eager call (the captured block is
+    kept, not freed), and a capture that would need a new or larger block is
+    refused on the host with an error instead of allocating."""
+    print("[case] scratch under graph capture", flush=True)
+    bs, bb, N = 256, 16384, 1024
+    g_small = rng.standard_normal((bs, N)).astype(np.float32)
+    g_big = rng.standard_normal((bb, N)).astype(np.float32)
+    gs, gbig = L.to_device(g_small), L.to_device(g_big)
+    out, out_big = L.alloc(N), L.alloc(N)
+    s = L.dll.nnhip_stream_create()
+    s3 = L.dll.nnhip_stream_create()
+    assert s and s3
+    graph = None
+    try:
+        L.launch_bias_grad(out.p, gs.p, bs, N, s)
+        L.dll.nnhip_stream_synchronize(s)
+        ref = out.download()
+        np.testing.assert_allclose(ref, orc.bias_grad(g_small, N), rtol=1e-5, atol=1e-4)
+        assert L.dll.nnhip_graph_capture_begin(s) == 0
+        L.launch_bias_grad(out.p, gs.p, bs, N, s)
+        graph = L.dll.nnhip_graph_capture_end(s)
+        assert graph, "graph capture failed"
+        for replay in range(3):
+            # a larger eager call on the same stream grows its cached block
+            L.launch_bias_grad(out_big.p, gbig.p, bb if replay == 0 else bb // 2, N, s)
+            out.fill_bytes(0)
+            L.dll.nnhip_stream_synchronize(s)
+            L.sync()
+            assert L.dll.nnhip_graph_launch(graph, s) == 0
+            L.dll.nnhip_stream_synchronize(s)
+            assert_bits_equal(out.download(), ref, f"replay {replay}")
+        np.testing.assert_allclose(out_big.download(), orc.bias_grad(g_big[: bb // 2], N), rtol=1e-4, atol=1e-3)
+        # a capture on a stream with no cached block is refused, not allocated
+        assert L.dll.nnhip_graph_capture_begin(s3) == 0
+        with pytest.raises(nn.NnHipError, match="launch_bias_grad: .*not cached for the capturing stream"):
+            L.call("launch_bias_grad", out.p, gs.p, bs, N, s3)
+        empty = L.dll.nnhip_graph_capture_end(s3)
+        if empty:
+            assert L.dll.nnhip_graph_destroy(empty) == 0
+        L.launch_bias_grad(out.p, gs.p, bs, N, s3)  # eager again: allocates as usual
+        L.dll.nnhip_stream_synchronize(s3)
+        assert_bits_equal(out.download(), ref, "eager after refusal")
+    finally:
+        if graph:
+            assert L.dll.nnhip_graph_destroy(graph) == 0
+        for st in (s, s3):
+            L.dll.nnhip_stream_synchronize(st)
+            assert L.dll.nnhip_stream_destroy(st) == 0
+
+
 def test_launcher_scratch_dropped_with_its_stream(L, orc, rng):
     """Destroying a stream drops its cached scratch block: streams created,
     used by a launcher without a workspace argument and destroyed in turn (a
