@@ -20,21 +20,24 @@
 //                walks the samples; tile i = round * P + w.  The T workgroups
 //                that own the tiles of one (sample, column block) are
 //                consecutive: a team.
-//   round r    : take tile i from the LDS stage into registers and start the
-//                direct-to-LDS loads of tile i+P into the stage;
-//                phase A on tile i (registers): per-group partial statistics
+//   round j    : take tile j (this workgroup's tile w + j * P) from its LDS
+//                stage buffer into registers and start the direct-to-LDS
+//                loads of tile j+2 into that buffer (two stage buffers, so
+//                two tiles are in flight while a round computes);
+//                phase A on tile j (registers): per-group partial statistics
 //                -> one epoch-tagged 64-bit record per (tile, group, value);
-//                phase B on tile i-P (parked in LDS by the previous round):
+//                phase B on tile j-2 (kept in registers since round j-2):
 //                read the T records of each of its groups, merge them in a
-//                fixed order, normalise / form dx, store;
-//                park tile i in LDS.
+//                fixed order, normalise / form dx, store.
 //
-// Only the current tile occupies registers (a second register tile makes the
-// compiler spill, and every spill reload waits on the in-order vector-memory
-// counter, i.e. on the whole prefetch).  The next tile lands in LDS by itself;
-// the workgroup barriers here wait for LDS operations only, so those loads
-// stay in flight through phases A and B.  Each lane reads back exactly the
-// stage slot its own load wrote, so the stage needs no barrier.
+// The tiles awaiting phase B stay in VGPRs, the stage is read with explicit
+// waits on the in-order vector-memory counter (the compiler does not track
+// direct-to-LDS loads into two buffers), and the workgroup barriers wait for
+// LDS operations only, so the staged loads stay in flight through phases A
+// and B.  Each lane reads back exactly the stage slot its own load wrote, so
+// the stage needs no barrier.  Phase B lags phase A by two rounds: a tile's
+// records have two rounds to arrive, so the exchange round trip stays off the
+// critical path.
 //
 // Records carry the launch epoch in their upper 32 bits and are written and
 // read with agent-scope atomic 64-bit accesses, so a reader accepts exactly
@@ -100,11 +103,43 @@ __device__ __forceinline__ void lds_barrier() {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
-// This wave's LDS reads have returned (before a direct-to-LDS load reuses the slots).
-__device__ __forceinline__ void lds_reads_done() {
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0xC07F);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+// Wait until at most N vector-memory operations of this wave are
+// outstanding.  They complete in issue order, so this waits for everything
+// issued before the last N.  The tile loops read the stage with inline
+// assembly that the compiler does not track, so each round waits for its
+// stage buffer explicitly, with N = the vector-memory operations that every
+// wave issues after that buffer's loads (see the tile loops); a wave that
+// issued more (conditional record stores, record polls) waits for more, never
+// for less.
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+typedef __attribute__((address_space(3))) float4 lds_float4;
+__device__ __forceinline__ uint32_t lds_addr(const float4* p) {
+    return (uint32_t)(uintptr_t)(const lds_float4*)p;
+}
+
+// This lane's four 16-byte stage slots at addr + k * 16 KiB (k = 0..3; the
+// slot stride of a 1024-thread workgroup), read and waited for in one
+// statement so that no use of v is scheduled before the data is there.
+__device__ __forceinline__ void lds_take4(float4 (&v)[4], uint32_t addr) {
+    f32x4 a, b, c, d;
+    asm volatile(
+        "ds_read_b128 %0, %4\n\t"
+        "ds_read_b128 %1, %4 offset:16384\n\t"
+        "ds_read_b128 %2, %4 offset:32768\n\t"
+        "ds_read_b128 %3, %4 offset:49152\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(a), "=&v"(b), "=&v"(c), "=&v"(d)
+        : "v"(addr)
+        : "memory");
+    v[0] = make_float4(a.x, a.y, a.z, a.w);
+    v[1] = make_float4(b.x, b.y, b.z, b.w);
+    v[2] = make_float4(c.x, c.y, c.z, c.w);
+    v[3] = make_float4(d.x, d.y, d.z, d.w);
 }
 
 // Make v's loads complete here.  Values loaded before the tile pipeline and
@@ -136,38 +171,6 @@ __device__ __forceinline__ void chan_merge_eq(float& m, float& q, float mo, floa
     const float d = mo - m;
     m = 0.5f * (m + mo);
     q = q + qo + d * d * (0.5f * c);
-}
-
-// Whether a round issues part of the next tile's loads after its phase A (see
-// the tile loops): for the activations whose phase A is shortest.
-template <int ACT>
-constexpr bool split_prefetch() {
-    return ACT == ACT_IDENTITY || ACT == ACT_RELU;
-}
-
-// Backward: s_sleep 1 periods (~64 clocks each) that a workgroup waits in
-// phase B before it writes the tile's dx.  Measured A/B on one GPU at the
-// north-star shape, SiLU backward: none 573-575 us, 8 -> 563-566, 12 ->
-// 558-561, 16 -> 556-559, a single s_sleep 12 -> 566-568; a vmcnt(0) wait
-// there instead (dx only after this workgroup's next-tile reads have landed)
-// gave 578 us, the same pause at the start of phase B or before its barrier
-// 563-575 us, a pause staggered over waves or workgroups 582-622 us, and a
-// scheduling barrier alone changed nothing, so it is the
-// delay that helps: the round's writes start once more of the device's
-// reads are done.  Identity (with its split prefetch): 583 -> 570 us with 8
-// or 16; tanh 577 -> 560 with 16 (568 with 8); GELU 541-556 -> 533-535 with 4
-// but 552-554 with 16; ReLU 580 with 8, 577 with 16.
-template <int ACT>
-constexpr int store_pause() {
-    switch (ACT) {
-    case ACT_SILU:
-    case ACT_MP_SILU:
-    case ACT_TANH: return 16;
-    case ACT_IDENTITY:
-    case ACT_RELU: return 8;
-    case ACT_GELU: return 4;
-    default: return 0;
-    }
 }
 
 // ---------------------------------------------------------------------------
@@ -212,7 +215,8 @@ struct Shape {
 constexpr size_t kHeaderBytes = 8192;
 constexpr size_t kCountOffset = 256;
 struct Work {
-    unsigned* err;
+    unsigned* err;             // the workspace's sticky timeout word
+    unsigned* hflag;           // the process-wide host-mapped timeout word (or err)
     unsigned* ep;              // the epoch of the last launch on this workspace (0: none yet)
     unsigned* count;
     unsigned long long* rec;   // ntiles * GT * 2, [sample, column block][group][value][pixel tile]
@@ -266,8 +270,11 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
     const float* __restrict__ beta, Shape sh, Work wk, float eps, unsigned spin_limit) {
 #pragma clang fp contract(fast)
     constexpr int NW = Gm::NW, NV = Gm::NV, GT = Gm::GT, TPB = Gm::TPB, CW4 = Gm::CW4;
-    __shared__ float4 stage[NV * TPB];          // next tile, written by direct-to-LDS loads
-    __shared__ float4 parked[NV * TPB];         // the tile awaiting phase B
+    static_assert(NV == 4 && TPB * 16 == 16384, "stage slots as lds_take4 reads them");
+    // Two stage buffers: the tiles of the next two rounds, written by
+    // direct-to-LDS loads (round j takes buffer j % 2).  The tiles awaiting
+    // phase B stay in registers.
+    __shared__ float4 stage[2][NV * TPB];
     // Double-buffered by loop parity pb: consecutive phase A's (and phase B's)
     // may run with no barrier between them (first and last rounds), so a
     // buffer is rewritten only two phases later, past the other phase's barrier.
@@ -289,27 +296,41 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
     const float nthr = (float)(NV * 4);
     const unsigned epoch = launch_epoch(wk);
     const unsigned long long tag = (unsigned long long)epoch << 32;
+    const WaitFail wf{wk.err, wk.hflag};
+    // A spin limit of 0 lets no wait succeed: the launch flags itself as
+    // timed out (the error path, forced from the host for its tests).
+    if (spin_limit == 0 && blockIdx.x == 0 && threadIdx.x == 0) wait_failed(wf);
     // merge role in phase B: LPG = T / RPL lanes per group (a power of two, at
     // most one wave and TPB / GT, so a group's mergers share a wave); lane rj
     // merges records rj, rj + LPG, ... (RPL of them)
     const int LPG = T / RPL;
     const int rg = tid / LPG, rj = tid % LPG;
     const bool merger = rg < GT;
+    const int nt = sh.ntiles;
 
-    auto sample_of = [&](int tile) { return tile / (NCB * T); };
-    // Record layout [unit = sample * NCB + column block][group][value][pixel tile]:
-    // the mergers of a group read consecutive tiles, i.e. contiguous records.
-    auto rec_slot = [&](int unit, int g, int tt) { return wk.rec + ((size_t)(unit * GT + g) * 2) * T + tt; };
-    auto issue_part = [&](int tile, auto k0c, auto k1c) {  // loads k0..k1-1 of `tile` into the stage
-        constexpr int K0 = decltype(k0c)::value, K1 = decltype(k1c)::value;
-        const __amdgpu_buffer_rsrc_t r = sample_rsrc(x + (size_t)sample_of(tile) * sh.HW * sh.C, sh.sample_bytes);
+    // Round j works on this workgroup's tile w + j * P.  P is a multiple of
+    // NCB * T (the tiles of one sample), so the tile's sample and its unit
+    // (sample * NCB + column block) advance by constants from round to round.
+    const int b0 = w / (NCB * T), spr = P / (NCB * T);
+    const int u0 = w / T, upr = P / T;
+    auto real_of = [&](int j) { return w + j * P < nt; };
+    // Record layout [unit][group][value][pixel tile]: the mergers of a group
+    // read consecutive tiles, i.e. contiguous records.
+    auto rec_slot = [&](int j, int g, int tt) { return wk.rec + ((size_t)((u0 + j * upr) * GT + g) * 2) * T + tt; };
+    // The NV loads of round j's tile into stage buffer sb.  A tile past the
+    // end is issued against an empty buffer range: the loads read nothing and
+    // only keep the operation count of every round the same.
+    auto issue = [&](int j, int sb) {
+        const bool real = real_of(j);
+        const __amdgpu_buffer_rsrc_t r =
+            sample_rsrc(x + (size_t)(real ? b0 + j * spr : 0) * sh.HW * sh.C, real ? sh.sample_bytes : 0u);
         const uint32_t base = (uint32_t)(t * Gm::TP) * row_bytes;
 #pragma unroll
-        for (int k = K0; k < K1; ++k)
-            dma16<NT>(r, stage + k * TPB + wid * kWave, voff, base + (uint32_t)(k * Gm::RSTEP) * row_bytes);
+        for (int k = 0; k < NV; ++k)
+            dma16<NT>(r, &stage[sb][k * TPB + wid * kWave], voff, base + (uint32_t)(k * Gm::RSTEP) * row_bytes);
     };
-    auto issue = [&](int tile) { issue_part(tile, std::integral_constant<int, 0>{}, std::integral_constant<int, NV>{}); };
-    auto phase_a = [&](const float4 (&v)[NV], int tile, int pb) {
+    auto take = [&](float4 (&v)[NV], int sb) { lds_take4(v, lds_addr(&stage[sb][tid])); };
+    auto phase_a = [&](const float4 (&v)[NV], int j, int pb) {
         float s = 0.0f;
 #pragma unroll
         for (int k = 0; k < NV; ++k) s += (v[k].x + v[k].y) + (v[k].z + v[k].w);
@@ -340,7 +361,7 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
                 cnt *= 2.0f;
             }
             if (i == 0) {
-                unsigned long long* r = rec_slot(tile / T, g, tile % T);
+                unsigned long long* r = rec_slot(j, g, t);
                 rec_store(r, tagged(tag, mm));
                 rec_store(r + T, tagged(tag, qq));
             }
@@ -348,18 +369,19 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
     };
     // Every lane loads (lanes past the mergers read group GT-1 and ignore it):
     // a branch here would put a path without these loads in front of the
-    // staged-tile wait.
-    auto records_prefetch = [&](int tile, unsigned long long (&r0)[RPL], unsigned long long (&r1)[RPL]) {
+    // record waits.
+    unsigned long long r0[RPL] = {}, r1[RPL] = {};
+    auto records_prefetch = [&](int j) {
         const int rgc = merger ? rg : GT - 1;
 #pragma unroll
         for (int u = 0; u < RPL; ++u) {
-            const unsigned long long* p = rec_slot(tile / T, rgc, rj + u * LPG);
+            const unsigned long long* p = rec_slot(j, rgc, rj + u * LPG);
             r0[u] = rec_load(p);
             r1[u] = rec_load(p + T);
         }
     };
-    auto phase_b = [&](int tile, const unsigned long long (&r0)[RPL], const unsigned long long (&r1)[RPL], int pb) {
-        const int b = sample_of(tile);
+    auto phase_b = [&](const float4 (&v)[NV], int j, int pb) {
+        const int b = b0 + j * spr;
         settle(r0);
         settle(r1);
         if (merger) {
@@ -368,9 +390,9 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
             float n = 0.0f, m = 0.0f, q = 0.0f;
 #pragma unroll
             for (int u = 0; u < RPL; ++u) {
-                const unsigned long long* p = rec_slot(tile / T, rg, rj + u * LPG);
-                const float mj = rec_wait(p, r0[u], epoch, spin_limit, wk.err);
-                const float qj = rec_wait(p + T, r1[u], epoch, spin_limit, wk.err);
+                const unsigned long long* p = rec_slot(j, rg, rj + u * LPG);
+                const float mj = rec_wait(p, r0[u], epoch, spin_limit, wf);
+                const float qj = rec_wait(p + T, r1[u], epoch, spin_limit, wf);
                 if (u == 0) {
                     n = ntile;
                     m = mj;
@@ -406,77 +428,90 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
         float* ys = y + (size_t)b * sh.HW * sh.C + (size_t)(t * Gm::TP + row0) * sh.C + c0;
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
-            const float4 v = parked[k * TPB + tid];
             float4 o;
-            o.x = act_fwd<ACT>(fmaf(v.x, sc.x, s0.x));
-            o.y = act_fwd<ACT>(fmaf(v.y, sc.y, s0.y));
-            o.z = act_fwd<ACT>(fmaf(v.z, sc.z, s0.z));
-            o.w = act_fwd<ACT>(fmaf(v.w, sc.w, s0.w));
+            o.x = act_fwd<ACT>(fmaf(v[k].x, sc.x, s0.x));
+            o.y = act_fwd<ACT>(fmaf(v[k].y, sc.y, s0.y));
+            o.z = act_fwd<ACT>(fmaf(v[k].z, sc.z, s0.z));
+            o.w = act_fwd<ACT>(fmaf(v[k].w, sc.w, s0.w));
             stS<NT>(ys + (size_t)(k * Gm::RSTEP) * sh.C, o);
         }
     };
 
-    // Tile i = round * P + w; its sample = i / (NCB * T).  The rounds are laid
-    // out as prologue / steady loop / last tile / final phase B so that the
-    // steady loop has no branch around its loads: the compiler's waits for the
-    // records and the staged tile then count only older operations instead of
-    // draining the counter at a control-flow merge.
-    const int nt = sh.ntiles;
+    // Round j: wait for stage buffer j % 2; take tile j into registers;
+    // issue the loads of tile j + 2 into the same buffer; phase A on tile j;
+    // phase B on tile j - 2 (in registers since round j - 2); prefetch the
+    // records of tile j - 1, which phase B reads in the next round.  Two
+    // tiles are in flight while a round computes, and a tile's records have
+    // two rounds to arrive, so the exchange round trip (agent-scope store,
+    // then load) stays off the critical path.  The register sets S0, S1, S2
+    // hold tile j in S[j % 3]; the steady loop is unrolled by three so that
+    // no tile is ever copied between registers.  Every round issues the same
+    // vector-memory operations (loads past the last tile are issued against
+    // an empty range) and the rounds without a phase B are peeled, so the
+    // stage waits are constants:
+    //   round 0: tile 1's NV loads were issued after tile 0's;
+    //   round 1: round 0 issued NV loads;
+    //   round 2: round 1 issued NV loads and 2 RPL record loads;
+    //   round j >= 3: round j - 1 issued NV loads, NV stores, 2 RPL record loads.
     if (w >= nt) return;
-    float4 v[NV];
-    auto take = [&]() {
-#pragma unroll
-        for (int k = 0; k < NV; ++k) v[k] = stage[k * TPB + tid];
+    const int K = (nt - w + P - 1) / P;
+    float4 S0[NV], S1[NV], S2[NV];
+    int pb = 0;
+    auto steady_round = [&](int j, float4 (&cur)[NV], const float4 (&old)[NV]) {  // j >= 3
+        vm_wait<2 * NV + 2 * RPL>();
+        take(cur, j & 1);
+        issue(j + 2, j & 1);
+        phase_a(cur, j, pb);
+        phase_b(old, j - 2, pb);
+        records_prefetch(j - 1);
+        pb ^= 1;
     };
-    auto park = [&]() {
-#pragma unroll
-        for (int k = 0; k < NV; ++k) parked[k * TPB + tid] = v[k];
-    };
-    unsigned long long r0[RPL] = {}, r1[RPL] = {};
-    int tA = w, pb = 0;
-    issue(tA);
-    take();
-    if (tA + P < nt) {
-        lds_reads_done();
-        issue(tA + P);
-    }
-    phase_a(v, tA, pb);
-    park();
-    int tB = tA;
-    tA += P;
+    issue(0, 0);
+    issue(1, 1);
+    vm_wait<NV>();
+    take(S0, 0);
+    issue(2, 0);
+    phase_a(S0, 0, pb);
     pb ^= 1;
-    // Tile tB's records are requested right after this workgroup's own
-    // phase A of it, a round before phase B reads them.
-    records_prefetch(tB, r0, r1);
-    // With an activation that costs next to nothing (identity, ReLU) phase A
-    // is short, and half of the next tile's loads are issued after it, which
-    // spreads the requests over the round (identity forward 386 -> 366 us at
-    // the north-star shape).  With SiLU and the like the split measured no
-    // better than issuing the whole tile at once.
-    constexpr int kFirst = split_prefetch<ACT>() ? NV / 2 : NV;
-    while (tA + P < nt) {
-        take();
-        lds_reads_done();
-        issue_part(tA + P, std::integral_constant<int, 0>{}, std::integral_constant<int, kFirst>{});
-        phase_a(v, tA, pb);
-        issue_part(tA + P, std::integral_constant<int, kFirst>{}, std::integral_constant<int, NV>{});
-        phase_b(tB, r0, r1, pb);
-        park();
-        tB = tA;
-        tA += P;
+    if (K > 1) {
+        vm_wait<NV>();
+        take(S1, 1);
+        issue(3, 1);
+        phase_a(S1, 1, pb);
+        records_prefetch(0);
         pb ^= 1;
-        records_prefetch(tB, r0, r1);
-    }
-    if (tA < nt) {
-        take();
-        phase_a(v, tA, pb);
-        phase_b(tB, r0, r1, pb);
-        park();
-        tB = tA;
+        if (K > 2) {
+            vm_wait<NV + 2 * RPL>();
+            take(S2, 0);
+            issue(4, 0);
+            phase_a(S2, 2, pb);
+            phase_b(S0, 0, pb);
+            records_prefetch(1);
+            pb ^= 1;
+            int j = 3;
+            for (; j + 2 < K; j += 3) {
+                steady_round(j, S0, S1);
+                steady_round(j + 1, S1, S2);
+                steady_round(j + 2, S2, S0);
+            }
+            if (j < K) steady_round(j, S0, S1);
+            if (j + 1 < K) steady_round(j + 1, S1, S2);
+        }
+        // phase B of tiles K - 2 and K - 1, in S[(K - 2) % 3] and S[(K - 1) % 3]
+        const int km = K % 3;
+        if (km == 2) phase_b(S0, K - 2, pb);
+        else if (km == 0) phase_b(S1, K - 2, pb);
+        else phase_b(S2, K - 2, pb);
         pb ^= 1;
-        records_prefetch(tB, r0, r1);
     }
-    phase_b(tB, r0, r1, pb);
+    records_prefetch(K - 1);
+    {
+        const int km = K % 3;
+        if (km == 1) phase_b(S0, K - 1, pb);
+        else if (km == 2) phase_b(S1, K - 1, pb);
+        else phase_b(S2, K - 1, pb);
+    }
+    vm_wait<0>();  // the loads past the last tile write the stage: let them land before the workgroup ends
     // the last active workgroup to finish advances the workspace's epoch
     __shared__ unsigned arrived;
     __syncthreads();
@@ -502,8 +537,11 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
     unsigned spin_limit) {
 #pragma clang fp contract(fast)
     constexpr int NW = Gm::NW, NV = Gm::NV, GT = Gm::GT, TPB = Gm::TPB, CW4 = Gm::CW4;
-    __shared__ float4 stage[2 * NV * TPB];      // x then dy of the next tile (direct-to-LDS loads)
-    __shared__ float4 parked[2 * NV * TPB];     // xhat then g of the tile awaiting phase B
+    static_assert(NV == 2 && TPB * 16 == 16384, "stage slots (x then dy) as lds_take4 reads them");
+    // Two stage buffers (x then dy of the tiles of the next two rounds,
+    // direct-to-LDS loads); the tiles awaiting phase B (xhat, g) stay in
+    // registers.
+    __shared__ float4 stage[2][2 * NV * TPB];
     __shared__ float2 wred[2][GT][NW];          // (S1, S2) partials, laid out as in the forward
     __shared__ float2 stat[2][GT];              // group means of g and g * xhat
     __shared__ float cred[NW][CW4][8];          // per-wave dgamma/dbeta sums at the end (then the reducer's)
@@ -525,45 +563,63 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
     settle(bt);
     const unsigned epoch = launch_epoch(wk);
     const unsigned long long tag = (unsigned long long)epoch << 32;
+    const WaitFail wf{wk.err, wk.hflag};
+    // A spin limit of 0 lets no wait succeed: the launch flags itself as
+    // timed out (the error path, forced from the host for its tests).
+    if (spin_limit == 0 && blockIdx.x == 0 && threadIdx.x == 0) wait_failed(wf);
     const int LPG = T / RPL;
     const int rg = tid / LPG, rj = tid % LPG;
     const bool merger = rg < GT;
+    const int nt = sh.ntiles;
     float4 cg = make_float4(0.0f, 0.0f, 0.0f, 0.0f), cbs = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 
-    auto sample_of = [&](int tile) { return tile / (NCB * T); };
-    // Record layout [unit = sample * NCB + column block][group][value][pixel tile]:
-    // the mergers of a group read consecutive tiles, i.e. contiguous records.
-    auto rec_slot = [&](int unit, int g, int tt) { return wk.rec + ((size_t)(unit * GT + g) * 2) * T + tt; };
-    // loads of x (X) and / or dy (D) of `tile` into the stage
-    auto issue_part = [&](int tile, auto xc, auto dc) {
-        const size_t so = (size_t)sample_of(tile) * sh.HW * sh.C;
-        const __amdgpu_buffer_rsrc_t rx = sample_rsrc(x + so, sh.sample_bytes);
-        const __amdgpu_buffer_rsrc_t rd = sample_rsrc(dy + so, sh.sample_bytes);
+    // Round j works on this workgroup's tile w + j * P (see the forward).
+    const int b0 = w / (NCB * T), spr = P / (NCB * T);
+    const int u0 = w / T, upr = P / T;
+    auto real_of = [&](int j) { return w + j * P < nt; };
+    // Record layout [unit][group][value][pixel tile]: the mergers of a group
+    // read consecutive tiles, i.e. contiguous records.
+    auto rec_slot = [&](int j, int g, int tt) { return wk.rec + ((size_t)((u0 + j * upr) * GT + g) * 2) * T + tt; };
+    // The x and dy loads of round j's tile into stage buffer sb (2 NV).  A
+    // tile past the end is issued against an empty buffer range: the loads
+    // read nothing and only keep the operation count of every round the same.
+    auto issue = [&](int j, int sb) {
+        const bool real = real_of(j);
+        const size_t so = (size_t)(real ? b0 + j * spr : 0) * sh.HW * sh.C;
+        const uint32_t bytes = real ? sh.sample_bytes : 0u;
+        const __amdgpu_buffer_rsrc_t rx = sample_rsrc(x + so, bytes);
+        const __amdgpu_buffer_rsrc_t rd = sample_rsrc(dy + so, bytes);
         const uint32_t base = (uint32_t)(t * Gm::TP) * row_bytes;
-        if constexpr (decltype(xc)::value) {
 #pragma unroll
-            for (int k = 0; k < NV; ++k)
-                dma16<NT>(rx, stage + k * TPB + wid * kWave, voff, base + (uint32_t)(k * Gm::RSTEP) * row_bytes);
-        }
-        if constexpr (decltype(dc)::value) {
+        for (int k = 0; k < NV; ++k)
+            dma16<NT>(rx, &stage[sb][k * TPB + wid * kWave], voff, base + (uint32_t)(k * Gm::RSTEP) * row_bytes);
 #pragma unroll
-            for (int k = 0; k < NV; ++k)
-                dma16<NT>(rd, stage + (NV + k) * TPB + wid * kWave, voff, base + (uint32_t)(k * Gm::RSTEP) * row_bytes);
-        }
+        for (int k = 0; k < NV; ++k)
+            dma16<NT>(rd, &stage[sb][(NV + k) * TPB + wid * kWave], voff,
+                base + (uint32_t)(k * Gm::RSTEP) * row_bytes);
     };
-    auto issue = [&](int tile) { issue_part(tile, std::true_type{}, std::true_type{}); };
-    // phase A: xv -> xhat, gv -> g in place; per-group S1 = sum g, S2 = sum g*xhat -> records
-    auto phase_a = [&](float4 (&xv)[NV], float4 (&gv)[NV], int tile, float mean, float rs, int pb) {
+    auto take = [&](float4 (&v)[2 * NV], int sb) { lds_take4(v, lds_addr(&stage[sb][tid])); };
+    // Mean and rstd of this lane's group in round j's sample (two loads; a
+    // tile past the end reads the last sample's and never uses them).
+    float mean, rs;
+    auto load_stats = [&](int j) {
+        const int b = real_of(j) ? b0 + j * spr : sh.B - 1;
+        mean = mu[b * sh.G + gglob];
+        rs = rstd[b * sh.G + gglob];
+    };
+    // phase A: v[0..NV) = x -> xhat, v[NV..2NV) = dy -> g in place; per-group
+    // S1 = sum g, S2 = sum g*xhat -> records
+    auto phase_a = [&](float4 (&v)[2 * NV], int j, int pb) {
         float4 s1v = make_float4(0.0f, 0.0f, 0.0f, 0.0f), s2v = s1v;
         const float nms = -mean * rs;
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
             float4 xh, d;
-            xh.x = fmaf(xv[k].x, rs, nms);
-            xh.y = fmaf(xv[k].y, rs, nms);
-            xh.z = fmaf(xv[k].z, rs, nms);
-            xh.w = fmaf(xv[k].w, rs, nms);
-            d = gv[k];
+            xh.x = fmaf(v[k].x, rs, nms);
+            xh.y = fmaf(v[k].y, rs, nms);
+            xh.z = fmaf(v[k].z, rs, nms);
+            xh.w = fmaf(v[k].w, rs, nms);
+            d = v[NV + k];
             if constexpr (ACT != ACT_IDENTITY) {
                 d.x = d.x * act_grad<ACT>(gm.x * xh.x + bt.x);
                 d.y = d.y * act_grad<ACT>(gm.y * xh.y + bt.y);
@@ -591,8 +647,8 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
             s2v.y = fmaf(g.y, xh.y, s2v.y);
             s2v.z = fmaf(g.z, xh.z, s2v.z);
             s2v.w = fmaf(g.w, xh.w, s2v.w);
-            xv[k] = xh;
-            gv[k] = g;
+            v[k] = xh;
+            v[NV + k] = g;
         }
         float s1 = (s1v.x + s1v.y) + (s1v.z + s1v.w);
         float s2 = (s2v.x + s2v.y) + (s2v.z + s2v.w);
@@ -614,7 +670,7 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
                 c += __shfl_xor(c, o, kWave);
             }
             if (i == 0) {
-                unsigned long long* r = rec_slot(tile / T, g, tile % T);
+                unsigned long long* r = rec_slot(j, g, t);
                 rec_store(r, tagged(tag, a));
                 rec_store(r + T, tagged(tag, c));
             }
@@ -622,28 +678,30 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
     };
     // Every lane loads (lanes past the mergers read group GT-1 and ignore it):
     // a branch here would put a path without these loads in front of the
-    // staged-tile wait.
-    auto records_prefetch = [&](int tile, unsigned long long (&r0)[RPL], unsigned long long (&r1)[RPL]) {
+    // record waits.
+    unsigned long long r0[RPL] = {}, r1[RPL] = {};
+    auto records_prefetch = [&](int j) {
         const int rgc = merger ? rg : GT - 1;
 #pragma unroll
         for (int u = 0; u < RPL; ++u) {
-            const unsigned long long* p = rec_slot(tile / T, rgc, rj + u * LPG);
+            const unsigned long long* p = rec_slot(j, rgc, rj + u * LPG);
             r0[u] = rec_load(p);
             r1[u] = rec_load(p + T);
         }
     };
-    auto phase_b = [&](int tile, const unsigned long long (&r0)[RPL], const unsigned long long (&r1)[RPL],
-                       float rs, int pb) {
-        const int b = sample_of(tile);
+    // phase B on a parked tile (xhat, g in v, its rstd rsv): merge its
+    // records, form dx, store
+    auto phase_b = [&](const float4 (&v)[2 * NV], float rsv, int j, int pb) {
+        const int b = b0 + j * spr;
         settle(r0);
         settle(r1);
         if (merger) {
             float a = 0.0f, c = 0.0f;
 #pragma unroll
             for (int u = 0; u < RPL; ++u) {
-                const unsigned long long* p = rec_slot(tile / T, rg, rj + u * LPG);
-                a += rec_wait(p, r0[u], epoch, spin_limit, wk.err);
-                c += rec_wait(p + T, r1[u], epoch, spin_limit, wk.err);
+                const unsigned long long* p = rec_slot(j, rg, rj + u * LPG);
+                a += rec_wait(p, r0[u], epoch, spin_limit, wf);
+                c += rec_wait(p + T, r1[u], epoch, spin_limit, wf);
             }
             for (int o = 1; o < LPG; o <<= 1) {
                 a += __shfl_xor(a, o, kWave);
@@ -654,108 +712,106 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
         lds_barrier();
         // dx = rs * ((g - m1) - xhat * m2) = g * rs + (xhat * (-rs m2) + (-rs m1))
         const float2 st = stat[pb][gl];
-        const float a1 = -rs * st.x, a2 = -rs * st.y;
+        const float a1 = -rsv * st.x, a2 = -rsv * st.y;
         float* dxs = dx + (size_t)b * sh.HW * sh.C + (size_t)(t * Gm::TP + row0) * sh.C + c0;
-        // A short pause before the tile's dx stores (see store_pause).
-#pragma unroll
-        for (int ip = 0; ip < store_pause<ACT>(); ++ip) __builtin_amdgcn_s_sleep(1);
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
-            const float4 xh = parked[k * TPB + tid];
-            const float4 g = parked[(NV + k) * TPB + tid];
+            const float4 xh = v[k];
+            const float4 g = v[NV + k];
             float4 o;
-            o.x = fmaf(g.x, rs, fmaf(xh.x, a2, a1));
-            o.y = fmaf(g.y, rs, fmaf(xh.y, a2, a1));
-            o.z = fmaf(g.z, rs, fmaf(xh.z, a2, a1));
-            o.w = fmaf(g.w, rs, fmaf(xh.w, a2, a1));
+            o.x = fmaf(g.x, rsv, fmaf(xh.x, a2, a1));
+            o.y = fmaf(g.y, rsv, fmaf(xh.y, a2, a1));
+            o.z = fmaf(g.z, rsv, fmaf(xh.z, a2, a1));
+            o.w = fmaf(g.w, rsv, fmaf(xh.w, a2, a1));
             stS<NT>(dxs + (size_t)(k * Gm::RSTEP) * sh.C, o);
         }
     };
 
-    // Rounds laid out as in the forward (prologue / steady loop / last tile /
-    // final phase B); mean and rstd of a tile are loaded with its data.
-    const int nt = sh.ntiles;
+    // Rounds as in the forward: round j waits for stage buffer j % 2, takes
+    // tile j, issues tile j + 2's loads, runs phase A on tile j, loads tile
+    // j + 1's statistics into the registers phase A has just used (a load
+    // into a register that is then copied would make the copy wait for it),
+    // runs phase B on tile j - 2 and prefetches tile j - 1's records.  The
+    // backward keeps its tiles in v (tile j), pk1 (j - 1) and pk2 (j - 2) and
+    // moves them along each round: unrolled by three as in the forward it
+    // needs more than the 128 VGPRs a 1024-thread workgroup has and spills.
+    // Stage waits (operations issued after the buffer's loads):
+    //   round 0: tile 1's 2 NV loads;
+    //   round 1: round 0's 2 NV tile loads and 2 statistics loads;
+    //   round 2: round 1's 2 NV + 2 loads and 2 RPL record loads;
+    //   round j >= 3: round j - 1's 2 NV + 2 loads, NV stores, 2 RPL record loads.
     if (w < nt) {
-        float4 xv[NV], gv[NV];
-        auto take = [&]() {
+        const int K = (nt - w + P - 1) / P;
+        float4 v[2 * NV], pk1[2 * NV], pk2[2 * NV];
+        float rs1 = 0.0f, rs2 = 0.0f;  // rstd of tiles j - 1 and j - 2
+        auto rotate = [&](float rs_j) {
 #pragma unroll
-            for (int k = 0; k < NV; ++k) {
-                xv[k] = stage[k * TPB + tid];
-                gv[k] = stage[(NV + k) * TPB + tid];
+            for (int k = 0; k < 2 * NV; ++k) {
+                pk2[k] = pk1[k];
+                pk1[k] = v[k];
             }
+            rs2 = rs1;
+            rs1 = rs_j;
         };
-        auto park = [&]() {
-#pragma unroll
-            for (int k = 0; k < NV; ++k) {
-                parked[k * TPB + tid] = xv[k];
-                parked[(NV + k) * TPB + tid] = gv[k];
-            }
-        };
-        float meanA, rsA, meanN = 0.0f, rsN = 0.0f;
-        auto issue_with_stats = [&](int tile, float& mean, float& rs) {
-            const int b = sample_of(tile);
-            mean = mu[b * sh.G + gglob];
-            rs = rstd[b * sh.G + gglob];
-            issue(tile);
-        };
-        unsigned long long r0[RPL] = {}, r1[RPL] = {};
-        int tA = w, pb = 0;
-        issue_with_stats(tA, meanA, rsA);
-        take();
-        if (tA + P < nt) {
-            lds_reads_done();
-            issue_with_stats(tA + P, meanN, rsN);
+        int pb = 0;
+        load_stats(0);
+        issue(0, 0);
+        issue(1, 1);
+        vm_wait<2 * NV>();
+        take(v, 0);
+        issue(2, 0);
+        phase_a(v, 0, pb);
+        {
+            const float rs_j = rs;
+            load_stats(1);
+            rotate(rs_j);
         }
-        phase_a(xv, gv, tA, meanA, rsA, pb);
-        park();
-        int tB = tA;
-        float rsB = rsA;
-        tA += P;
-        meanA = meanN;
-        rsA = rsN;
         pb ^= 1;
-        // The records of tile tB are requested as soon as this workgroup's
-        // own phase A of it is done, a whole round before phase B needs them
-        // (with a short phase A, as for the identity, a request at the top of
-        // the round would still be in flight at phase B).
-        records_prefetch(tB, r0, r1);
-        while (tA + P < nt) {
-            take();
-            lds_reads_done();
-            // dy of the next tile after phase A when the activation is cheap
-            // (as in the forward: identity backward 609 -> 582 us; SiLU 570 ->
-            // 575 us, so there the whole tile goes at once)
-            if constexpr (split_prefetch<ACT>()) {
-                const int b = sample_of(tA + P);
-                meanN = mu[b * sh.G + gglob];
-                rsN = rstd[b * sh.G + gglob];
-                issue_part(tA + P, std::true_type{}, std::false_type{});
-            } else {
-                issue_with_stats(tA + P, meanN, rsN);
+        if (K > 1) {
+            vm_wait<2 * NV + 2>();
+            take(v, 1);
+            issue(3, 1);
+            phase_a(v, 1, pb);
+            {
+                const float rs_j = rs;
+                load_stats(2);
+                records_prefetch(0);
+                rotate(rs_j);
             }
-            phase_a(xv, gv, tA, meanA, rsA, pb);
-            if constexpr (split_prefetch<ACT>()) issue_part(tA + P, std::false_type{}, std::true_type{});
-            phase_b(tB, r0, r1, rsB, pb);
-            park();
-            tB = tA;
-            rsB = rsA;
-            tA += P;
-            meanA = meanN;
-            rsA = rsN;
             pb ^= 1;
-            records_prefetch(tB, r0, r1);
-        }
-        if (tA < nt) {
-            take();
-            phase_a(xv, gv, tA, meanA, rsA, pb);
-            phase_b(tB, r0, r1, rsB, pb);
-            park();
-            tB = tA;
-            rsB = rsA;
+            if (K > 2) {
+                vm_wait<2 * NV + 2 + 2 * RPL>();
+                take(v, 0);
+                issue(4, 0);
+                phase_a(v, 2, pb);
+                {
+                    const float rs_j = rs;
+                    load_stats(3);
+                    phase_b(pk2, rs2, 0, pb);
+                    records_prefetch(1);
+                    rotate(rs_j);
+                }
+                pb ^= 1;
+                for (int j = 3; j < K; ++j) {
+                    vm_wait<3 * NV + 2 + 2 * RPL>();
+                    take(v, j & 1);
+                    issue(j + 2, j & 1);
+                    phase_a(v, j, pb);
+                    const float rs_j = rs;
+                    load_stats(j + 1);
+                    phase_b(pk2, rs2, j - 2, pb);
+                    records_prefetch(j - 1);
+                    rotate(rs_j);
+                    pb ^= 1;
+                }
+            }
+            // tiles K - 2 and K - 1 (now pk2 and pk1)
+            phase_b(pk2, rs2, K - 2, pb);
             pb ^= 1;
-            records_prefetch(tB, r0, r1);
         }
-        phase_b(tB, r0, r1, rsB, pb);
+        records_prefetch(K - 1);
+        phase_b(pk1, rs1, K - 1, pb);
+        vm_wait<0>();  // the loads past the last tile write the stage: let them land before it is reused
     }
 
     // dgamma/dbeta partials of this workgroup: lanes with equal column own the
@@ -799,7 +855,7 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
     {
         const int v = tid % NVAL, q = tid / NVAL;  // q is uniform over the wave (NVAL >= 64)
         const unsigned long long* src = wk.part + ((size_t)team * T + q) * NVAL + v;
-        chain[q][v] = rec_sum<16>(src, (size_t)Q * NVAL, (T - q + Q - 1) / Q, epoch, spin_limit, wk.err);
+        chain[q][v] = rec_sum<16>(src, (size_t)Q * NVAL, (T - q + Q - 1) / Q, epoch, spin_limit, wf);
     }
     __syncthreads();
     for (int v = tid; v < NVAL; v += TPB) {
@@ -824,7 +880,7 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
         const int cbc = c / (CW4 * 4), cl = c % (CW4 * 4);
         const unsigned long long* p = wk.tpart + (size_t)cbc * NVAL + d * (CW4 * 4) + cl;
         (d ? gbeta : ggamma)[c] = rec_sum<4>(p, (size_t)NCB * NVAL, (nteams - cbc + NCB - 1) / NCB, epoch,
-                                             spin_limit, wk.err);
+                                             spin_limit, wf);
     }
     if (tid == 0) {
         publish_epoch(wk, epoch);  // every workgroup has arrived, so all have read the old one

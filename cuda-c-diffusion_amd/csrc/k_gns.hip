@@ -82,6 +82,17 @@ void nnk_clear_workspace(float* ws, size_t n_floats, hipStream_t s) {
     gns_clear<<<dim3((unsigned)blocks), dim3(256), 0, s>>>(reinterpret_cast<unsigned*>(ws), n_floats);
 }
 
+// Polls of one statistics record before a wait gives up: kSpinLimit, or
+// NNHIP_GN_SPIN_LIMIT when it is a number no larger (read per launch, so a
+// test can force the wait-failure path: 0 makes every launch flag itself).
+unsigned nnk_gns_spin_limit() {
+    const char* e = getenv("NNHIP_GN_SPIN_LIMIT");
+    if (!e || !*e) return nnk::gns::kSpinLimit;
+    char* end = nullptr;
+    const unsigned long v = strtoul(e, &end, 10);
+    return (end && *end == '\0' && v <= nnk::gns::kSpinLimit) ? (unsigned)v : nnk::gns::kSpinLimit;
+}
+
 // Launch a persistent grid: a plain launch (its progress does not depend on
 // residency; see gn_stream.h), or a cooperative one with
 // NNHIP_GN_COOPERATIVE=1 for callers that run streaming GroupNorms

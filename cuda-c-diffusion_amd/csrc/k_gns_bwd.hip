@@ -4,6 +4,7 @@
 
 int nnk_gns_grid(const void* fn, int key, size_t lds, int unit);
 bool nnk_gns_launch(const void* fn, int P, void** args, hipStream_t s, const char* what);
+unsigned nnk_gns_spin_limit();
 
 namespace {
 
@@ -22,12 +23,14 @@ bool launch(const Plan& p, float* dx, float* ggamma, float* gbeta, const float* 
     Shape sh = p.sh;
     Work wk;
     wk.err = reinterpret_cast<unsigned*>(ws);
+    unsigned* hf = nnk_wait_flag(s);
+    wk.hflag = hf ? hf : wk.err;
     wk.ep = reinterpret_cast<unsigned*>(ws) + 1;
     wk.count = reinterpret_cast<unsigned*>(reinterpret_cast<char*>(ws) + kCountOffset);
     wk.rec = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(ws) + p.rec_offset);
     wk.part = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(ws) + p.part_offset);
     wk.tpart = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(ws) + p.tpart_offset);
-    unsigned limit = kSpinLimit;
+    unsigned limit = nnk_gns_spin_limit();
     void* args[] = {&dx, &ggamma, &gbeta, const_cast<float**>(&dy), const_cast<float**>(&x), const_cast<float**>(&gamma),
         const_cast<float**>(&beta), const_cast<float**>(&mu), const_cast<float**>(&rstd), &sh, &wk,
         &limit};

@@ -4,6 +4,7 @@
 
 int nnk_gns_grid(const void* fn, int key, size_t lds, int unit);
 bool nnk_gns_launch(const void* fn, int P, void** args, hipStream_t s, const char* what);
+unsigned nnk_gns_spin_limit();
 
 namespace {
 
@@ -22,12 +23,14 @@ bool launch(const Plan& p, float* y, float* mu, float* rstd, const float* x, con
     Shape sh = p.sh;
     Work wk;
     wk.err = reinterpret_cast<unsigned*>(ws);
+    unsigned* hf = nnk_wait_flag(s);
+    wk.hflag = hf ? hf : wk.err;
     wk.ep = reinterpret_cast<unsigned*>(ws) + 1;
     wk.count = reinterpret_cast<unsigned*>(reinterpret_cast<char*>(ws) + kCountOffset);
     wk.rec = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(ws) + p.rec_offset);
     wk.part = nullptr;
     wk.tpart = nullptr;
-    unsigned limit = kSpinLimit;
+    unsigned limit = nnk_gns_spin_limit();
     void* args[] = {&y, &mu, &rstd, const_cast<float**>(&x), const_cast<float**>(&gamma),
         const_cast<float**>(&beta), &sh, &wk, &eps, &limit};
     return nnk_gns_launch(fn, P, args, s, "streaming GroupNorm forward");

@@ -368,14 +368,27 @@ __device__ __forceinline__ unsigned long long rec_load(const unsigned long long*
     return __hip_atomic_load(const_cast<unsigned long long*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Where a bounded wait that gives up leaves its mark: the sticky word of the
+// launch's workspace (nnhip_groupnorm_workspace_status reads it) and a
+// process-wide word in host-mapped memory, which nnhip_get_last_error reads
+// without synchronising the device.  Written only on that failure path.
+struct WaitFail {
+    unsigned* ws;
+    unsigned* host;
+};
+__device__ __forceinline__ void wait_failed(const WaitFail& f) {
+    atomicOr(f.ws, 1u);
+    __hip_atomic_store(f.host, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 // Poll one record until it carries `epoch`, at most spin_limit times (each
-// poll sleeps first); past that set *err and return what is there.
+// poll sleeps first); past that flag the failure and return what is there.
 __device__ __forceinline__ float rec_wait(const unsigned long long* p, unsigned long long r, unsigned epoch,
-    unsigned spin_limit, unsigned* err) {
+    unsigned spin_limit, const WaitFail& fail) {
     unsigned n = 0;
     while ((unsigned)(r >> 32) != epoch) {
         if (++n > spin_limit) {
-            atomicOr(err, 1u);
+            wait_failed(fail);
             break;
         }
         __builtin_amdgcn_s_sleep(1);
@@ -387,11 +400,11 @@ __device__ __forceinline__ float rec_wait(const unsigned long long* p, unsigned 
 // Sum of the n tagged records p[0], p[stride], ... in index order, KB loads
 // in flight.  The records of a batch that do not carry `epoch` yet are loaded
 // again together, so a batch costs one round trip per poll rather than one
-// per late record; past spin_limit polls *err is set and the sum is taken as
-// it stands.  n must be uniform over the wave.
+// per late record; past spin_limit polls the failure is flagged and the sum
+// is taken as it stands.  n must be uniform over the wave.
 template <int KB>
 __device__ __forceinline__ float rec_sum(const unsigned long long* p, size_t stride, int n, unsigned epoch,
-    unsigned spin_limit, unsigned* err) {
+    unsigned spin_limit, const WaitFail& fail) {
     float acc = 0.0f;
     for (int m = 0; m < n; m += KB) {
         const int nb = n - m < KB ? n - m : KB;
@@ -405,7 +418,7 @@ __device__ __forceinline__ float rec_sum(const unsigned long long* p, size_t str
             for (int u = 0; u < KB; ++u) late |= u < nb && (unsigned)(r[u] >> 32) != epoch;
             if (!late) break;
             if (polls >= spin_limit) {
-                atomicOr(err, 1u);
+                wait_failed(fail);
                 break;
             }
             __builtin_amdgcn_s_sleep(1);
@@ -442,6 +455,11 @@ void nnk_scratch_forget_stream(hipStream_t s);
 // Zero n_floats words of a workspace drawn from the scratch pool (a fill
 // kernel, so that the sequence can be captured in a graph).
 void nnk_clear_workspace(float* ws, size_t n_floats, hipStream_t s);
+// Device address of the process-wide host-mapped word that a streaming
+// kernel's bounded wait sets when it gives up (see WaitFail), allocated by
+// the first call outside stream capture; nullptr before that or when it
+// could not be allocated.
+unsigned* nnk_wait_flag(hipStream_t s);
 
 #define NNK_REQUIRE(cond, what, ...)                         \
     do {                                                     \

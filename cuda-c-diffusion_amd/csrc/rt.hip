@@ -64,10 +64,54 @@ bool nnk_capturing(hipStream_t s) {
     return s && hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
 }
 
+// The process-wide word that a streaming kernel's bounded wait sets when it
+// gives up: host memory mapped into the device's address space (coherent, so
+// the kernel's system-scope store is visible to the host once it is done),
+// allocated on first use and kept until the process ends.
+namespace {
+std::mutex g_wait_flag_mu;
+unsigned* g_wait_flag_host = nullptr;
+unsigned* g_wait_flag_dev = nullptr;
+bool g_wait_flag_failed = false;
+
+// Move a wait failure the device has flagged into the error record.
+void take_wait_flag() {
+    unsigned* h = __atomic_load_n(&g_wait_flag_host, __ATOMIC_ACQUIRE);
+    if (!h || __atomic_load_n(h, __ATOMIC_ACQUIRE) == 0) return;
+    __atomic_store_n(h, 0u, __ATOMIC_RELAXED);
+    nnk_set_error((int)hipErrorLaunchTimeOut,
+        "streaming GroupNorm: a statistics wait ran out of polls; the outputs of that launch are invalid");
+}
+}  // namespace
+
+unsigned* nnk_wait_flag(hipStream_t s) {
+    std::lock_guard<std::mutex> lock(g_wait_flag_mu);
+    // allocated outside stream capture only (a capture that comes first
+    // reports wait failures through the workspace word alone)
+    if (!g_wait_flag_dev && !g_wait_flag_failed && !nnk_capturing(s)) {
+        void* p = nullptr;
+        void* d = nullptr;
+        if (hipHostMalloc(&p, 64, hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess || !p ||
+            hipHostGetDevicePointer(&d, p, 0) != hipSuccess || !d) {
+            (void)hipGetLastError();
+            if (p) (void)hipHostFree(p);
+            g_wait_flag_failed = true;
+            nnk_path_note("host-mapped wait flag: allocation failed; wait failures are reported per workspace only");
+        } else {
+            memset(p, 0, 64);
+            g_wait_flag_dev = static_cast<unsigned*>(d);
+            __atomic_store_n(&g_wait_flag_host, static_cast<unsigned*>(p), __ATOMIC_RELEASE);
+        }
+    }
+    return g_wait_flag_dev;
+}
+
 void nnk_after_launch(const char* what, hipStream_t s) {
     hipError_t e = hipGetLastError();
-    if (e == hipSuccess && check_mode() && !nnk_capturing(s)) e = hipStreamSynchronize(s);
+    const bool sync = e == hipSuccess && check_mode() && !nnk_capturing(s);
+    if (sync) e = hipStreamSynchronize(s);
     if (e != hipSuccess) nnk_set_error((int)e, "%s: %s", what, hipGetErrorString(e));
+    else if (sync) take_wait_flag();
 }
 
 // Scratch for launchers whose reference signature has no workspace argument.
@@ -241,6 +285,7 @@ __global__ __launch_bounds__(256) void copy_f32_kernel(float* __restrict__ dst,
 extern "C" {
 
 int nnhip_get_last_error(char* buf, int buflen) {
+    if (g_err.code == 0) take_wait_flag();
     const int code = g_err.code;
     if (buf && buflen > 0) {
         strncpy(buf, g_err.msg, (size_t)buflen - 1);

@@ -380,3 +380,109 @@ def test_stream_groupnorm_graph_replay(L, orc, rng, monkeypatch):
             L.dll.nnhip_graph_destroy(graph)
         L.dll.nnhip_stream_synchronize(s)
         L.dll.nnhip_stream_destroy(s)
+
+
+HIP_ERROR_LAUNCH_TIMEOUT = 702  # hipErrorLaunchTimeOut
+
+
+def test_wait_failure_surfaces_in_error_record(L, orc, rng, monkeypatch):
+    """A statistics wait that gives up is reported, not lost.  With
+    NNHIP_GN_SPIN_LIMIT=0 no wait may succeed (each kernel still runs to its
+    end); the failure reaches nnhip_get_last_error through the library's
+    host-mapped flag, once, for a lent workspace and for the reference-named
+    launchers that draw theirs from the stream's pool block.  Back at the
+    normal limit the same launches are clean and match the oracle."""
+    print("[case] stream groupnorm wait failure -> error record", flush=True)
+    monkeypatch.setenv("NNHIP_GN_PATH", "stream")
+    B, H, W, C, G = 2, 64, 64, 256, 32
+    HW = H * W
+    x, gamma, beta, dy = make_inputs(rng, B, H, W, C)
+    xd, dyd, yd, dxd = L.to_device(x), L.to_device(dy), L.alloc(x.size), L.alloc(x.size)
+    gd, bd, mu, rs, gg, gb = L.to_device(gamma), L.to_device(beta), L.alloc(B * G), L.alloc(B * G), L.alloc(C), L.alloc(C)
+    fws = zeroed(L, L.nnhip_groupnorm_forward_workspace(B, HW, C, G))
+    bws = zeroed(L, L.nnhip_groupnorm_backward_workspace(B, HW, C, G))
+
+    def fwd(ws):
+        if ws is None:
+            L.dll.launch_groupnorm_act_forward(yd.p, mu.p, rs.p, xd.p, gd.p, bd.p, B, HW, C, G, 1e-5, 3, None)
+        else:
+            L.dll.launch_groupnorm_act_forward_ws(yd.p, mu.p, rs.p, xd.p, gd.p, bd.p, B, HW, C, G, 1e-5, 3, ws.p, None)
+
+    def bwd(ws):
+        if ws is None:
+            L.dll.launch_groupnorm_act_backward(dxd.p, gg.p, gb.p, dyd.p, xd.p, gd.p, bd.p, mu.p, rs.p, B, HW, C, G, 3,
+                                                None)
+        else:
+            L.dll.launch_groupnorm_act_backward_ws(dxd.p, gg.p, gb.p, dyd.p, xd.p, gd.p, bd.p, mu.p, rs.p, B, HW, C, G,
+                                                   3, ws.p, None)
+
+    L.sync()
+    assert L.last_error()[0] == 0
+    monkeypatch.setenv("NNHIP_GN_SPIN_LIMIT", "0")
+    for what, launch, ws in (("forward, lent workspace", fwd, fws), ("backward, lent workspace", bwd, bws),
+                             ("forward, pool workspace", fwd, None), ("backward, pool workspace", bwd, None)):
+        launch(ws)
+        L.sync()
+        code, msg = L.last_error()
+        assert code == HIP_ERROR_LAUNCH_TIMEOUT and "ran out of polls" in msg, (what, code, msg)
+        assert L.last_error()[0] == 0, f"{what}: reported more than once"
+        if ws is not None:
+            assert L.nnhip_groupnorm_workspace_status(ws.p) == 1, what
+
+    monkeypatch.delenv("NNHIP_GN_SPIN_LIMIT")
+    fws2 = zeroed(L, L.nnhip_groupnorm_forward_workspace(B, HW, C, G))
+    bws2 = zeroed(L, L.nnhip_groupnorm_backward_workspace(B, HW, C, G))
+    for ws_f, ws_b in ((fws2, bws2), (None, None)):
+        fwd(ws_f)
+        bwd(ws_b)
+        L.sync()
+        assert L.last_error()[0] == 0
+        y_ref, mu_ref, rs_ref = orc.groupnorm_forward(x, gamma, beta, G, 1e-5, 3)
+        assert rel_err(yd.download(shape=x.shape), y_ref) <= TOL
+        dx_ref, _, _ = orc.groupnorm_backward(dy, x, gamma, beta, mu.download(), rs.download(), G, 3)
+        assert rel_err(dxd.download(shape=x.shape), dx_ref) <= TOL
+    assert L.nnhip_groupnorm_workspace_status(fws2.p) == 0 and L.nnhip_groupnorm_workspace_status(bws2.p) == 0
+
+
+def test_stream_groupnorm_beside_independent_work(L, orc, rng, monkeypatch):
+    """The plain launch's progress argument: workgroups wait only for their
+    own team, and whatever else holds the compute units ends by itself.  A
+    streaming GroupNorm+SiLU forward and backward (several rounds) runs on one
+    stream while another stream keeps the device busy with long elementwise
+    kernels.  Every wait finishes (status 0, no error) and the results match
+    the oracle."""
+    print("[case] stream groupnorm beside elementwise work on another stream", flush=True)
+    monkeypatch.setenv("NNHIP_GN_PATH", "stream")
+    monkeypatch.delenv("NNHIP_GN_COOPERATIVE", raising=False)
+    B, H, W, C, G = 16, 64, 64, 256, 32  # forward 4 rounds, backward 8 rounds of the persistent grid
+    HW = H * W
+    x, gamma, beta, dy = make_inputs(rng, B, H, W, C)
+    xd, dyd, yd, dxd = L.to_device(x), L.to_device(dy), L.alloc(x.size), L.alloc(x.size)
+    gd, bd, mu, rs, gg, gb = L.to_device(gamma), L.to_device(beta), L.alloc(B * G), L.alloc(B * G), L.alloc(C), L.alloc(C)
+    fws = zeroed(L, L.nnhip_groupnorm_forward_workspace(B, HW, C, G))
+    bws = zeroed(L, L.nnhip_groupnorm_backward_workspace(B, HW, C, G))
+    n_other = 1 << 27
+    a_in, a_out = L.alloc(n_other), L.alloc(n_other)
+    a_in.fill_bytes(0)
+    s_gn, s_other = L.dll.nnhip_stream_create(), L.dll.nnhip_stream_create()
+    try:
+        L.launch_activation_forward(a_out.p, a_in.p, n_other, 3, s_other)
+        for rep in range(3):
+            for _ in range(3):
+                L.launch_activation_forward(a_out.p, a_in.p, n_other, 3, s_other)
+            L.launch_groupnorm_act_forward_ws(yd.p, mu.p, rs.p, xd.p, gd.p, bd.p, B, HW, C, G, 1e-5, 3, fws.p, s_gn)
+            L.launch_groupnorm_act_backward_ws(dxd.p, gg.p, gb.p, dyd.p, xd.p, gd.p, bd.p, mu.p, rs.p, B, HW, C, G, 3,
+                                               bws.p, s_gn)
+        L.dll.nnhip_stream_synchronize(s_gn)
+        L.dll.nnhip_stream_synchronize(s_other)
+        L.sync()
+        L.check("beside independent work")
+        assert L.nnhip_groupnorm_workspace_status(fws.p) == 0 and L.nnhip_groupnorm_workspace_status(bws.p) == 0
+        y_ref, mu_ref, rs_ref = orc.groupnorm_forward(x, gamma, beta, G, 1e-5, 3)
+        assert rel_err(yd.download(shape=x.shape), y_ref) <= TOL
+        dx_ref, _, _ = orc.groupnorm_backward(dy, x, gamma, beta, mu_ref, rs_ref, G, 3)
+        assert rel_err(dxd.download(shape=x.shape), dx_ref) <= TOL
+    finally:
+        for s in (s_gn, s_other):
+            L.dll.nnhip_stream_synchronize(s)
+            L.dll.nnhip_stream_destroy(s)
