@@ -120,6 +120,7 @@ _SIGS = {
     "launch_groupnorm_act_forward_ws": (None, [P, P, P, P, P, P, I, I, I, I, F, I, P, P], True),
     "nnhip_layernorm_backward_workspace": (SZ, [I, I], False),
     "launch_groupnorm_act_backward_ws": (None, [P, P, P, P, P, P, P, P, P, I, I, I, I, I, P, P], True),
+    "launch_groupnorm_act_backward_noalloc": (None, [P, P, P, P, P, P, P, P, P, I, I, I, I, I, P], True),
     "launch_layernorm_backward_ws": (None, [P, P, P, P, P, P, P, P, I, I, P, P], True),
     "launch_col2im_set": (None, [P, P, I, I, I, I, I, I, I, I, I, P], True),
     "nnhip_multi_tensor_plan_create": (P, [P, I], True),

@@ -10,6 +10,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "gn_kernels.h"
 #include "gn_stream.h"
 
@@ -315,9 +317,12 @@ void gn_forward_impl(const char* what, float* y, float* mu, float* rstd, const f
     nnk_after_launch(what, s);
 }
 
+// ws: a lent workspace (nullptr: draw from the stream's pool block).
+// reg_ws: where the register and generic paths keep their 2 * B * C channel
+// partials (nullptr: in ws past its streaming region, or in the pool block).
 void gn_backward_impl(const char* what, float* dx, float* ggamma, float* gbeta, const float* dy,
     const float* x, const float* gamma, const float* beta, const float* mu, const float* rstd,
-    int B, int HW, int C, int G, int act, float* ws, hipStream_t s) {
+    int B, int HW, int C, int G, int act, float* ws, hipStream_t s, float* reg_ws = nullptr) {
     if (!shape_ok(what, B, HW, C, G)) return;
     NNK_REQUIRE(valid_act(act), what, "%s: unknown activation %d", what, act);
     NNK_REQUIRE(ggamma && gbeta, what, "%s: null pointer", what);
@@ -344,8 +349,8 @@ void gn_backward_impl(const char* what, float* dx, float* ggamma, float* gbeta, 
             return;
         }
     }
-    float* scratch = ws;
-    const size_t part_off = ws ? reg_partials_offset(B, HW, C, G) : 0;
+    float* scratch = reg_ws ? reg_ws : ws;
+    const size_t part_off = (ws && !reg_ws) ? reg_partials_offset(B, HW, C, G) : 0;
     if (!scratch) {
         scratch = nnk_scratch_acquire((size_t)2 * B * C, s, what);
         if (!scratch) return;
@@ -370,10 +375,58 @@ void gn_backward_impl(const char* what, float* dx, float* ggamma, float* gbeta, 
     }
     gn_param_reduce<<<dim3((unsigned)((C + kWave - 1) / kWave)), dim3(kRedTpb), 0, s>>>(ggamma,
         gbeta, part_g, part_b, B, C);
-    if (!ws) nnk_scratch_release(scratch, s);
+    if (!ws && !reg_ws) nnk_scratch_release(scratch, s);
     nnk_after_launch(what, s);
 }
 
+}  // namespace
+
+// Scratch of launch_groupnorm_act_backward_noalloc, for callers that cannot
+// allocate.  A device global: each device the library runs on holds its own
+// copy until the process ends; it is zero when the code object is loaded and
+// written only by that entry point.  The first kNoAllocStreamBytes are the
+// streaming kernels' workspace (header, epoch-tagged records and partials:
+// the epoch lives in the header, so records left by earlier calls never match
+// a later one and nothing needs clearing between calls); the rest holds the
+// register and generic paths' untagged channel partials, apart, so that a
+// streaming launch never reads them as records.
+constexpr size_t kNoAllocStreamBytes = 12u << 20;
+constexpr size_t kNoAllocPartialBytes = 4u << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocStreamBytes + kNoAllocPartialBytes];
+
+namespace {
+constexpr int kNoAllocDevices = 64;
+std::mutex g_noalloc_mu;
+float* g_noalloc_ptr[kNoAllocDevices] = {};  // address of `scratch` on each device
+
+// The address of `scratch` on the device of stream s (the current device for
+// the null stream), looked up once per device with that device current.
+float* noalloc_scratch(hipStream_t s, const char* what) {
+    int cur = -1, dev = -1;
+    hipError_t e = hipGetDevice(&cur);
+    if (e == hipSuccess) e = s ? hipStreamGetDevice(s, &dev) : hipGetDevice(&dev);
+    if (e != hipSuccess || dev < 0 || dev >= kNoAllocDevices) {
+        nnk_set_error(e != hipSuccess ? (int)e : (int)hipErrorInvalidDevice, "%s: no device for the stream", what);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    if (!g_noalloc_ptr[dev]) {
+        if (dev != cur && (e = hipSetDevice(dev)) != hipSuccess) {
+            nnk_set_error((int)e, "%s: hipSetDevice(%d): %s", what, dev, hipGetErrorString(e));
+            return nullptr;
+        }
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (dev != cur) (void)hipSetDevice(cur);
+        if (e != hipSuccess || !p) {
+            nnk_set_error(e != hipSuccess ? (int)e : (int)hipErrorInvalidSymbol, "%s: scratch address: %s", what,
+                hipGetErrorString(e));
+            return nullptr;
+        }
+        g_noalloc_ptr[dev] = static_cast<float*>(p);
+    }
+    return g_noalloc_ptr[dev];
+}
 }  // namespace
 
 extern "C" {
@@ -435,6 +488,23 @@ void launch_groupnorm_act_backward_ws(float* dx, float* ggamma, float* gbeta, co
     }
     gn_backward_impl("launch_groupnorm_act_backward_ws", dx, ggamma, gbeta, dy, x, gamma, beta,
         mu, rstd, batch, HW, C, G, (int)act, workspace, s);
+}
+
+void launch_groupnorm_act_backward_noalloc(float* dx, float* ggamma, float* gbeta, const float* dy,
+    const float* x, const float* gamma, const float* beta, const float* mu, const float* rstd,
+    int batch, int HW, int C, int G, Activation act, hipStream_t s) {
+    const char* what = "launch_groupnorm_act_backward_noalloc";
+    if (!shape_ok(what, batch, HW, C, G)) return;
+    const size_t stream_bytes = reg_partials_offset(batch, HW, C, G) * sizeof(float);
+    const size_t partial_bytes = (size_t)2 * batch * C * sizeof(float);
+    NNK_REQUIRE(stream_bytes <= kNoAllocStreamBytes && partial_bytes <= kNoAllocPartialBytes, what,
+        "%s: [%d, %d, %d] G=%d needs %zu + %zu bytes of scratch, more than its %zu + %zu (use "
+        "launch_groupnorm_act_backward_ws with a workspace of nnhip_groupnorm_backward_workspace floats)",
+        what, batch, HW, C, G, stream_bytes, partial_bytes, kNoAllocStreamBytes, kNoAllocPartialBytes);
+    float* ws = noalloc_scratch(s, what);
+    if (!ws) return;
+    gn_backward_impl(what, dx, ggamma, gbeta, dy, x, gamma, beta, mu, rstd, batch, HW, C, G, (int)act, ws, s,
+        ws + kNoAllocStreamBytes / sizeof(float));
 }
 
 size_t nnhip_groupnorm_backward_workspace(int batch, int HW, int C, int G) {

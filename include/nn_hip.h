@@ -323,6 +323,23 @@ void launch_layernorm_backward_ws(float* grad_in, float* ggamma, float* gbeta,
    one word of device memory). */
 int nnhip_groupnorm_workspace_status(const float* workspace);
 
+/* launch_groupnorm_act_backward without any allocation (no counterpart in the
+   reference).  For callers that cannot allocate device memory: code under
+   HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.
+   Same kernels and results as launch_groupnorm_act_backward; instead of a
+   pool block its partial sums live in a fixed scratch array of the library
+   (16 MiB per device, held until the process ends): up to 12 MiB for the
+   streaming kernels' workspace and 4 MiB for the 2*batch*C channel partials
+   of the smaller-tensor paths.  The north-star shape [256, 64*64, 256], G=32,
+   needs 10.5 MiB.  A larger shape is refused with an error naming the sizes
+   (nnhip_get_last_error); nothing is launched then.  Every call on one device
+   shares that scratch: calls that may overlap on one device (several streams
+   or host threads) race and must be serialised by the caller. */
+void launch_groupnorm_act_backward_noalloc(float* dx, float* ggamma, float* gbeta,
+    const float* dy, const float* x, const float* gamma, const float* beta,
+    const float* mu, const float* rstd,
+    int batch, int HW, int C, int G, Activation act, hipStream_t s);
+
 /* grad_im = col2im(grad_col) written, not accumulated: the same fixed order as
    launch_col2im starting from +0.0f.  Replaces the caller's memset + col2im pair
    (src/conv2d.c:61-65). */
