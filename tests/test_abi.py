@@ -36,6 +36,8 @@ def test_reference_launcher_set_is_declared(nn):
         "launch_mp_cat", "launch_mp_channel_cat", "launch_mp_channel_split", "launch_mp_fourier",
         "launch_sinusoidal", "launch_layernorm_forward", "launch_layernorm_backward",
         "launch_groupnorm_forward", "launch_groupnorm_backward", "launch_im2col", "launch_col2im",
+        "launch_spatial_add", "launch_spatial_reduce_sum", "launch_spatial_modulate",
+        "launch_spatial_modulate_backward",
     }
     assert ref_names <= set(nn.header_functions())
 
@@ -67,6 +69,14 @@ def test_launchers_keep_reference_argument_order(nn):
         "launch_sinusoidal": "ppiifs",
         "launch_im2col": "ppiiiiiiiiis",
         "launch_col2im": "ppiiiiiiiiis",
+        "launch_add_bias": "ppiis",
+        "launch_bias_grad": "ppiis",
+        "launch_sgd_step": "ppfis",
+        "launch_scale_by_scalar": "ppis",
+        "launch_spatial_add": "ppiiiis",
+        "launch_spatial_reduce_sum": "ppiiis",
+        "launch_spatial_modulate": "pppiiiis",
+        "launch_spatial_modulate_backward": "pppppiiiis",
     }
 
     def kind(a: str) -> str:
@@ -81,6 +91,20 @@ def test_launchers_keep_reference_argument_order(nn):
     for name, k in expect.items():
         got = "".join(kind(a) for a in sig[name])
         assert got == k, (name, got, k)
+
+
+def test_reference_call_sites_compile_against_the_header():
+    """tests/refcalls.c: the reference's launcher prototypes (src/nn.h:354-456)
+    with the stream re-typed to hipStream_t, each launcher of include/nn_hip.h
+    assigned to a pointer of that exact type, and call sites written as the
+    reference's host modules write them (src/groupnorm.c:16, 27,
+    src/layernorm.c:16, 26, src/activation.c:12, 21, src/mp_linear.c:16-38,
+    src/conv2d.c:24-64, src/optimizer.c:58, 66, src/ema.c:32, ...), compiled
+    with -Werror: no compatibility header, no cast."""
+    cmd = ["gcc", "-std=c11", "-Wall", "-Wextra", "-Werror", "-fsyntax-only", "-D__HIP_PLATFORM_AMD__",
+           f"-I{ROOT / 'include'}", "-I/opt/rocm/include", str(ROOT / "tests" / "refcalls.c")]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    assert res.returncode == 0, res.stderr[-3000:]
 
 
 def test_host_refusals_record_an_error(nn):

@@ -145,6 +145,50 @@ def test_groupnorm_forward_backward_vs_torch(orc, rng, shape):
     assert rel_err(gb, bt.grad.numpy(), floor=1.0) <= TOL
 
 
+@pytest.mark.parametrize("act", [0, 3], ids=["identity", "silu"])
+def test_groupnorm_f32_baseline_within_summation_bounds(orc, rng, act):
+    """The CPU baseline's fp32 transcription (serial fp32 sums, E[x^2]-mu^2,
+    one serial loop per channel for dgamma/dbeta, as src/kernels.cu:622-717)
+    computes what the double oracle computes, within the worst-case error of
+    recursive fp32 summation (u = 2^-24): the bench times correct code.  A
+    wrong sign, index or a dropped row is off by O(1); for the channel sums
+    the bound is tight enough that one dropped term of typical size fails."""
+    B, H, W, C, G = 8, 32, 32, 128, 32  # BASELINE cfg1
+    HW, cpg = H * W, C // G
+    x = rng.standard_normal((B, HW, C), dtype=np.float32)
+    dy = rng.standard_normal((B, HW, C), dtype=np.float32)
+    gamma = (1 + 0.1 * rng.standard_normal(C)).astype(np.float32)
+    beta = (0.1 * rng.standard_normal(C)).astype(np.float32)
+    u = 2.0 ** -24
+    n = HW * cpg  # terms per group sum
+    N = B * HW    # terms per channel sum
+    y, mu, rs = orc.groupnorm_forward(x, gamma, beta, G, 1e-5, act)
+    y32, mu32, rs32 = orc.groupnorm_forward_f32(x, gamma, beta, G, 1e-5, act)
+    xg = x.reshape(B, HW, G, cpg).astype(np.float64)
+    abs_mean = np.mean(np.abs(xg), axis=(1, 3)).ravel()  # sum|x| / n per (b, g)
+    assert np.all(np.abs(mu32.astype(np.float64) - mu) <= (n + 2) * u * abs_mean)
+    assert rel_err(rs32, rs) <= n * u
+    assert rel_err(y32, y) <= n * u
+    dx, gg, gb = orc.groupnorm_backward(dy, x, gamma, beta, mu, rs, G, act)
+    dx32, gg32, gb32 = orc.groupnorm_backward_f32(dy, x, gamma, beta, mu, rs, G, act)
+    assert rel_err(dx32, dx) <= n * u
+    m = np.repeat(mu.reshape(B, G), cpg, axis=1)[:, None, :].astype(np.float64)
+    r = np.repeat(rs.reshape(B, G), cpg, axis=1)[:, None, :].astype(np.float64)
+    xh = (x - m) * r
+    d = dy if act == 0 else orc.act_backward(dy, (gamma * xh + beta).astype(np.float32), act).reshape(x.shape)
+    d = d.astype(np.float64)
+    # first-order bound of recursive summation in the port's order (b, then
+    # hw, per channel): u * (sum_k |partial sum k| + sum |terms|) (Higham,
+    # Accuracy and Stability of Numerical Algorithms, 4.2), plus the rounding
+    # of each term; tight enough that one dropped term of typical size fails
+    for terms, got, ref in ((d * xh, gg32, gg), (d, gb32, gb)):
+        t = terms.reshape(N, C)
+        bound = u * (np.sum(np.abs(np.cumsum(t, axis=0)), axis=0) + 3 * np.sum(np.abs(t), axis=0))
+        assert np.all(np.abs(got.astype(np.float64) - ref) <= bound), float(np.max(np.abs(got - ref) / bound))
+        dropped = np.abs(t).mean(axis=0)
+        assert np.all(bound < dropped), "bound too loose to see one dropped term"
+
+
 def test_groupnorm_closed_forms(orc, rng):
     B, HW, C, G = 2, 64, 32, 4
     x = (3.0 + 2.0 * rng.standard_normal((B, HW, C))).astype(np.float32)
