@@ -1,0 +1,76 @@
+/* layer.h -- the record behind every host module of this library.
+ *
+ * A Layer is what a Module* points at: the Module vtable the callers use is its
+ * first member, and the four vtable entries are the same for every kind (they
+ * dispatch through the kind's table entry).  All device memory a layer owns
+ * (parameters, their gradients, cached statistics, lent workspaces, scratch)
+ * is carved out of ONE device allocation, the arena, described by a list of
+ * buffer requests made at construction time; the ParamList entries are
+ * (value buffer, gradient buffer, size) triples in the order the module
+ * exports them, and composite layers own child modules whose parameters
+ * follow the layer's own.
+ *
+ * Construction: layer_begin -> layer_buf / layer_param / layer_sub ->
+ * layer_end, which makes the single allocation, zero-fills the buffers asked
+ * for zeroed and wires the vtable.  Only after layer_end are the buffers
+ * addressable (L->buf[i]).
+ */
+#ifndef NN_LAYER_H
+#define NN_LAYER_H
+
+#include "nn_modules.h"
+
+#define LAYER_MAX_BUFS 16
+#define LAYER_MAX_PARAMS 3
+#define LAYER_MAX_SUBS 6
+#define LAYER_MAX_DIMS 12
+
+typedef struct Layer Layer;
+
+typedef struct {
+    const char* name;
+    void (*fwd)(Layer* L, const float* in, float* out, int batch, Context* ctx);
+    void (*bwd)(Layer* L, const float* in, const float* out, const float* grad_out, float* grad_in,
+        int batch, Context* ctx);
+} LayerKind;
+
+struct Layer {
+    Module mod; /* must stay first: a Module* of this library is a Layer* */
+    const LayerKind* kind;
+    int max_batch;
+    int dim[LAYER_MAX_DIMS]; /* the kind's geometry, indexed by the kind's own enum */
+    float k[4];              /* the kind's constants (eps, blend weights, ...) */
+    Activation act;
+    /* device buffers: requests, then the carved views */
+    int nbuf;
+    size_t want[LAYER_MAX_BUFS];
+    unsigned char zero[LAYER_MAX_BUFS];
+    float* buf[LAYER_MAX_BUFS];
+    float* arena;
+    /* ParamList export */
+    int nparam;
+    int pval[LAYER_MAX_PARAMS], pgrad[LAYER_MAX_PARAMS], pn[LAYER_MAX_PARAMS];
+    /* owned child modules, exported after this layer's own parameters */
+    int nsub;
+    Module* sub[LAYER_MAX_SUBS];
+};
+
+/* Start a layer of `kind` with the Module's in/out dimensions. */
+Layer* layer_begin(const LayerKind* kind, int in_dim, int out_dim, int max_batch);
+/* Request a device buffer of `floats` floats (0: none, its view stays NULL);
+   zero != 0 zero-fills it at layer_end.  Returns its index. */
+int layer_buf(Layer* L, size_t floats, int zero);
+/* Export (value, gradient) buffers of n floats as the next ParamList entry. */
+void layer_param(Layer* L, int value_buf, int grad_buf, int n);
+/* Take ownership of a child module (freed with the layer). */
+void layer_sub(Layer* L, Module* child);
+/* Allocate and carve the arena, zero-fill the buffers asked for, wire the
+   vtable; returns the Module callers hold. */
+Module* layer_end(Layer* L);
+
+static inline Layer* as_layer(Module* m) { return (Layer*)m; }
+
+/* Host-to-device fill of a buffer with one value (construction time). */
+void layer_fill_value(Layer* L, int b, size_t n, float value);
+
+#endif /* NN_LAYER_H */

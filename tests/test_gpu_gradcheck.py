@@ -19,3 +19,12 @@ def test_module_gradcheck(L):
     gc.nn_gradcheck_run.argtypes = [ctypes.c_int]
     fails = gc.nn_gradcheck_run(1)
     assert fails == 0, f"{fails} module(s) failed the gradcheck"
+
+
+def test_sequential_chain_matches_modules_called_by_hand(L):
+    """The Sequential container (src/sequential.c:31-118 semantics) against
+    the same modules called one by one: bit-identical output, input gradient
+    and parameter gradients, ParamList in module order, input copied."""
+    gc = ctypes.CDLL(str(LIB))
+    gc.nn_chaincheck_run.restype = ctypes.c_int
+    assert gc.nn_chaincheck_run() == 0
