@@ -12,6 +12,9 @@
  * 1, EMA geometric decay); im2col/col2im against brute force and F.unfold /
  * F.fold; finite-difference gradchecks of every backward with the reference's
  * gradcheck tolerances (tests/gradcheck.c:15-21, 51-56).
+ *
+ * The maths restated here is vyeoms/cuda-c-diffusion's (MIT License; the
+ * notice is in THIRD_PARTY_NOTICES.md at the repository root).
  */
 #include "oracle.h"
 
