@@ -121,6 +121,9 @@ _SIGS = {
     "nnhip_layernorm_backward_workspace": (SZ, [I, I], False),
     "launch_groupnorm_act_backward_ws": (None, [P, P, P, P, P, P, P, P, P, I, I, I, I, I, P, P], True),
     "launch_groupnorm_act_backward_noalloc": (None, [P, P, P, P, P, P, P, P, P, I, I, I, I, I, P], True),
+    "launch_groupnorm_act_shift_forward_ws": (None, [P, P, P, P, P, P, P, I, I, I, I, F, I, P, P], True),
+    "launch_groupnorm_act_shift_backward_ws": (None, [P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, P, P], True),
+    "nnhip_groupnorm_shift_backward_workspace": (SZ, [I, I, I, I], False),
     "launch_layernorm_backward_ws": (None, [P, P, P, P, P, P, P, P, I, I, P, P], True),
     "launch_col2im_set": (None, [P, P, I, I, I, I, I, I, I, I, I, P], True),
     "nnhip_multi_tensor_plan_create": (P, [P, I], True),

@@ -142,6 +142,34 @@ __device__ __forceinline__ void lds_take4(float4 (&v)[4], uint32_t addr) {
     v[3] = make_float4(d.x, d.y, d.z, d.w);
 }
 
+// lds_take4 plus the 16-byte shift slot at zaddr, added to v[0..NX) (the x
+// part of the tile) once all five reads have landed.
+template <int NX>
+__device__ __forceinline__ void lds_take4_shift(float4 (&v)[4], uint32_t addr, uint32_t zaddr) {
+    f32x4 a, b, c, d, z;
+    asm volatile(
+        "ds_read_b128 %0, %5\n\t"
+        "ds_read_b128 %1, %5 offset:16384\n\t"
+        "ds_read_b128 %2, %5 offset:32768\n\t"
+        "ds_read_b128 %3, %5 offset:49152\n\t"
+        "ds_read_b128 %4, %6\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(a), "=&v"(b), "=&v"(c), "=&v"(d), "=&v"(z)
+        : "v"(addr), "v"(zaddr)
+        : "memory");
+    v[0] = make_float4(a.x, a.y, a.z, a.w);
+    v[1] = make_float4(b.x, b.y, b.z, b.w);
+    v[2] = make_float4(c.x, c.y, c.z, c.w);
+    v[3] = make_float4(d.x, d.y, d.z, d.w);
+#pragma unroll
+    for (int k = 0; k < NX; ++k) {
+        v[k].x += z.x;
+        v[k].y += z.y;
+        v[k].z += z.z;
+        v[k].w += z.w;
+    }
+}
+
 // Make v's loads complete here.  Values loaded before the tile pipeline and
 // used inside it would otherwise make the compiler's wait at their first use
 // inside the loop a full vector-memory wait, i.e. a wait for the staged tile.
@@ -264,10 +292,13 @@ __device__ __forceinline__ int wave_slot(int g, int w) {
 // ---------------------------------------------------------------------------
 // Forward.
 // ---------------------------------------------------------------------------
-template <class Gm, int ACT, int RPL, bool NT>
+// SHIFT: normalise x + shift[b, c] (a per-sample, per-channel term broadcast
+// over the pixels, added to each tile as it is taken; x is not modified).
+template <class Gm, int ACT, int RPL, bool NT, bool SHIFT>
 __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float* __restrict__ mu_out,
     float* __restrict__ rstd_out, const float* __restrict__ x, const float* __restrict__ gamma,
-    const float* __restrict__ beta, Shape sh, Work wk, float eps, unsigned spin_limit) {
+    const float* __restrict__ beta, const float* __restrict__ shift, Shape sh, Work wk, float eps,
+    unsigned spin_limit) {
 #pragma clang fp contract(fast)
     constexpr int NW = Gm::NW, NV = Gm::NV, GT = Gm::GT, TPB = Gm::TPB, CW4 = Gm::CW4;
     static_assert(NV == 4 && TPB * 16 == 16384, "stage slots as lds_take4 reads them");
@@ -275,6 +306,8 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
     // direct-to-LDS loads (round j takes buffer j % 2).  The tiles awaiting
     // phase B stay in registers.
     __shared__ float4 stage[2][NV * TPB];
+    static_assert(2 * CW4 == kWave, "a wave's shift load covers the column block twice");
+    __shared__ float4 shs[SHIFT ? 4 : 1][SHIFT ? kWave : 1];  // with SHIFT: the shift ring
     // Double-buffered by loop parity pb: consecutive phase A's (and phase B's)
     // may run with no barrier between them (first and last rounds), so a
     // buffer is rewritten only two phases later, past the other phase's barrier.
@@ -317,6 +350,22 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
     // Record layout [unit][group][value][pixel tile]: the mergers of a group
     // read consecutive tiles, i.e. contiguous records.
     auto rec_slot = [&](int j, int g, int tt) { return wk.rec + ((size_t)((u0 + j * upr) * GT + g) * 2) * T + tt; };
+    // With SHIFT the input is x + shift[b, c]: the 128 shift values of a
+    // tile's sample and column block go into slot j % 4 of a small LDS ring
+    // with one direct-to-LDS load per wave, issued just before the tile's own
+    // loads (so the stage wait covers it), and are added to the tile as it is
+    // taken.  Every wave writes the same values to the same slot: a wave reads
+    // the slot only after its own load has landed, and a slot is rewritten
+    // (tile j + 4) only after every wave has passed the barriers of the
+    // rounds that read it (tile j).  A tile past the end reloads the last sample's shift.
+    // One resource over the whole [B, C] shift for the kernel; the sample
+    // moves the scalar offset (a tile past the end reads the last sample's).
+    const __amdgpu_buffer_rsrc_t shr = sample_rsrc(shift, SHIFT ? (uint32_t)(sh.B * sh.C * 4) : 0u);
+    const uint32_t shv = (uint32_t)(cb * CW4 * 4 + col * 4) * 4u;
+    auto issue_shift = [&](int j) {
+        if constexpr (SHIFT)
+            dma16<false>(shr, &shs[j & 3][0], shv, (uint32_t)(real_of(j) ? b0 + j * spr : sh.B - 1) * row_bytes);
+    };
     // The NV loads of round j's tile into stage buffer sb.  A tile past the
     // end is issued against an empty buffer range: the loads read nothing and
     // only keep the operation count of every round the same.
@@ -325,12 +374,18 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
         const __amdgpu_buffer_rsrc_t r =
             sample_rsrc(x + (size_t)(real ? b0 + j * spr : 0) * sh.HW * sh.C, real ? sh.sample_bytes : 0u);
         const uint32_t base = (uint32_t)(t * Gm::TP) * row_bytes;
+        issue_shift(j);
 #pragma unroll
         for (int k = 0; k < NV; ++k)
             dma16<NT>(r, &stage[sb][k * TPB + wid * kWave], voff, base + (uint32_t)(k * Gm::RSTEP) * row_bytes);
     };
-    auto take = [&](float4 (&v)[NV], int sb) { lds_take4(v, lds_addr(&stage[sb][tid])); };
-    auto phase_a = [&](const float4 (&v)[NV], int j, int pb) {
+    auto take = [&](float4 (&v)[NV], int j) {
+        if constexpr (SHIFT)
+            lds_take4_shift<NV>(v, lds_addr(&stage[j & 1][tid]), lds_addr(&shs[j & 3][col]));
+        else
+            lds_take4(v, lds_addr(&stage[j & 1][tid]));
+    };
+    auto phase_a = [&](float4 (&v)[NV], int j, int pb) {
         float s = 0.0f;
 #pragma unroll
         for (int k = 0; k < NV; ++k) s += (v[k].x + v[k].y) + (v[k].z + v[k].w);
@@ -452,14 +507,16 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
     //   round 0: tile 1's NV loads were issued after tile 0's;
     //   round 1: round 0 issued NV loads;
     //   round 2: round 1 issued NV loads and 2 RPL record loads;
-    //   round j >= 3: round j - 1 issued NV loads, NV stores, 2 RPL record loads.
+    //   round j >= 3: round j - 1 issued NV loads, NV stores, 2 RPL record loads;
+    // plus, with SHIFT, the shift load issued before each tile's loads.
     if (w >= nt) return;
     const int K = (nt - w + P - 1) / P;
     float4 S0[NV], S1[NV], S2[NV];
+    constexpr int SH = SHIFT ? 1 : 0;
     int pb = 0;
-    auto steady_round = [&](int j, float4 (&cur)[NV], const float4 (&old)[NV]) {  // j >= 3
-        vm_wait<2 * NV + 2 * RPL>();
-        take(cur, j & 1);
+    auto steady_round = [&](int j, float4 (&cur)[NV], const float4 (&old)[NV]) {
+        vm_wait<2 * NV + 2 * RPL + SH>();  // j >= 3
+        take(cur, j);
         issue(j + 2, j & 1);
         phase_a(cur, j, pb);
         phase_b(old, j - 2, pb);
@@ -468,21 +525,21 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
     };
     issue(0, 0);
     issue(1, 1);
-    vm_wait<NV>();
+    vm_wait<NV + SH>();
     take(S0, 0);
     issue(2, 0);
     phase_a(S0, 0, pb);
     pb ^= 1;
     if (K > 1) {
-        vm_wait<NV>();
+        vm_wait<NV + SH>();
         take(S1, 1);
         issue(3, 1);
         phase_a(S1, 1, pb);
         records_prefetch(0);
         pb ^= 1;
         if (K > 2) {
-            vm_wait<NV + 2 * RPL>();
-            take(S2, 0);
+            vm_wait<NV + 2 * RPL + SH>();
+            take(S2, 2);
             issue(4, 0);
             phase_a(S2, 2, pb);
             phase_b(S0, 0, pb);
@@ -529,12 +586,16 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
 // Backward.  dy is the gradient of act(GN(x)); the pre-activation is
 // recomputed from x, mu, rstd, gamma, beta.  Parks xhat and g = d*gamma.
 // ---------------------------------------------------------------------------
-template <class Gm, int ACT, int RPL, bool NT>
+// SHIFT: the input of the forward was x + shift[b, c]; besides dx the kernel
+// writes, per tile, the column sums of dx over its pixel rows to colpart
+// [tile][column block channel] (gns_colsum adds them per sample into the
+// gradient of the shift).
+template <class Gm, int ACT, int RPL, bool NT, bool SHIFT>
 __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float* __restrict__ ggamma,
     float* __restrict__ gbeta, const float* __restrict__ dy,
     const float* __restrict__ x, const float* __restrict__ gamma, const float* __restrict__ beta,
-    const float* __restrict__ mu, const float* __restrict__ rstd, Shape sh, Work wk,
-    unsigned spin_limit) {
+    const float* __restrict__ mu, const float* __restrict__ rstd, const float* __restrict__ shift,
+    float* __restrict__ colpart, Shape sh, Work wk, unsigned spin_limit) {
 #pragma clang fp contract(fast)
     constexpr int NW = Gm::NW, NV = Gm::NV, GT = Gm::GT, TPB = Gm::TPB, CW4 = Gm::CW4;
     static_assert(NV == 2 && TPB * 16 == 16384, "stage slots (x then dy) as lds_take4 reads them");
@@ -542,9 +603,15 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
     // direct-to-LDS loads); the tiles awaiting phase B (xhat, g) stay in
     // registers.
     __shared__ float4 stage[2][2 * NV * TPB];
+    static_assert(2 * CW4 == kWave, "a wave's shift load covers the column block twice");
+    __shared__ float4 shs[SHIFT ? 4 : 1][SHIFT ? kWave : 1];  // with SHIFT: the shift ring
     __shared__ float2 wred[2][GT][NW];          // (S1, S2) partials, laid out as in the forward
     __shared__ float2 stat[2][GT];              // group means of g and g * xhat
     __shared__ float cred[NW][CW4][8];          // per-wave dgamma/dbeta sums at the end (then the reducer's)
+    // with SHIFT, during the tile loop: the per-wave column sums of a tile's
+    // dx, double-buffered by the parity of the phase B that wrote them
+    float4 (*csum)[NW][CW4] = reinterpret_cast<float4 (*)[NW][CW4]>(&cred[0][0][0]);
+    static_assert(sizeof(float4) * 2 * NW * CW4 <= sizeof(cred), "column sums fit the reduction buffer");
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
     const int col = lane % CW4, row0 = wid * Gm::RW + lane / CW4;
     const int gl = col / Gm::CPG4;
@@ -556,11 +623,24 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
     const int gglob = cb * GT + gl;             // global group index of this lane
     const uint32_t voff = (uint32_t)(row0 * sh.C + c0) * 4u;
     const uint32_t row_bytes = (uint32_t)sh.C * 4u;
-    const float4 gm = ld4(gamma + c0);
-    float4 bt = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if constexpr (ACT != ACT_IDENTITY) bt = ld4(beta + c0);
-    settle(gm);
-    settle(bt);
+    // gamma and beta of this lane's channels: held in registers, or, where
+    // the tile loop needs those registers (the shift's column sums), read
+    // from LDS in each phase A
+    constexpr bool kAffineLds = SHIFT;
+    __shared__ float4 affine[kAffineLds ? 2 : 1][kAffineLds ? CW4 : 1];
+    float4 gm_r = make_float4(0.0f, 0.0f, 0.0f, 0.0f), bt_r = gm_r;
+    if constexpr (kAffineLds) {
+        if (tid < CW4) {
+            affine[0][tid] = ld4(gamma + cb * CW4 * 4 + tid * 4);
+            affine[1][tid] = ACT != ACT_IDENTITY ? ld4(beta + cb * CW4 * 4 + tid * 4) : gm_r;
+        }
+        __syncthreads();
+    } else {
+        gm_r = ld4(gamma + c0);
+        if constexpr (ACT != ACT_IDENTITY) bt_r = ld4(beta + c0);
+        settle(gm_r);
+        settle(bt_r);
+    }
     const unsigned epoch = launch_epoch(wk);
     const unsigned long long tag = (unsigned long long)epoch << 32;
     const WaitFail wf{wk.err, wk.hflag};
@@ -583,6 +663,16 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
     // The x and dy loads of round j's tile into stage buffer sb (2 NV).  A
     // tile past the end is issued against an empty buffer range: the loads
     // read nothing and only keep the operation count of every round the same.
+    // With SHIFT the forward's input was x + shift[b, c]: the shift ring as in
+    // the forward, filled before each tile's x and dy loads.
+    // One resource over the whole [B, C] shift for the kernel; the sample
+    // moves the scalar offset (a tile past the end reads the last sample's).
+    const __amdgpu_buffer_rsrc_t shr = sample_rsrc(shift, SHIFT ? (uint32_t)(sh.B * sh.C * 4) : 0u);
+    const uint32_t shv = (uint32_t)(cb * CW4 * 4 + col * 4) * 4u;
+    auto issue_shift = [&](int j) {
+        if constexpr (SHIFT)
+            dma16<false>(shr, &shs[j & 3][0], shv, (uint32_t)(real_of(j) ? b0 + j * spr : sh.B - 1) * row_bytes);
+    };
     auto issue = [&](int j, int sb) {
         const bool real = real_of(j);
         const size_t so = (size_t)(real ? b0 + j * spr : 0) * sh.HW * sh.C;
@@ -590,6 +680,7 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
         const __amdgpu_buffer_rsrc_t rx = sample_rsrc(x + so, bytes);
         const __amdgpu_buffer_rsrc_t rd = sample_rsrc(dy + so, bytes);
         const uint32_t base = (uint32_t)(t * Gm::TP) * row_bytes;
+        issue_shift(j);
 #pragma unroll
         for (int k = 0; k < NV; ++k)
             dma16<NT>(rx, &stage[sb][k * TPB + wid * kWave], voff, base + (uint32_t)(k * Gm::RSTEP) * row_bytes);
@@ -598,7 +689,12 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
             dma16<NT>(rd, &stage[sb][(NV + k) * TPB + wid * kWave], voff,
                 base + (uint32_t)(k * Gm::RSTEP) * row_bytes);
     };
-    auto take = [&](float4 (&v)[2 * NV], int sb) { lds_take4(v, lds_addr(&stage[sb][tid])); };
+    auto take = [&](float4 (&v)[2 * NV], int j) {
+        if constexpr (SHIFT)
+            lds_take4_shift<NV>(v, lds_addr(&stage[j & 1][tid]), lds_addr(&shs[j & 3][col]));
+        else
+            lds_take4(v, lds_addr(&stage[j & 1][tid]));
+    };
     // Mean and rstd of this lane's group in round j's sample (two loads; a
     // tile past the end reads the last sample's and never uses them).
     float mean, rs;
@@ -607,10 +703,32 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
         mean = mu[b * sh.G + gglob];
         rs = rstd[b * sh.G + gglob];
     };
+    // With SHIFT: the column sums of round j's tile (written by its phase B
+    // into csum[par] after that phase's barrier) added over the waves in
+    // order, one channel per lane, and stored to its row of colpart.  Called
+    // past a later barrier and before the next phase B of the same parity
+    // passes its own barrier, after which csum[par] is rewritten; the tile
+    // loop calls it at the end of a round, where few registers are live.
+    auto flush_colsum = [&](int j, int par) {
+        if constexpr (SHIFT) {
+            if (tid < CW4 * 4) {
+                const float* cf = reinterpret_cast<const float*>(&csum[par][0][0]) + tid;
+                float a = cf[0];
+#pragma unroll 3
+                for (int ww = 1; ww < NW; ++ww) a += cf[ww * CW4 * 4];
+                colpart[(size_t)(w + j * P) * (CW4 * 4) + tid] = a;
+            }
+        } else {
+            (void)j;
+            (void)par;
+        }
+    };
     // phase A: v[0..NV) = x -> xhat, v[NV..2NV) = dy -> g in place; per-group
     // S1 = sum g, S2 = sum g*xhat -> records
     auto phase_a = [&](float4 (&v)[2 * NV], int j, int pb) {
         float4 s1v = make_float4(0.0f, 0.0f, 0.0f, 0.0f), s2v = s1v;
+        const float4 gm = kAffineLds ? affine[0][col] : gm_r;
+        const float4 bt = kAffineLds ? affine[1][col] : bt_r;
         const float nms = -mean * rs;
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
@@ -714,6 +832,7 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
         const float2 st = stat[pb][gl];
         const float a1 = -rsv * st.x, a2 = -rsv * st.y;
         float* dxs = dx + (size_t)b * sh.HW * sh.C + (size_t)(t * Gm::TP + row0) * sh.C + c0;
+        float4 cs = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
             const float4 xh = v[k];
@@ -724,6 +843,23 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
             o.z = fmaf(g.z, rsv, fmaf(xh.z, a2, a1));
             o.w = fmaf(g.w, rsv, fmaf(xh.w, a2, a1));
             stS<NT>(dxs + (size_t)(k * Gm::RSTEP) * sh.C, o);
+            if constexpr (SHIFT) {
+                cs.x += o.x;
+                cs.y += o.y;
+                cs.z += o.z;
+                cs.w += o.w;
+            }
+        }
+        if constexpr (SHIFT) {
+            // this wave's rows of the tile, in a fixed xor tree over the row lanes
+#pragma unroll
+            for (int o = CW4; o < kWave; o <<= 1) {
+                cs.x += __shfl_xor(cs.x, o, kWave);
+                cs.y += __shfl_xor(cs.y, o, kWave);
+                cs.z += __shfl_xor(cs.z, o, kWave);
+                cs.w += __shfl_xor(cs.w, o, kWave);
+            }
+            if (lane < CW4) csum[pb][wid][lane] = cs;
         }
     };
 
@@ -739,11 +875,13 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
     //   round 0: tile 1's 2 NV loads;
     //   round 1: round 0's 2 NV tile loads and 2 statistics loads;
     //   round 2: round 1's 2 NV + 2 loads and 2 RPL record loads;
-    //   round j >= 3: round j - 1's 2 NV + 2 loads, NV stores, 2 RPL record loads.
+    //   round j >= 3: round j - 1's 2 NV + 2 loads, NV stores, 2 RPL record loads;
+    // plus, with SHIFT, the shift load issued before each tile's loads.
     if (w < nt) {
         const int K = (nt - w + P - 1) / P;
         float4 v[2 * NV], pk1[2 * NV], pk2[2 * NV];
         float rs1 = 0.0f, rs2 = 0.0f;  // rstd of tiles j - 1 and j - 2
+        constexpr int SH = SHIFT ? 1 : 0;  // the shift load issued before each tile's loads
         auto rotate = [&](float rs_j) {
 #pragma unroll
             for (int k = 0; k < 2 * NV; ++k) {
@@ -757,7 +895,7 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
         load_stats(0);
         issue(0, 0);
         issue(1, 1);
-        vm_wait<2 * NV>();
+        vm_wait<2 * NV + SH>();
         take(v, 0);
         issue(2, 0);
         phase_a(v, 0, pb);
@@ -768,7 +906,7 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
         }
         pb ^= 1;
         if (K > 1) {
-            vm_wait<2 * NV + 2>();
+            vm_wait<2 * NV + 2 + SH>();
             take(v, 1);
             issue(3, 1);
             phase_a(v, 1, pb);
@@ -780,8 +918,8 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
             }
             pb ^= 1;
             if (K > 2) {
-                vm_wait<2 * NV + 2 + 2 * RPL>();
-                take(v, 0);
+                vm_wait<2 * NV + 2 + 2 * RPL + SH>();
+                take(v, 2);
                 issue(4, 0);
                 phase_a(v, 2, pb);
                 {
@@ -793,8 +931,8 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
                 }
                 pb ^= 1;
                 for (int j = 3; j < K; ++j) {
-                    vm_wait<3 * NV + 2 + 2 * RPL>();
-                    take(v, j & 1);
+                    vm_wait<3 * NV + 2 + 2 * RPL + SH>();
+                    take(v, j);
                     issue(j + 2, j & 1);
                     phase_a(v, j, pb);
                     const float rs_j = rs;
@@ -803,15 +941,23 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
                     records_prefetch(j - 1);
                     rotate(rs_j);
                     pb ^= 1;
+                    flush_colsum(j - 3, pb);  // round j - 1's phase B, the other parity
                 }
             }
             // tiles K - 2 and K - 1 (now pk2 and pk1)
             phase_b(pk2, rs2, K - 2, pb);
+            if (K > 2) flush_colsum(K - 3, pb ^ 1);
             pb ^= 1;
         }
         records_prefetch(K - 1);
         phase_b(pk1, rs1, K - 1, pb);
         vm_wait<0>();  // the loads past the last tile write the stage: let them land before it is reused
+        if constexpr (SHIFT) {  // the last two tiles, before the buffer serves the dgamma/dbeta sums
+            __syncthreads();
+            flush_colsum(K - 1, pb);
+            if (K > 1) flush_colsum(K - 2, pb ^ 1);
+            __syncthreads();
+        }
     }
 
     // dgamma/dbeta partials of this workgroup: lanes with equal column own the
@@ -913,14 +1059,20 @@ constexpr int kMaxGrid = 1024;        // persistent workgroups at most
 // run time of the grid itself.
 constexpr unsigned kSpinLimit = 1u << 20;
 
+// Kernel keys of the persistent-grid cache (nnk_gns_grid): forwards below
+// kGnsBwdKeys, backwards from it.
+constexpr int kGnsBwdKeys = 256;
+
 struct Plan {
     bool ok;
     int cpg4, rpl;
     Shape sh;
-    size_t ws_floats;   // workspace needed (header + records [+ partials])
-    size_t rec_offset;  // in bytes from the workspace start
+    size_t ws_floats;        // workspace needed (header + records [+ partials])
+    size_t rec_offset;       // in bytes from the workspace start
     size_t part_offset;
     size_t tpart_offset;
+    size_t colpart_offset;   // backward with a shift: per-tile column sums of dx (plain floats)
+    size_t ws_shift_floats;  // workspace needed by the backward with a shift
 };
 
 // Applicability and sizes; `bwd` selects the backward geometry.
@@ -933,8 +1085,11 @@ Plan make_plan(bool bwd, int B, int HW, int C, int G);
 // device workspace of at least plan.ws_floats floats whose records region
 // never holds this launch's epoch and whose counters are zero (a zero-filled
 // workspace, only ever used by these launchers, is both).
+// With `shift` non-null the input is x + shift[b, c] (formed in registers;
+// x is not modified), and the backward also writes gshift[b, c] = the sum over
+// the pixels of dx (its workspace then needs plan.ws_shift_floats floats).
 bool nnk_gns_forward(int act, float* y, float* mu, float* rstd, const float* x, const float* gamma,
-    const float* beta, int B, int HW, int C, int G, float eps, float* ws, hipStream_t s);
+    const float* beta, const float* shift, int B, int HW, int C, int G, float eps, float* ws, hipStream_t s);
 bool nnk_gns_backward(int act, float* dx, float* ggamma, float* gbeta, const float* dy, const float* x,
-    const float* gamma, const float* beta, const float* mu, const float* rstd, int B, int HW, int C, int G,
-    float* ws, hipStream_t s);
+    const float* gamma, const float* beta, const float* mu, const float* rstd, const float* shift, float* gshift,
+    int B, int HW, int C, int G, float* ws, hipStream_t s);

@@ -59,6 +59,10 @@ Plan make_plan(bool bwd, int B, int HW, int C, int G) {
     p.tpart_offset = p.part_offset + part_bytes;
     const size_t tpart_bytes = bwd ? (size_t)((kMaxGrid + T - 1) / T) * nval_bytes : 0;
     p.ws_floats = (p.tpart_offset + tpart_bytes + sizeof(float) - 1) / sizeof(float);
+    // after everything epoch-tagged, on a 256-byte boundary: [tile][4 * kCw4]
+    p.colpart_offset = (p.ws_floats * sizeof(float) + 255) / 256 * 256;
+    p.ws_shift_floats =
+        bwd ? p.colpart_offset / sizeof(float) + (size_t)p.sh.ntiles * 4 * kCw4 : p.ws_floats;
     p.ok = true;
     return p;
 }
@@ -114,7 +118,7 @@ bool nnk_gns_launch(const void* fn, int P, void** args, hipStream_t s, const cha
 // Persistent grid size for a kernel: resident workgroups of the device
 // (cached per device and kernel), capped and rounded down to whole units.
 int nnk_gns_grid(const void* fn, int key, size_t lds, int unit) {
-    constexpr int kDev = 16, kKeys = 256;
+    constexpr int kDev = 16, kKeys = 2 * nnk::gns::kGnsBwdKeys;
     // per device and kernel: 0 = not yet queried, -1 = unusable, else the
     // resident workgroups per CU (relaxed atomics: concurrent callers may both
     // query, and store the same value)

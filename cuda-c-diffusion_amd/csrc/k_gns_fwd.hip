@@ -11,13 +11,14 @@ namespace {
 using namespace nnk;
 using namespace nnk::gns;
 
-template <int ACT, int CPG4, int RPL, bool NT>
+template <int ACT, int CPG4, int RPL, bool NT, bool SHIFT>
 bool launch(const Plan& p, float* y, float* mu, float* rstd, const float* x, const float* gamma,
-    const float* beta, float eps, float* ws, hipStream_t s) {
+    const float* beta, const float* shift, float eps, float* ws, hipStream_t s) {
     using Gm = Geom<kTpb, kFwdTp, kFwdCw4, CPG4>;
-    const void* fn = reinterpret_cast<const void*>(&gns_fwd<Gm, ACT, RPL, NT>);
+    const void* fn = reinterpret_cast<const void*>(&gns_fwd<Gm, ACT, RPL, NT, SHIFT>);
     const size_t lds = 0;  // all LDS is static (stage, parked, reduction buffers)
-    const int key = ((ACT * 3 + (CPG4 == 1 ? 0 : CPG4 == 2 ? 1 : 2)) * 2 + (RPL - 1)) * 2 + (NT ? 1 : 0);
+    const int key =
+        (((ACT * 3 + (CPG4 == 1 ? 0 : CPG4 == 2 ? 1 : 2)) * 2 + (RPL - 1)) * 2 + (NT ? 1 : 0)) * 2 + (SHIFT ? 1 : 0);
     const int P = nnk_gns_grid(fn, key, lds, p.sh.T * p.sh.NCB);
     if (P <= 0) return false;
     Shape sh = p.sh;
@@ -32,24 +33,31 @@ bool launch(const Plan& p, float* y, float* mu, float* rstd, const float* x, con
     wk.tpart = nullptr;
     unsigned limit = nnk_gns_spin_limit();
     void* args[] = {&y, &mu, &rstd, const_cast<float**>(&x), const_cast<float**>(&gamma),
-        const_cast<float**>(&beta), &sh, &wk, &eps, &limit};
+        const_cast<float**>(&beta), const_cast<float**>(&shift), &sh, &wk, &eps, &limit};
     return nnk_gns_launch(fn, P, args, s, "streaming GroupNorm forward");
 }
 
-template <int ACT>
+template <int ACT, bool SHIFT>
 bool by_shape(const Plan& p, float* y, float* mu, float* rstd, const float* x, const float* gamma,
-    const float* beta, float eps, float* ws, hipStream_t s) {
+    const float* beta, const float* shift, float eps, float* ws, hipStream_t s) {
     const bool nt = use_nt(8LL * p.sh.B * p.sh.HW * p.sh.C);
-#define NNK_GNS_FWD_CASE(CPG4, RPL)                                                     \
-    if (p.cpg4 == CPG4 && p.rpl == RPL)                                                 \
-        return nt ? launch<ACT, CPG4, RPL, true>(p, y, mu, rstd, x, gamma, beta, eps, ws, s)  \
-                  : launch<ACT, CPG4, RPL, false>(p, y, mu, rstd, x, gamma, beta, eps, ws, s);
-    NNK_GNS_FWD_CASE(1, 1)
-    NNK_GNS_FWD_CASE(1, 2)
-    NNK_GNS_FWD_CASE(2, 1)
-    NNK_GNS_FWD_CASE(2, 2)
-    NNK_GNS_FWD_CASE(4, 1)
-    NNK_GNS_FWD_CASE(4, 2)
+#define NNK_GNS_FWD_CASE(CPG4, RPL)                                                                      \
+    if (p.cpg4 == CPG4 && p.rpl == RPL)                                                                  \
+        return nt ? launch<ACT, CPG4, RPL, true, SHIFT>(p, y, mu, rstd, x, gamma, beta, shift, eps, ws, s) \
+                  : launch<ACT, CPG4, RPL, false, SHIFT>(p, y, mu, rstd, x, gamma, beta, shift, eps, ws, s);
+    // With a shift, only the geometry of the DDPM block's GroupNorm (8
+    // channels per group, one record per merging lane): the others need more
+    // registers than the tile loop has and take the launcher's composed path.
+    if constexpr (SHIFT) {
+        NNK_GNS_FWD_CASE(2, 1)
+    } else {
+        NNK_GNS_FWD_CASE(1, 1)
+        NNK_GNS_FWD_CASE(1, 2)
+        NNK_GNS_FWD_CASE(2, 1)
+        NNK_GNS_FWD_CASE(2, 2)
+        NNK_GNS_FWD_CASE(4, 1)
+        NNK_GNS_FWD_CASE(4, 2)
+    }
 #undef NNK_GNS_FWD_CASE
     return false;
 }
@@ -57,10 +65,16 @@ bool by_shape(const Plan& p, float* y, float* mu, float* rstd, const float* x, c
 }  // namespace
 
 bool nnk_gns_forward(int act, float* y, float* mu, float* rstd, const float* x, const float* gamma,
-    const float* beta, int B, int HW, int C, int G, float eps, float* ws, hipStream_t s) {
+    const float* beta, const float* shift, int B, int HW, int C, int G, float eps, float* ws, hipStream_t s) {
     const Plan p = make_plan(false, B, HW, C, G);
     if (!p.ok || !ws) return false;
     bool launched = false;
-    NNK_ACT_DISPATCH(act, A, launched = by_shape<A>(p, y, mu, rstd, x, gamma, beta, eps, ws, s));
+    // with a shift: SiLU only (the DDPM block's GN2); other activations take
+    // the launcher's composed path
+    if (shift)
+        launched = act == ACT_SILU &&
+            by_shape<ACT_SILU, true>(p, y, mu, rstd, x, gamma, beta, shift, eps, ws, s);
+    else
+        NNK_ACT_DISPATCH(act, A, launched = by_shape<A, false>(p, y, mu, rstd, x, gamma, beta, shift, eps, ws, s));
     return launched;
 }

@@ -264,14 +264,17 @@ bool want_stream(bool bwd, int B, int HW, int C, int G, bool reg_ok) {
 // gets a new one).  A lent workspace is zero-filled by its owner before first
 // use and written only by these launchers, so it can hold only zeros and older
 // epochs; a pool block may hold anything and is zeroed first.
+// `shift`: the launch is a backward with a shift, whose workspace also holds
+// the per-tile column sums (plain floats past the epoch-tagged region, which
+// alone needs clearing).
 template <class F>
 bool try_stream(bool bwd, int B, int HW, int C, int G, bool reg_ok, float* ws, hipStream_t s, const char* what,
-    F launch) {
+    F launch, bool shift = false) {
     if (!want_stream(bwd, B, HW, C, G, reg_ok)) return false;
     const nnk::gns::Plan p = nnk::gns::make_plan(bwd, B, HW, C, G);
     float* w = ws;
     if (!w) {
-        w = nnk_scratch_acquire(p.ws_floats, s, what);
+        w = nnk_scratch_acquire(shift ? p.ws_shift_floats : p.ws_floats, s, what);
         if (!w) return false;
         nnk_clear_workspace(w, p.ws_floats, s);
     }
@@ -302,7 +305,7 @@ void gn_forward_impl(const char* what, float* y, float* mu, float* rstd, const f
     bool launched = false;
     const bool stream_aligned = aligned16(x) && aligned16(y) && aligned16(gamma) && aligned16(beta);
     if (stream_aligned && try_stream(false, B, HW, C, G, v4pp != 0, ws, s, what, [&](float* w) {
-            return nnk_gns_forward(act, y, mu, rstd, x, gamma, beta, B, HW, C, G, eps, w, s);
+            return nnk_gns_forward(act, y, mu, rstd, x, gamma, beta, nullptr, B, HW, C, G, eps, w, s);
         })) {
         nnk_after_launch(what, s);
         return;
@@ -342,8 +345,8 @@ void gn_backward_impl(const char* what, float* dx, float* ggamma, float* gbeta, 
             (act == ACT_IDENTITY || aligned16(beta));
         if (stream_aligned &&
             try_stream(true, B, HW, C, G, reg_ok, ws, s, what, [&](float* w) {
-                return nnk_gns_backward(act, dx, ggamma, gbeta, dy, x, gamma, beta, mu, rstd, B, HW, C, G, w,
-                    s);
+                return nnk_gns_backward(act, dx, ggamma, gbeta, dy, x, gamma, beta, mu, rstd, nullptr, nullptr, B,
+                    HW, C, G, w, s);
             })) {
             nnk_after_launch(what, s);
             return;
@@ -377,6 +380,85 @@ void gn_backward_impl(const char* what, float* dx, float* ggamma, float* gbeta, 
         gbeta, part_g, part_b, B, C);
     if (!ws && !reg_ws) nnk_scratch_release(scratch, s);
     nnk_after_launch(what, s);
+}
+
+// x + shift[b, c] into a block of the stream's pool: the input of the
+// composition that the shift launchers fall back to (the reference's
+// broadcast add, src/conv_residual.c:34, one rounding per element).
+float* shifted_copy(const float* x, const float* shift, int B, int HW, int C, hipStream_t s, const char* what) {
+    const size_t n = (size_t)B * HW * C;
+    float* xs = nnk_scratch_acquire(n, s, what);
+    if (!xs) return nullptr;
+    const hipError_t e = hipMemcpyAsync(xs, x, n * sizeof(float), hipMemcpyDeviceToDevice, s);
+    if (e != hipSuccess) {
+        nnk_set_error((int)e, "%s: copy of the input: %s", what, hipGetErrorString(e));
+        nnk_scratch_release(xs, s);
+        return nullptr;
+    }
+    launch_spatial_add(xs, shift, B, HW, 1, C, s);
+    return xs;
+}
+
+void gn_shift_forward_impl(const char* what, float* y, float* mu, float* rstd, const float* x, const float* shift,
+    const float* gamma, const float* beta, int B, int HW, int C, int G, float eps, int act, float* ws,
+    hipStream_t s) {
+    if (!shape_ok(what, B, HW, C, G)) return;
+    NNK_REQUIRE(valid_act(act), what, "%s: unknown activation %d", what, act);
+    if (B == 0) return;
+    NNK_REQUIRE(y && mu && rstd && x && shift && gamma && beta, what, "%s: null pointer", what);
+    NNK_REQUIRE(ws == nullptr || aligned16(ws), what, "%s: workspace must be 16-byte aligned", what);
+    int cfg = -1;
+    const bool reg_ok = reg_v4pp(C / G, HW, x, y, gamma, beta, cfg) != 0;
+    const bool stream_aligned =
+        aligned16(x) && aligned16(y) && aligned16(gamma) && aligned16(beta) && aligned16(shift);
+    if (stream_aligned && try_stream(false, B, HW, C, G, reg_ok, ws, s, what, [&](float* w) {
+            return nnk_gns_forward(act, y, mu, rstd, x, gamma, beta, shift, B, HW, C, G, eps, w, s);
+        })) {
+        nnk_after_launch(what, s);
+        return;
+    }
+    float* xs = shifted_copy(x, shift, B, HW, C, s, what);
+    if (!xs) return;
+    gn_forward_impl(what, y, mu, rstd, xs, gamma, beta, B, HW, C, G, eps, act, ws, s);
+    nnk_scratch_release(xs, s);
+}
+
+void gn_shift_backward_impl(const char* what, float* dx, float* gshift, float* ggamma, float* gbeta,
+    const float* dy, const float* x, const float* shift, const float* gamma, const float* beta, const float* mu,
+    const float* rstd, int B, int HW, int C, int G, int act, float* ws, hipStream_t s) {
+    if (!shape_ok(what, B, HW, C, G)) return;
+    NNK_REQUIRE(valid_act(act), what, "%s: unknown activation %d", what, act);
+    NNK_REQUIRE(ggamma && gbeta, what, "%s: null pointer", what);
+    if (B == 0) {
+        gn_backward_impl(what, dx, ggamma, gbeta, dy, x, gamma, beta, mu, rstd, B, HW, C, G, act, ws, s);
+        return;
+    }
+    NNK_REQUIRE(dx && gshift && dy && x && shift && gamma && mu && rstd, what, "%s: null pointer", what);
+    NNK_REQUIRE(act == ACT_IDENTITY || beta, what, "%s: beta is required with an activation", what);
+    NNK_REQUIRE(ws == nullptr || aligned16(ws), what, "%s: workspace must be 16-byte aligned", what);
+    {
+        const bool stream_aligned = aligned16(x) && aligned16(dy) && aligned16(dx) && aligned16(gamma) &&
+            aligned16(shift) && (act == ACT_IDENTITY || aligned16(beta));
+        int cfg = -1;
+        const bool reg_ok = reg_v4pp(C / G, HW, x, dy, dx, gamma, cfg) != 0 &&
+            (act == ACT_IDENTITY || aligned16(beta));
+        if (stream_aligned &&
+            try_stream(
+                true, B, HW, C, G, reg_ok, ws, s, what,
+                [&](float* w) {
+                    return nnk_gns_backward(act, dx, ggamma, gbeta, dy, x, gamma, beta, mu, rstd, shift, gshift,
+                        B, HW, C, G, w, s);
+                },
+                true)) {
+            nnk_after_launch(what, s);
+            return;
+        }
+    }
+    float* xs = shifted_copy(x, shift, B, HW, C, s, what);
+    if (!xs) return;
+    gn_backward_impl(what, dx, ggamma, gbeta, dy, xs, gamma, beta, mu, rstd, B, HW, C, G, act, ws, s);
+    nnk_scratch_release(xs, s);
+    launch_spatial_reduce_sum(gshift, dx, B, HW, C, s);
 }
 
 }  // namespace
@@ -510,6 +592,26 @@ void launch_groupnorm_act_backward_noalloc(float* dx, float* ggamma, float* gbet
 size_t nnhip_groupnorm_backward_workspace(int batch, int HW, int C, int G) {
     if (batch <= 0 || C <= 0) return 0;
     return reg_partials_offset(batch, HW, C, G) + (size_t)2 * batch * C;
+}
+
+void launch_groupnorm_act_shift_forward_ws(float* y, float* mu, float* rstd, const float* x, const float* shift,
+    const float* gamma, const float* beta, int batch, int HW, int C, int G, float eps, Activation act,
+    float* workspace, hipStream_t s) {
+    gn_shift_forward_impl("launch_groupnorm_act_shift_forward_ws", y, mu, rstd, x, shift, gamma, beta, batch, HW,
+        C, G, eps, (int)act, workspace, s);
+}
+
+void launch_groupnorm_act_shift_backward_ws(float* dx, float* gshift, float* ggamma, float* gbeta,
+    const float* dy, const float* x, const float* shift, const float* gamma, const float* beta, const float* mu,
+    const float* rstd, int batch, int HW, int C, int G, Activation act, float* workspace, hipStream_t s) {
+    gn_shift_backward_impl("launch_groupnorm_act_shift_backward_ws", dx, gshift, ggamma, gbeta, dy, x, shift,
+        gamma, beta, mu, rstd, batch, HW, C, G, (int)act, workspace, s);
+}
+
+size_t nnhip_groupnorm_shift_backward_workspace(int batch, int HW, int C, int G) {
+    const size_t plain = nnhip_groupnorm_backward_workspace(batch, HW, C, G);
+    const nnk::gns::Plan p = nnk::gns::make_plan(true, batch, HW, C, G);
+    return p.ok && p.ws_shift_floats > plain ? p.ws_shift_floats : plain;
 }
 
 }  // extern "C"

@@ -14,8 +14,11 @@
  *   * every GroupNorm -> SiLU pair is one fused module, the modulation and the
  *     MP-SiLU after it one fused launch each way; the pre-activation tensors
  *     and their gradients never exist;
- *   * the embedding broadcast-sum's gradient is a parallel reduction into a
- *     lent workspace;
+ *   * the DDPM block's embedding broadcast add is folded into GN2 (its input
+ *     h + c is formed inside the GroupNorm kernels, never stored) and the
+ *     embedding gradient's pixel sum into GN2's backward;
+ *   * the EDM block's modulation gradient is a parallel reduction into a lent
+ *     workspace;
  *   * the arena holds only what the backward reads (the inputs of the
  *     children) plus two gradient tensors that the backward reuses as each
  *     one's last reader has run.
@@ -29,7 +32,7 @@
  * ------------------------------------------------------------------------ */
 
 enum { DS_GN1, DS_CONV1, DS_PROJ, DS_GN2, DS_CONV2 };
-enum { DT_A1, DT_H, DT_C, DT_A2, DT_G0, DT_G1, DT_GC, DT_GEMB, DT_RED };
+enum { DT_A1, DT_H, DT_C, DT_A2, DT_G0, DT_G1, DT_GC, DT_GEMB };
 enum { DD_C, DD_EMB, DD_HW, DD_SLOT };
 
 static void ddpm_fwd(Layer* L, const float* x, float* out, int batch, Context* ctx)
@@ -40,8 +43,7 @@ static void ddpm_fwd(Layer* L, const float* x, float* out, int batch, Context* c
     s[DS_GN1]->forward(s[DS_GN1], x, t[DT_A1], batch, ctx);                         /* a1 = silu(gn1(x)) */
     s[DS_CONV1]->forward(s[DS_CONV1], t[DT_A1], t[DT_H], batch, ctx);               /* h = conv1(a1) */
     s[DS_PROJ]->forward(s[DS_PROJ], ctx->cond[L->dim[DD_SLOT]].fwd, t[DT_C], batch, ctx); /* c = proj(emb) */
-    launch_spatial_add(t[DT_H], t[DT_C], batch, L->dim[DD_HW], 1, L->dim[DD_C], ctx->stream); /* h += c */
-    s[DS_GN2]->forward(s[DS_GN2], t[DT_H], t[DT_A2], batch, ctx);                   /* a2 = silu(gn2(h)) */
+    groupnorm_shift_forward(s[DS_GN2], t[DT_H], t[DT_C], t[DT_A2], batch, ctx);      /* a2 = silu(gn2(h + c)) */
     s[DS_CONV2]->forward(s[DS_CONV2], t[DT_A2], out, batch, ctx);                   /* out = conv2(a2) */
     launch_weighted_sum(out, x, out, 1.0f, 1.0f, n, ctx->stream);                   /* out += x */
 }
@@ -55,9 +57,8 @@ static void ddpm_bwd(Layer* L, const float* x, const float* out, const float* g_
     const int n = batch * L->dim[DD_HW] * L->dim[DD_C];
     CondSlot* slot = &ctx->cond[L->dim[DD_SLOT]];
     s[DS_CONV2]->backward(s[DS_CONV2], t[DT_A2], NULL, g_out, t[DT_G0], batch, ctx);   /* G0 = d a2 */
-    s[DS_GN2]->backward(s[DS_GN2], t[DT_H], NULL, t[DT_G0], t[DT_G1], batch, ctx);     /* G1 = d h */
-    launch_spatial_reduce_sum_ws(t[DT_GC], t[DT_G1], batch, L->dim[DD_HW], L->dim[DD_C], t[DT_RED],
-        ctx->stream);                                                                  /* dc = sum_hw d h */
+    groupnorm_shift_backward(s[DS_GN2], t[DT_H], t[DT_C], t[DT_G0], t[DT_G1], t[DT_GC], batch,
+        ctx);                                                                          /* G1 = d h, dc */
     s[DS_PROJ]->backward(s[DS_PROJ], slot->fwd, t[DT_C], t[DT_GC], t[DT_GEMB], batch, ctx);
     launch_weighted_sum(slot->grad, slot->grad, t[DT_GEMB], 1.0f, 1.0f, batch * L->dim[DD_EMB], ctx->stream);
     s[DS_CONV1]->backward(s[DS_CONV1], t[DT_A1], NULL, t[DT_G1], t[DT_G0], batch, ctx); /* G0 = d a1 */
@@ -80,18 +81,17 @@ Module* conv_residual_create(Context* ctx, int C, int emb_dim, int H, int W, int
     layer_sub(L, spatial_groupnorm_act_create(C, num_groups, H, W, max_batch, ACT_SILU));
     layer_sub(L, conv2d_create(ctx, C, C, 3, 1, 1, H, W, max_batch, 0, 1.0f));
     layer_sub(L, linear_create(ctx, emb_dim, C));
-    layer_sub(L, spatial_groupnorm_act_create(C, num_groups, H, W, max_batch, ACT_SILU));
+    layer_sub(L, spatial_groupnorm_act_shift_create(C, num_groups, H, W, max_batch, ACT_SILU));
     layer_sub(L, conv2d_create(ctx, C, C, 3, 1, 1, H, W, max_batch, 0, 1.0f));
     const size_t ns = (size_t)max_batch * HW * C;
     layer_buf(L, ns, 0);                                   /* a1 */
-    layer_buf(L, ns, 0);                                   /* h (then h + c) */
+    layer_buf(L, ns, 0);                                   /* h */
     layer_buf(L, (size_t)max_batch * C, 0);                /* c */
     layer_buf(L, ns, 0);                                   /* a2 */
     layer_buf(L, ns, 0);                                   /* gradient tensor 0 */
     layer_buf(L, ns, 0);                                   /* gradient tensor 1 */
     layer_buf(L, (size_t)max_batch * C, 0);                /* dc */
     layer_buf(L, (size_t)max_batch * emb_dim, 0);          /* d emb of this block */
-    layer_buf(L, nnhip_spatial_reduce_workspace(max_batch, HW, C), 1);
     return layer_end(L);
 }
 

@@ -73,4 +73,16 @@ static inline Layer* as_layer(Module* m) { return (Layer*)m; }
 /* Host-to-device fill of a buffer with one value (construction time). */
 void layer_fill_value(Layer* L, int b, size_t n, float value);
 
+/* A fused GroupNorm+activation layer whose input may carry a per-(sample,
+   channel) shift: an ordinary spatial_groupnorm_act module (same parameters,
+   ParamList and vtable) whose backward workspace also fits the shift path.
+   groupnorm_shift_forward / _backward run it on x + shift[b, c] (shift
+   [batch, C], never added in memory): y = act(GN(x + shift)); g_x = the
+   gradient of x + shift, g_shift[b, c] = its sum over the pixels (both
+   overwritten; the parameter gradients too, as in the plain backward). */
+Module* spatial_groupnorm_act_shift_create(int C, int num_groups, int H, int W, int max_batch, Activation act);
+void groupnorm_shift_forward(Module* gn, const float* x, const float* shift, float* y, int batch, Context* ctx);
+void groupnorm_shift_backward(Module* gn, const float* x, const float* shift, const float* g_y, float* g_x,
+    float* g_shift, int batch, Context* ctx);
+
 #endif /* NN_LAYER_H */

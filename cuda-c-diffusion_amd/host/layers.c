@@ -126,7 +126,7 @@ Module* layernorm_create(int dim, int max_batch)
 }
 
 static Module* groupnorm_make(const LayerKind* kind, int C, int num_groups, int H, int W, int max_batch,
-    Activation act)
+    Activation act, int shift)
 {
     NN_ASSERT(num_groups > 0 && C % num_groups == 0, "groupnorm: C must be divisible by num_groups");
     Layer* L = layer_begin(kind, H * W * C, H * W * C, max_batch);
@@ -135,19 +135,45 @@ static Module* groupnorm_make(const LayerKind* kind, int C, int num_groups, int 
     L->dim[ND_HW] = H * W;
     /* workspaces sized for max_batch serve every smaller batch; a forward that
        needs none gets no buffer (the launcher then works without one) */
+    const int HW = H * W;
     return affine_norm(L, C, (size_t)max_batch * num_groups,
-        nnhip_groupnorm_backward_workspace(max_batch, H * W, C, num_groups),
-        nnhip_groupnorm_forward_workspace(max_batch, H * W, C, num_groups));
+        shift ? nnhip_groupnorm_shift_backward_workspace(max_batch, HW, C, num_groups)
+              : nnhip_groupnorm_backward_workspace(max_batch, HW, C, num_groups),
+        nnhip_groupnorm_forward_workspace(max_batch, HW, C, num_groups));
 }
 
 Module* spatial_groupnorm_create(int C, int num_groups, int H, int W, int max_batch)
 {
-    return groupnorm_make(&kGroupNorm, C, num_groups, H, W, max_batch, ACT_IDENTITY);
+    return groupnorm_make(&kGroupNorm, C, num_groups, H, W, max_batch, ACT_IDENTITY, 0);
 }
 
 Module* spatial_groupnorm_act_create(int C, int num_groups, int H, int W, int max_batch, Activation act)
 {
-    return groupnorm_make(&kGroupNormAct, C, num_groups, H, W, max_batch, act);
+    return groupnorm_make(&kGroupNormAct, C, num_groups, H, W, max_batch, act, 0);
+}
+
+Module* spatial_groupnorm_act_shift_create(int C, int num_groups, int H, int W, int max_batch, Activation act)
+{
+    return groupnorm_make(&kGroupNormAct, C, num_groups, H, W, max_batch, act, 1);
+}
+
+void groupnorm_shift_forward(Module* gn, const float* x, const float* shift, float* y, int batch, Context* ctx)
+{
+    Layer* L = as_layer(gn);
+    NN_ASSERT(batch <= L->max_batch, L->kind->name);
+    launch_groupnorm_act_shift_forward_ws(y, L->buf[NB_MU], L->buf[NB_RSTD], x, shift, L->buf[NB_GAMMA],
+        L->buf[NB_BETA], batch, L->dim[ND_HW], L->dim[ND_C], L->dim[ND_G], L->k[0], L->act, L->buf[NB_FWS],
+        ctx->stream);
+}
+
+void groupnorm_shift_backward(Module* gn, const float* x, const float* shift, const float* g_y, float* g_x,
+    float* g_shift, int batch, Context* ctx)
+{
+    Layer* L = as_layer(gn);
+    NN_ASSERT(batch <= L->max_batch, L->kind->name);
+    launch_groupnorm_act_shift_backward_ws(g_x, g_shift, L->buf[NB_GGAMMA], L->buf[NB_GBETA], g_y, x, shift,
+        L->buf[NB_GAMMA], L->buf[NB_BETA], L->buf[NB_MU], L->buf[NB_RSTD], batch, L->dim[ND_HW], L->dim[ND_C],
+        L->dim[ND_G], L->act, L->buf[NB_BWS], ctx->stream);
 }
 
 /* ------------------------------------------------------------------------

@@ -311,6 +311,34 @@ void launch_layernorm_backward_ws(float* grad_in, float* ggamma, float* gbeta,
     const float* mu, const float* rstd,
     int batch, int C, float* workspace, hipStream_t s);
 
+/* y = act(GroupNorm(x + shift[b, c])): the DDPM block's broadcast add of the
+   embedding projection folded into the GroupNorm that reads it.  Replaces
+   launch_spatial_add + launch_groupnorm_forward + launch_activation_forward
+   (src/conv_residual.c:34-37); x is not modified and x + shift is not stored
+   (each element is the same single fp32 sum the add would store).
+   `workspace` as for launch_groupnorm_act_forward_ws
+   (nnhip_groupnorm_forward_workspace floats). */
+void launch_groupnorm_act_shift_forward_ws(float* y, float* mu, float* rstd,
+    const float* x, const float* shift, const float* gamma, const float* beta,
+    int batch, int HW, int C, int G, float eps, Activation act,
+    float* workspace, hipStream_t s);
+/* Backward of launch_groupnorm_act_shift_forward_ws: dx = the gradient of
+   x + shift (hence of x), gshift[b, c] = the sum over the pixels of dx,
+   ggamma/gbeta, all overwritten.  Replaces launch_activation_backward +
+   launch_groupnorm_backward + launch_spatial_reduce_sum
+   (src/conv_residual.c:51-55).  gshift is summed in a fixed order that differs
+   from launch_spatial_reduce_sum's (per 64-pixel tile, then over the tiles);
+   dx, ggamma and gbeta are those of launch_groupnorm_act_backward on
+   x + shift.  `workspace` holds nnhip_groupnorm_shift_backward_workspace
+   floats.  Shapes that the persistent kernels do not take compose the
+   separate launches on a batch*HW*C temporary from the stream's pool. */
+void launch_groupnorm_act_shift_backward_ws(float* dx, float* gshift, float* ggamma, float* gbeta,
+    const float* dy, const float* x, const float* shift, const float* gamma, const float* beta,
+    const float* mu, const float* rstd,
+    int batch, int HW, int C, int G, Activation act,
+    float* workspace, hipStream_t s);
+size_t nnhip_groupnorm_shift_backward_workspace(int batch, int HW, int C, int G);
+
 /* Large GroupNorm launches use persistent workgroups that exchange per-tile
    statistics through the workspace and wait for each other with bounded
    polls.  A workspace lent to the GroupNorm launchers must be zero-filled

@@ -1,0 +1,171 @@
+"""GroupNorm + activation of x + shift[b, c]
+(launch_groupnorm_act_shift_forward_ws / _backward_ws): the DDPM block's
+embedding broadcast add folded into GN2, and the embedding gradient's pixel
+sum folded into GN2's backward (reference src/conv_residual.c:34-37, 51-55).
+
+Bars:
+  * y, mu, rstd, dx, dgamma, dbeta are bit-identical to the plain launchers
+    run on xs = x + shift formed in float32 (one rounding per element, as
+    launch_spatial_add stores it): the reference's own composition;
+  * gshift, summed per 64-pixel tile and then over the tiles, is within TOL of
+    the float64 pixel sum of that dx, relative to max(|sum|, sqrt(sum dx^2))
+    per channel (the floor of every reduced output in these tests);
+  * on one case, y and dx against the oracle's composition.
+The streaming shift kernels take SiLU at 8 channels per group with one record
+per merging lane; other activations and geometries compose the plain launchers
+on a pooled x + shift (checked the same way).  Where the streaming kernels are
+meant to run, the workspaces must hold this launch's tagged records.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from helpers import TOL, assert_bits_equal, rel_err
+from test_gpu_groupnorm import make_inputs
+from test_gpu_groupnorm_stream import BWD_TP, FWD_TP, records_tagged, tiles, zeroed
+
+pytestmark = pytest.mark.gpu
+
+SILU = 3
+
+
+def shift_case(rng, B, C):
+    return (0.5 * rng.standard_normal((B, C))).astype(np.float32)
+
+
+def run_shift(L, x, sh, gamma, beta, dy, G, act, fws, bws):
+    """The fused launchers; returns (y, mu, rstd, dx, gshift, dgamma, dbeta)."""
+    B, HW, C = x.shape
+    xd, shd, dyd = L.to_device(x), L.to_device(sh), L.to_device(dy)
+    gd, bd = L.to_device(gamma), L.to_device(beta)
+    yd, dxd, gsd = L.alloc(x.size), L.alloc(x.size), L.alloc(B * C)
+    mud, rsd, ggd, gbd = L.alloc(B * G), L.alloc(B * G), L.alloc(C), L.alloc(C)
+    L.launch_groupnorm_act_shift_forward_ws(yd.p, mud.p, rsd.p, xd.p, shd.p, gd.p, bd.p, B, HW, C, G, 1e-5, act,
+                                            fws.p, None)
+    L.launch_groupnorm_act_shift_backward_ws(dxd.p, gsd.p, ggd.p, gbd.p, dyd.p, xd.p, shd.p, gd.p, bd.p, mud.p,
+                                             rsd.p, B, HW, C, G, act, bws.p, None)
+    L.sync()
+    return (yd.download(shape=x.shape), mud.download(), rsd.download(), dxd.download(shape=x.shape),
+            gsd.download(shape=(B, C)), ggd.download(), gbd.download())
+
+
+def run_plain(L, xs, gamma, beta, dy, G, act):
+    """The plain launchers on xs = x + shift, each with a fresh workspace, and
+    launch_spatial_reduce_sum of their dx."""
+    B, HW, C = xs.shape
+    xd, dyd = L.to_device(xs), L.to_device(dy)
+    gd, bd = L.to_device(gamma), L.to_device(beta)
+    yd, dxd, gsd = L.alloc(xs.size), L.alloc(xs.size), L.alloc(B * C)
+    mud, rsd, ggd, gbd = L.alloc(B * G), L.alloc(B * G), L.alloc(C), L.alloc(C)
+    fws = zeroed(L, max(1, L.nnhip_groupnorm_forward_workspace(B, HW, C, G)))
+    bws = zeroed(L, L.nnhip_groupnorm_backward_workspace(B, HW, C, G))
+    L.launch_groupnorm_act_forward_ws(yd.p, mud.p, rsd.p, xd.p, gd.p, bd.p, B, HW, C, G, 1e-5, act, fws.p, None)
+    L.launch_groupnorm_act_backward_ws(dxd.p, ggd.p, gbd.p, dyd.p, xd.p, gd.p, bd.p, mud.p, rsd.p, B, HW, C, G,
+                                       act, bws.p, None)
+    L.launch_spatial_reduce_sum(gsd.p, dxd.p, B, HW, C, None)
+    L.sync()
+    return (yd.download(shape=xs.shape), mud.download(), rsd.download(), dxd.download(shape=xs.shape),
+            gsd.download(shape=(B, C)), ggd.download(), gbd.download())
+
+
+def pixel_sum_check(gs, dx, what):
+    ref = dx.astype(np.float64).sum(axis=1)
+    floor = np.sqrt((dx.astype(np.float64) ** 2).sum(axis=1))
+    err = rel_err(gs, ref, floor=floor)
+    assert err <= TOL, f"{what}: relative error {err:.3e}"
+
+
+def check(L, rng, shape, act, stream_expected):
+    B, H, W, C, G = shape
+    HW = H * W
+    x, gamma, beta, dy = make_inputs(rng, B, H, W, C)
+    sh = shift_case(rng, B, C)
+    xs = (x + sh[:, None, :]).astype(np.float32)
+    fws = zeroed(L, max(1, L.nnhip_groupnorm_forward_workspace(B, HW, C, G)))
+    bws = zeroed(L, L.nnhip_groupnorm_shift_backward_workspace(B, HW, C, G))
+    got = run_shift(L, x, sh, gamma, beta, dy, G, act, fws, bws)
+    if stream_expected:
+        ok, nrec = tiles(L, B, HW, C, G, FWD_TP)
+        assert ok and records_tagged(fws, nrec), "forward did not take the streaming path"
+        ok, nrec = tiles(L, B, HW, C, G, BWD_TP)
+        assert ok and records_tagged(bws, nrec), "backward did not take the streaming path"
+    assert L.nnhip_groupnorm_workspace_status(fws.p) == 0
+    assert L.nnhip_groupnorm_workspace_status(bws.p) == 0
+    ref = run_plain(L, xs, gamma, beta, dy, G, act)
+    for g, r, what in zip(got, ref, ("y", "mu", "rstd", "dx", None, "dgamma", "dbeta")):
+        if what:
+            assert_bits_equal(g, r, what)
+    pixel_sum_check(got[4], got[3], "gshift vs the pixel sum of dx")
+    pixel_sum_check(ref[4], ref[3], "launch_spatial_reduce_sum vs the pixel sum of dx")
+    return x, sh, xs, gamma, beta, dy, got
+
+
+# (B, H, W, C, G); rounds per backward workgroup on a 256-CU device: the
+# backward has 128 tiles per 64x64x256 sample, so B = 1, 3, 6, 8, 16 give
+# 1, 1-2, 3, 4, 8 rounds (the epilogue cases K = 1, 2, 3 and the steady loop).
+STREAM_SHAPES = [
+    (1, 64, 64, 256, 32),
+    (3, 64, 64, 256, 32),
+    (6, 64, 64, 256, 32),
+    (8, 64, 64, 256, 32),
+    (16, 64, 64, 256, 32),
+    (16, 32, 32, 256, 32),   # the DDPM block test's streaming shape
+    (2, 64, 64, 512, 64),    # cpg 8, four column blocks
+]
+
+
+@pytest.mark.parametrize("shape", STREAM_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_shift_stream_matches_plain_composition(L, rng, monkeypatch, shape):
+    print(f"[case] groupnorm shift stream {shape}", flush=True)
+    monkeypatch.setenv("NNHIP_GN_PATH", "stream")
+    check(L, rng, shape, SILU, True)
+
+
+@pytest.mark.parametrize("shape,act,path", [
+    ((2, 32, 32, 128, 32), SILU, "stream"),   # cpg 4: composed
+    ((2, 16, 16, 256, 16), SILU, "stream"),   # cpg 16: composed
+    ((2, 64, 64, 256, 32), 0, "stream"),      # identity: composed
+    ((2, 64, 64, 256, 32), SILU, "reg"),      # register path forced: composed
+    ((2, 8, 8, 32, 8), SILU, ""),             # the small block test's shape, auto policy
+], ids=["cpg4", "cpg16", "identity", "reg", "small-auto"])
+def test_shift_composed_matches_plain_composition(L, rng, monkeypatch, shape, act, path):
+    print(f"[case] groupnorm shift composed {shape} act={act} path={path or 'auto'}", flush=True)
+    if path:
+        monkeypatch.setenv("NNHIP_GN_PATH", path)
+    else:
+        monkeypatch.delenv("NNHIP_GN_PATH", raising=False)
+    check(L, rng, shape, act, False)
+
+
+def test_shift_against_oracle(L, orc, rng, monkeypatch):
+    print("[case] groupnorm shift vs oracle", flush=True)
+    monkeypatch.setenv("NNHIP_GN_PATH", "stream")
+    B, H, W, C, G = 3, 64, 64, 256, 32
+    x, sh, xs, gamma, beta, dy, got = check(L, rng, (B, H, W, C, G), SILU, True)
+    xs_o = orc.spatial_add(x, sh)
+    assert_bits_equal(xs_o, xs, "oracle spatial_add vs float32 x + shift")
+    y_ref, mu_ref, rs_ref = orc.groupnorm_forward(xs_o, gamma, beta, G, 1e-5, SILU)
+    assert rel_err(got[0], y_ref) <= TOL
+    dx_ref, _, _ = orc.groupnorm_backward(dy, xs_o, gamma, beta, mu_ref, rs_ref, G, SILU)
+    assert rel_err(got[3], dx_ref) <= TOL
+    gs_ref = orc.spatial_reduce_sum(dx_ref)
+    floor = np.sqrt((dx_ref.astype(np.float64) ** 2).sum(axis=1))
+    assert rel_err(got[4], gs_ref, floor=floor) <= TOL
+
+
+def test_shift_repeat_is_bit_identical(L, rng, monkeypatch):
+    """Two launches on the same lent workspaces give the same bits (fixed
+    orders of every sum, the column sums included)."""
+    print("[case] groupnorm shift determinism", flush=True)
+    monkeypatch.setenv("NNHIP_GN_PATH", "stream")
+    B, H, W, C, G = 6, 64, 64, 256, 32
+    HW = H * W
+    x, gamma, beta, dy = make_inputs(rng, B, H, W, C)
+    sh = shift_case(rng, B, C)
+    fws = zeroed(L, L.nnhip_groupnorm_forward_workspace(B, HW, C, G))
+    bws = zeroed(L, L.nnhip_groupnorm_shift_backward_workspace(B, HW, C, G))
+    a = run_shift(L, x, sh, gamma, beta, dy, G, SILU, fws, bws)
+    b = run_shift(L, x, sh, gamma, beta, dy, G, SILU, fws, bws)
+    for u, v, what in zip(a, b, ("y", "mu", "rstd", "dx", "gshift", "dgamma", "dbeta")):
+        assert_bits_equal(u, v, what)
