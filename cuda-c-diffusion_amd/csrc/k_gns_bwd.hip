@@ -74,17 +74,16 @@ bool by_shape(const Plan& p, float* dx, float* ggamma, float* gbeta, const float
                         shift, gshift, ws, s)                                                                  \
                   : launch<ACT, CPG4, RPL, false, SHIFT>(p, dx, ggamma, gbeta, dy, x, gamma, beta, mu, rstd,    \
                         shift, gshift, ws, s);
-    // With a shift, only the geometry of the DDPM block's GroupNorm (8
-    // channels per group, one record per merging lane): the others need more
-    // registers than the tile loop has and take the launcher's composed path.
-    if constexpr (SHIFT) {
-        NNK_GNS_BWD_CASE(2, 1)
-    } else {
-        NNK_GNS_BWD_CASE(1, 1)
+    // With a shift, one record per merging lane: with two, the tile loop runs
+    // out of registers and would spill inside the loop (a spill reload is a
+    // full wait on the staged loads); the launcher composes the plain kernel
+    // on a pooled x + shift instead.
+    NNK_GNS_BWD_CASE(1, 1)
+    NNK_GNS_BWD_CASE(2, 1)
+    NNK_GNS_BWD_CASE(4, 1)
+    if constexpr (!SHIFT) {
         NNK_GNS_BWD_CASE(1, 2)
-        NNK_GNS_BWD_CASE(2, 1)
         NNK_GNS_BWD_CASE(2, 2)
-        NNK_GNS_BWD_CASE(4, 1)
         NNK_GNS_BWD_CASE(4, 2)
     }
 #undef NNK_GNS_BWD_CASE

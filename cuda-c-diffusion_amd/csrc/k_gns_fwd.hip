@@ -45,11 +45,15 @@ bool by_shape(const Plan& p, float* y, float* mu, float* rstd, const float* x, c
     if (p.cpg4 == CPG4 && p.rpl == RPL)                                                                  \
         return nt ? launch<ACT, CPG4, RPL, true, SHIFT>(p, y, mu, rstd, x, gamma, beta, shift, eps, ws, s) \
                   : launch<ACT, CPG4, RPL, false, SHIFT>(p, y, mu, rstd, x, gamma, beta, shift, eps, ws, s);
-    // With a shift, only the geometry of the DDPM block's GroupNorm (8
-    // channels per group, one record per merging lane): the others need more
-    // registers than the tile loop has and take the launcher's composed path.
+    // With a shift, 8 or 16 channels per group: at 4 the tile loop runs out
+    // of registers and would spill inside the loop (a spill reload is a full
+    // wait on the staged loads); the launcher composes the plain kernel on a
+    // pooled x + shift instead.
     if constexpr (SHIFT) {
         NNK_GNS_FWD_CASE(2, 1)
+        NNK_GNS_FWD_CASE(2, 2)
+        NNK_GNS_FWD_CASE(4, 1)
+        NNK_GNS_FWD_CASE(4, 2)
     } else {
         NNK_GNS_FWD_CASE(1, 1)
         NNK_GNS_FWD_CASE(1, 2)

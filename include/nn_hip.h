@@ -330,8 +330,10 @@ void launch_groupnorm_act_shift_forward_ws(float* y, float* mu, float* rstd,
    from launch_spatial_reduce_sum's (per 64-pixel tile, then over the tiles);
    dx, ggamma and gbeta are those of launch_groupnorm_act_backward on
    x + shift.  `workspace` holds nnhip_groupnorm_shift_backward_workspace
-   floats.  Shapes that the persistent kernels do not take compose the
-   separate launches on a batch*HW*C temporary from the stream's pool. */
+   floats.  The persistent kernels take SiLU: the forward at 8 or 16 channels
+   per group, the backward at 4 (up to 2048 pixels) or 8 or 16 (up to 4096).
+   Other activations and shapes compose the separate launches on a
+   batch*HW*C temporary from the stream's pool. */
 void launch_groupnorm_act_shift_backward_ws(float* dx, float* gshift, float* ggamma, float* gbeta,
     const float* dy, const float* x, const float* shift, const float* gamma, const float* beta,
     const float* mu, const float* rstd,

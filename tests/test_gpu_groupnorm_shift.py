@@ -11,10 +11,12 @@ Bars:
     the float64 pixel sum of that dx, relative to max(|sum|, sqrt(sum dx^2))
     per channel (the floor of every reduced output in these tests);
   * on one case, y and dx against the oracle's composition.
-The streaming shift kernels take SiLU at 8 channels per group with one record
-per merging lane; other activations and geometries compose the plain launchers
-on a pooled x + shift (checked the same way).  Where the streaming kernels are
-meant to run, the workspaces must hold this launch's tagged records.
+The streaming shift kernels take SiLU, the forward at 8 or 16 channels per
+group and the backward at 4, 8 or 16 with one record per merging lane (at most
+64 pixel tiles per sample and column block); other activations and geometries compose
+the plain launchers on a pooled x + shift (checked the same way).  Where the
+streaming kernels are meant to run, the workspaces must hold this launch's
+tagged records.
 """
 from __future__ import annotations
 
@@ -76,7 +78,7 @@ def pixel_sum_check(gs, dx, what):
     assert err <= TOL, f"{what}: relative error {err:.3e}"
 
 
-def check(L, rng, shape, act, stream_expected):
+def check(L, rng, shape, act, stream_fwd, stream_bwd):
     B, H, W, C, G = shape
     HW = H * W
     x, gamma, beta, dy = make_inputs(rng, B, H, W, C)
@@ -85,9 +87,10 @@ def check(L, rng, shape, act, stream_expected):
     fws = zeroed(L, max(1, L.nnhip_groupnorm_forward_workspace(B, HW, C, G)))
     bws = zeroed(L, L.nnhip_groupnorm_shift_backward_workspace(B, HW, C, G))
     got = run_shift(L, x, sh, gamma, beta, dy, G, act, fws, bws)
-    if stream_expected:
+    if stream_fwd:
         ok, nrec = tiles(L, B, HW, C, G, FWD_TP)
         assert ok and records_tagged(fws, nrec), "forward did not take the streaming path"
+    if stream_bwd:
         ok, nrec = tiles(L, B, HW, C, G, BWD_TP)
         assert ok and records_tagged(bws, nrec), "backward did not take the streaming path"
     assert L.nnhip_groupnorm_workspace_status(fws.p) == 0
@@ -101,48 +104,51 @@ def check(L, rng, shape, act, stream_expected):
     return x, sh, xs, gamma, beta, dy, got
 
 
-# (B, H, W, C, G); rounds per backward workgroup on a 256-CU device: the
-# backward has 128 tiles per 64x64x256 sample, so B = 1, 3, 6, 8, 16 give
-# 1, 1-2, 3, 4, 8 rounds (the epilogue cases K = 1, 2, 3 and the steady loop).
+# (B, H, W, C, G), streaming shift kernels expected (forward, backward).  On a
+# 256-CU device the backward has 128 tiles per 64x64x256 sample, so B = 1, 3,
+# 6, 8, 16 give 1, 1-2, 3, 4, 8 rounds per workgroup (the epilogue cases K =
+# 1, 2, 3 and both halves of the two-round loop).
 STREAM_SHAPES = [
-    (1, 64, 64, 256, 32),
-    (3, 64, 64, 256, 32),
-    (6, 64, 64, 256, 32),
-    (8, 64, 64, 256, 32),
-    (16, 64, 64, 256, 32),
-    (16, 32, 32, 256, 32),   # the DDPM block test's streaming shape
-    (2, 64, 64, 512, 64),    # cpg 8, four column blocks
+    ((1, 64, 64, 256, 32), True, True),
+    ((3, 64, 64, 256, 32), True, True),
+    ((6, 64, 64, 256, 32), True, True),
+    ((8, 64, 64, 256, 32), True, True),
+    ((16, 64, 64, 256, 32), True, True),
+    ((16, 32, 32, 256, 32), True, True),   # the DDPM block test's streaming shape
+    ((2, 64, 64, 512, 64), True, True),    # cpg 8, four column blocks
+    ((2, 16, 16, 256, 16), True, True),    # cpg 16
+    ((4, 32, 32, 128, 32), False, True),   # cpg 4: forward composed, backward streamed
+    ((1, 64, 128, 256, 32), True, False),  # backward merges 2 records per lane: composed
+    ((1, 128, 128, 128, 8), True, False),  # forward merges 2 records per lane; backward too large
 ]
 
 
-@pytest.mark.parametrize("shape", STREAM_SHAPES, ids=lambda s: "x".join(map(str, s)))
-def test_shift_stream_matches_plain_composition(L, rng, monkeypatch, shape):
+@pytest.mark.parametrize("shape,sf,sb", STREAM_SHAPES, ids=lambda v: "x".join(map(str, v)) if isinstance(v, tuple) else None)
+def test_shift_stream_matches_plain_composition(L, rng, monkeypatch, shape, sf, sb):
     print(f"[case] groupnorm shift stream {shape}", flush=True)
     monkeypatch.setenv("NNHIP_GN_PATH", "stream")
-    check(L, rng, shape, SILU, True)
+    check(L, rng, shape, SILU, sf, sb)
 
 
 @pytest.mark.parametrize("shape,act,path", [
-    ((2, 32, 32, 128, 32), SILU, "stream"),   # cpg 4: composed
-    ((2, 16, 16, 256, 16), SILU, "stream"),   # cpg 16: composed
     ((2, 64, 64, 256, 32), 0, "stream"),      # identity: composed
     ((2, 64, 64, 256, 32), SILU, "reg"),      # register path forced: composed
     ((2, 8, 8, 32, 8), SILU, ""),             # the small block test's shape, auto policy
-], ids=["cpg4", "cpg16", "identity", "reg", "small-auto"])
+], ids=["identity", "reg", "small-auto"])
 def test_shift_composed_matches_plain_composition(L, rng, monkeypatch, shape, act, path):
     print(f"[case] groupnorm shift composed {shape} act={act} path={path or 'auto'}", flush=True)
     if path:
         monkeypatch.setenv("NNHIP_GN_PATH", path)
     else:
         monkeypatch.delenv("NNHIP_GN_PATH", raising=False)
-    check(L, rng, shape, act, False)
+    check(L, rng, shape, act, False, False)
 
 
 def test_shift_against_oracle(L, orc, rng, monkeypatch):
     print("[case] groupnorm shift vs oracle", flush=True)
     monkeypatch.setenv("NNHIP_GN_PATH", "stream")
     B, H, W, C, G = 3, 64, 64, 256, 32
-    x, sh, xs, gamma, beta, dy, got = check(L, rng, (B, H, W, C, G), SILU, True)
+    x, sh, xs, gamma, beta, dy, got = check(L, rng, (B, H, W, C, G), SILU, True, True)
     xs_o = orc.spatial_add(x, sh)
     assert_bits_equal(xs_o, xs, "oracle spatial_add vs float32 x + shift")
     y_ref, mu_ref, rs_ref = orc.groupnorm_forward(xs_o, gamma, beta, G, 1e-5, SILU)
