@@ -266,14 +266,73 @@ __device__ __forceinline__ void publish_epoch(const Work& wk, unsigned epoch) {
     __hip_atomic_store(wk.ep, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Lanes that share this lane's group inside a wave: xor over the column bits
-// inside the group and over the row bits of the wave.
+// One level of an xor reduction tree without LDS traffic: this lane's value
+// and its partner's at lane distance O, as (lo, hi).  Every merge below is
+// symmetric in its two operands (a + b, and Chan's equal-count merge), so
+// both lanes of a pair compute the same bits, exactly as with __shfl_xor.
+//   O = 1, 2: DPP quad permutes (the xor partner itself);
+//   O = 4, 8: DPP mirrors within 8 and 16 lanes; the mirrored lane holds the
+//     xor partner's value because the tree has already made every aligned
+//     group of O lanes uniform (the levels below O run first);
+//   O = 16, 32: the row swaps v_permlane16/32_swap (lo = the lower lane's value).
+template <int O>
+__device__ __forceinline__ void xpair(float v, float& lo, float& hi) {
+    static_assert(O == 1 || O == 2 || O == 4 || O == 8 || O == 16 || O == 32, "xor distance");
+    if constexpr (O <= 8) {
+        constexpr int ctl = O == 1 ? 0xB1 : O == 2 ? 0x4E : O == 4 ? 0x141 : 0x140;
+        lo = v;
+        hi = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), ctl, 0xF, 0xF, false));
+    } else if constexpr (O == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        lo = __uint_as_float(r[0]);
+        hi = __uint_as_float(r[1]);
+    } else {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        lo = __uint_as_float(r[0]);
+        hi = __uint_as_float(r[1]);
+    }
+}
+template <int O>
+using xlevel = std::integral_constant<int, O>;
+
+// The levels 1, 2, 4, ... n/2 of a tree over aligned groups of n lanes (n a
+// power of two <= 64, uniform over the wave), smallest first: f(xlevel<O>).
+template <class F>
+__device__ __forceinline__ void for_xor_levels(int n, F f) {
+    if (n > 1) f(xlevel<1>{});
+    if (n > 2) f(xlevel<2>{});
+    if (n > 4) f(xlevel<4>{});
+    if (n > 8) f(xlevel<8>{});
+    if (n > 16) f(xlevel<16>{});
+    if (n > 32) f(xlevel<32>{});
+}
+
+// Lanes that share this lane's group inside a wave: the column bits inside
+// the group (levels 1 .. CPG4 / 2), then the row bits of the wave (CW4 .. 32).
 template <class Gm, class F>
 __device__ __forceinline__ void for_group_xor(F f) {
-#pragma unroll
-    for (int o = 1; o < Gm::CPG4; o <<= 1) f(o);
-#pragma unroll
-    for (int o = Gm::CW4; o < kWave; o <<= 1) f(o);
+    static_assert(Gm::CW4 == 16 || Gm::CW4 == 32, "row levels of the group tree");
+    if constexpr (Gm::CPG4 > 1) f(xlevel<1>{});
+    if constexpr (Gm::CPG4 > 2) f(xlevel<2>{});
+    if constexpr (Gm::CW4 <= 16) f(xlevel<16>{});
+    f(xlevel<32>{});
+}
+
+// a + (the partner's a) for each of the values, at one tree level
+template <int O>
+__device__ __forceinline__ void xsum(float& a) {
+    float lo, hi;
+    xpair<O>(a, lo, hi);
+    a = lo + hi;
+}
+template <int O>
+__device__ __forceinline__ void xmerge_eq(float& m, float& q, float c) {
+    float ml, mh, ql, qh;
+    xpair<O>(m, ml, mh);
+    xpair<O>(q, ql, qh);
+    m = ml;
+    q = ql;
+    chan_merge_eq(m, q, mh, qh, c);
 }
 
 // Slot of wave w's partial pair of group g in the per-tile exchange
@@ -396,8 +455,8 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
             q += (a * a + bb * bb) + (c * c + d * d);
         }
         float cnt = nthr;
-        for_group_xor<Gm>([&](int o) {
-            chan_merge_eq(m, q, __shfl_xor(m, o, kWave), __shfl_xor(q, o, kWave), cnt);
+        for_group_xor<Gm>([&](auto o) {
+            xmerge_eq<decltype(o)::value>(m, q, cnt);
             cnt *= 2.0f;
         });
         if (lane % CW4 % Gm::CPG4 == 0 && lane < CW4) wred[pb][gl][wave_slot<Gm>(gl, wid)] = make_float2(m, q);
@@ -405,16 +464,15 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
         // the NW wave partials of group g merge on lanes (g, i = 0..NW-1) of
         // one wave in a fixed xor tree (the merge is symmetric, so every lane
         // of the pair holds the same value)
-        static_assert(kWave % NW == 0, "a group's wave partials share a wave");
-        if (tid < GT * NW) {
+        static_assert(kWave % NW == 0 && GT * NW % kWave == 0, "a group's wave partials share a wave");
+        if (tid < GT * NW) {  // whole waves: GT * NW is a multiple of 64
             const int g = tid / NW, i = tid % NW;
             const float2 pq = wred[pb][g][wave_slot<Gm>(g, i)];
             float mm = pq.x, qq = pq.y;
-#pragma unroll
-            for (int o = 1; o < NW; o <<= 1) {
-                chan_merge_eq(mm, qq, __shfl_xor(mm, o, kWave), __shfl_xor(qq, o, kWave), cnt);
+            for_xor_levels(NW, [&](auto o) {
+                xmerge_eq<decltype(o)::value>(mm, qq, cnt);
                 cnt *= 2.0f;
-            }
+            });
             if (i == 0) {
                 unsigned long long* r = rec_slot(j, g, t);
                 rec_store(r, tagged(tag, mm));
@@ -439,29 +497,30 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
         const int b = b0 + j * spr;
         settle(r0);
         settle(r1);
+        // lane rj merges records rj, rj+LPG, ... of group rg in tile order,
+        // then the group's LPG lanes a fixed xor tree (run by every lane, in
+        // uniform control flow; lanes past the mergers carry zeros)
+        const float ntile = (float)(Gm::TP * Gm::CPG4 * 4);
+        float n = ntile, m = 0.0f, q = 0.0f;
         if (merger) {
-            // lane rj merges records rj, rj+LPG, ... of group rg in tile order, then a fixed xor tree
-            const float ntile = (float)(Gm::TP * Gm::CPG4 * 4);
-            float n = 0.0f, m = 0.0f, q = 0.0f;
 #pragma unroll
             for (int u = 0; u < RPL; ++u) {
                 const unsigned long long* p = rec_slot(j, rg, rj + u * LPG);
                 const float mj = rec_wait(p, r0[u], epoch, spin_limit, wf);
                 const float qj = rec_wait(p + T, r1[u], epoch, spin_limit, wf);
                 if (u == 0) {
-                    n = ntile;
                     m = mj;
                     q = qj;
                 } else {
                     chan_merge(n, m, q, ntile, mj, qj);
                 }
             }
-            for (int o = 1; o < LPG; o <<= 1) {
-                chan_merge_eq(m, q, __shfl_xor(m, o, kWave), __shfl_xor(q, o, kWave), n);
-                n *= 2.0f;
-            }
-            if (rj == 0) stat[pb][rg] = make_float2(m, rsqrtf(q / n + eps));
         }
+        for_xor_levels(LPG, [&](auto o) {
+            xmerge_eq<decltype(o)::value>(m, q, n);
+            n *= 2.0f;
+        });
+        if (merger && rj == 0) stat[pb][rg] = make_float2(m, rsqrtf(q / n + eps));
         lds_barrier();
         const float2 st = stat[pb][gl];
         const float mean = st.x, rs = st.y;
@@ -770,23 +829,22 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
         }
         float s1 = (s1v.x + s1v.y) + (s1v.z + s1v.w);
         float s2 = (s2v.x + s2v.y) + (s2v.z + s2v.w);
-        for_group_xor<Gm>([&](int o) {
-            s1 += __shfl_xor(s1, o, kWave);
-            s2 += __shfl_xor(s2, o, kWave);
+        for_group_xor<Gm>([&](auto o) {
+            xsum<decltype(o)::value>(s1);
+            xsum<decltype(o)::value>(s2);
         });
         if (lane % CW4 % Gm::CPG4 == 0 && lane < CW4) wred[pb][gl][wave_slot<Gm>(gl, wid)] = make_float2(s1, s2);
         lds_barrier();
         // wave partials of group g summed on lanes (g, i) in a fixed xor tree
-        static_assert(kWave % NW == 0, "a group's wave partials share a wave");
-        if (tid < GT * NW) {
+        static_assert(kWave % NW == 0 && GT * NW % kWave == 0, "a group's wave partials share a wave");
+        if (tid < GT * NW) {  // whole waves: GT * NW is a multiple of 64
             const int g = tid / NW, i = tid % NW;
             const float2 ac = wred[pb][g][wave_slot<Gm>(g, i)];
             float a = ac.x, c = ac.y;
-#pragma unroll
-            for (int o = 1; o < NW; o <<= 1) {
-                a += __shfl_xor(a, o, kWave);
-                c += __shfl_xor(c, o, kWave);
-            }
+            for_xor_levels(NW, [&](auto o) {
+                xsum<decltype(o)::value>(a);
+                xsum<decltype(o)::value>(c);
+            });
             if (i == 0) {
                 unsigned long long* r = rec_slot(j, g, t);
                 rec_store(r, tagged(tag, a));
@@ -813,20 +871,23 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
         const int b = b0 + j * spr;
         settle(r0);
         settle(r1);
+        // the group's LPG merging lanes add its records, then a fixed xor
+        // tree (run by every lane, in uniform control flow; lanes past the
+        // mergers carry zeros)
+        float a = 0.0f, c = 0.0f;
         if (merger) {
-            float a = 0.0f, c = 0.0f;
 #pragma unroll
             for (int u = 0; u < RPL; ++u) {
                 const unsigned long long* p = rec_slot(j, rg, rj + u * LPG);
                 a += rec_wait(p, r0[u], epoch, spin_limit, wf);
                 c += rec_wait(p + T, r1[u], epoch, spin_limit, wf);
             }
-            for (int o = 1; o < LPG; o <<= 1) {
-                a += __shfl_xor(a, o, kWave);
-                c += __shfl_xor(c, o, kWave);
-            }
-            if (rj == 0) stat[pb][rg] = make_float2(a * sh.inv_n, c * sh.inv_n);
         }
+        for_xor_levels(LPG, [&](auto o) {
+            xsum<decltype(o)::value>(a);
+            xsum<decltype(o)::value>(c);
+        });
+        if (merger && rj == 0) stat[pb][rg] = make_float2(a * sh.inv_n, c * sh.inv_n);
         lds_barrier();
         // dx = rs * ((g - m1) - xhat * m2) = g * rs + (xhat * (-rs m2) + (-rs m1))
         const float2 st = stat[pb][gl];
@@ -852,13 +913,11 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
         }
         if constexpr (SHIFT) {
             // this wave's rows of the tile, in a fixed xor tree over the row lanes
-#pragma unroll
-            for (int o = CW4; o < kWave; o <<= 1) {
-                cs.x += __shfl_xor(cs.x, o, kWave);
-                cs.y += __shfl_xor(cs.y, o, kWave);
-                cs.z += __shfl_xor(cs.z, o, kWave);
-                cs.w += __shfl_xor(cs.w, o, kWave);
-            }
+            static_assert(CW4 == 32, "one row level");
+            xsum<32>(cs.x);
+            xsum<32>(cs.y);
+            xsum<32>(cs.z);
+            xsum<32>(cs.w);
             if (lane < CW4) csum[pb][wid][lane] = cs;
         }
     };
@@ -964,10 +1023,7 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
     // same 4 channels; sum over the wave's rows, then over the waves in order.
     float c8[8] = {cg.x, cg.y, cg.z, cg.w, cbs.x, cbs.y, cbs.z, cbs.w};
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-#pragma unroll
-        for (int o = CW4; o < kWave; o <<= 1) c8[j] += __shfl_xor(c8[j], o, kWave);
-    }
+    for (int j = 0; j < 8; ++j) xsum<32>(c8[j]);
     if (lane < CW4) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) cred[wid][lane][j] = c8[j];
