@@ -373,6 +373,9 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
     __shared__ float2 wred[2][GT][NW];          // [parity][group][wave slot] (mean, M2)
     __shared__ float2 stat[2][GT];              // (mean, rstd)
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
+    // the wave index as a scalar: the direct-to-LDS loads take their LDS
+    // address from a scalar register (M0), computed once per address
+    const int wid_s = __builtin_amdgcn_readfirstlane(wid);
     const int col = lane % CW4, row0 = wid * Gm::RW + lane / CW4;
     const int gl = col / Gm::CPG4;              // group of this lane within the tile
     const int P = gridDim.x, w = blockIdx.x;
@@ -409,6 +412,13 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
     // Record layout [unit][group][value][pixel tile]: the mergers of a group
     // read consecutive tiles, i.e. contiguous records.
     auto rec_slot = [&](int j, int g, int tt) { return wk.rec + ((size_t)((u0 + j * upr) * GT + g) * 2) * T + tt; };
+    // The same addresses as per-lane bases plus a uniform step per round, so
+    // the tile loop adds one scalar offset instead of redoing the index
+    // arithmetic: the merging lane's first record (group rg, or GT - 1 past
+    // the mergers; tile rj) and the group leader's own (group tid / NW; tile t).
+    const size_t rec_round = (size_t)upr * GT * 2 * T;
+    const unsigned long long* const rec_m = rec_slot(0, merger ? rg : GT - 1, rj);
+    unsigned long long* const rec_s = rec_slot(0, tid / NW < GT ? tid / NW : GT - 1, t);
     // With SHIFT the input is x + shift[b, c]: the 128 shift values of a
     // tile's sample and column block go into slot j % 4 of a small LDS ring
     // with one direct-to-LDS load per wave, issued just before the tile's own
@@ -436,7 +446,7 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
         issue_shift(j);
 #pragma unroll
         for (int k = 0; k < NV; ++k)
-            dma16<NT>(r, &stage[sb][k * TPB + wid * kWave], voff, base + (uint32_t)(k * Gm::RSTEP) * row_bytes);
+            dma16<NT>(r, &stage[sb][k * TPB + wid_s * kWave], voff, base + (uint32_t)(k * Gm::RSTEP) * row_bytes);
     };
     auto take = [&](float4 (&v)[NV], int j) {
         if constexpr (SHIFT)
@@ -474,7 +484,7 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
                 cnt *= 2.0f;
             });
             if (i == 0) {
-                unsigned long long* r = rec_slot(j, g, t);
+                unsigned long long* r = rec_s + (size_t)j * rec_round;
                 rec_store(r, tagged(tag, mm));
                 rec_store(r + T, tagged(tag, qq));
             }
@@ -485,10 +495,9 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
     // record waits.
     unsigned long long r0[RPL] = {}, r1[RPL] = {};
     auto records_prefetch = [&](int j) {
-        const int rgc = merger ? rg : GT - 1;
 #pragma unroll
         for (int u = 0; u < RPL; ++u) {
-            const unsigned long long* p = rec_slot(j, rgc, rj + u * LPG);
+            const unsigned long long* p = rec_m + (size_t)j * rec_round + u * LPG;
             r0[u] = rec_load(p);
             r1[u] = rec_load(p + T);
         }
@@ -505,7 +514,7 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
         if (merger) {
 #pragma unroll
             for (int u = 0; u < RPL; ++u) {
-                const unsigned long long* p = rec_slot(j, rg, rj + u * LPG);
+                const unsigned long long* p = rec_m + (size_t)j * rec_round + u * LPG;
                 const float mj = rec_wait(p, r0[u], epoch, spin_limit, wf);
                 const float qj = rec_wait(p + T, r1[u], epoch, spin_limit, wf);
                 if (u == 0) {
@@ -672,6 +681,9 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
     float4 (*csum)[NW][CW4] = reinterpret_cast<float4 (*)[NW][CW4]>(&cred[0][0][0]);
     static_assert(sizeof(float4) * 2 * NW * CW4 <= sizeof(cred), "column sums fit the reduction buffer");
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
+    // the wave index as a scalar: the direct-to-LDS loads take their LDS
+    // address from a scalar register (M0), computed once per address
+    const int wid_s = __builtin_amdgcn_readfirstlane(wid);
     const int col = lane % CW4, row0 = wid * Gm::RW + lane / CW4;
     const int gl = col / Gm::CPG4;
     const int P = gridDim.x, w = blockIdx.x;
@@ -719,6 +731,13 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
     // Record layout [unit][group][value][pixel tile]: the mergers of a group
     // read consecutive tiles, i.e. contiguous records.
     auto rec_slot = [&](int j, int g, int tt) { return wk.rec + ((size_t)((u0 + j * upr) * GT + g) * 2) * T + tt; };
+    // The same addresses as per-lane bases plus a uniform step per round, so
+    // the tile loop adds one scalar offset instead of redoing the index
+    // arithmetic: the merging lane's first record (group rg, or GT - 1 past
+    // the mergers; tile rj) and the group leader's own (group tid / NW; tile t).
+    const size_t rec_round = (size_t)upr * GT * 2 * T;
+    const unsigned long long* const rec_m = rec_slot(0, merger ? rg : GT - 1, rj);
+    unsigned long long* const rec_s = rec_slot(0, tid / NW < GT ? tid / NW : GT - 1, t);
     // The x and dy loads of round j's tile into stage buffer sb (2 NV).  A
     // tile past the end is issued against an empty buffer range: the loads
     // read nothing and only keep the operation count of every round the same.
@@ -742,10 +761,10 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
         issue_shift(j);
 #pragma unroll
         for (int k = 0; k < NV; ++k)
-            dma16<NT>(rx, &stage[sb][k * TPB + wid * kWave], voff, base + (uint32_t)(k * Gm::RSTEP) * row_bytes);
+            dma16<NT>(rx, &stage[sb][k * TPB + wid_s * kWave], voff, base + (uint32_t)(k * Gm::RSTEP) * row_bytes);
 #pragma unroll
         for (int k = 0; k < NV; ++k)
-            dma16<NT>(rd, &stage[sb][(NV + k) * TPB + wid * kWave], voff,
+            dma16<NT>(rd, &stage[sb][(NV + k) * TPB + wid_s * kWave], voff,
                 base + (uint32_t)(k * Gm::RSTEP) * row_bytes);
     };
     auto take = [&](float4 (&v)[2 * NV], int j) {
@@ -846,7 +865,7 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
                 xsum<decltype(o)::value>(c);
             });
             if (i == 0) {
-                unsigned long long* r = rec_slot(j, g, t);
+                unsigned long long* r = rec_s + (size_t)j * rec_round;
                 rec_store(r, tagged(tag, a));
                 rec_store(r + T, tagged(tag, c));
             }
@@ -857,10 +876,9 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
     // record waits.
     unsigned long long r0[RPL] = {}, r1[RPL] = {};
     auto records_prefetch = [&](int j) {
-        const int rgc = merger ? rg : GT - 1;
 #pragma unroll
         for (int u = 0; u < RPL; ++u) {
-            const unsigned long long* p = rec_slot(j, rgc, rj + u * LPG);
+            const unsigned long long* p = rec_m + (size_t)j * rec_round + u * LPG;
             r0[u] = rec_load(p);
             r1[u] = rec_load(p + T);
         }
@@ -878,7 +896,7 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
         if (merger) {
 #pragma unroll
             for (int u = 0; u < RPL; ++u) {
-                const unsigned long long* p = rec_slot(j, rg, rj + u * LPG);
+                const unsigned long long* p = rec_m + (size_t)j * rec_round + u * LPG;
                 a += rec_wait(p, r0[u], epoch, spin_limit, wf);
                 c += rec_wait(p + T, r1[u], epoch, spin_limit, wf);
             }

@@ -57,21 +57,24 @@ __device__ __forceinline__ float pade_tanh_fast(float x) {
     return fmaxf(-1.0f, fminf(1.0f, p * __builtin_amdgcn_rcpf(q)));
 }
 
-// tanh(z / 2), fast form: with w = z^2 = 4 (z/2)^2 the half-argument scaling
-// is folded into the coefficients.  Every coefficient and every intermediate
-// differs from the (z/2)-form by a power of two, so the values are identical
-// to pade_tanh_fast(z * 0.5f); one multiply fewer.
-__device__ __forceinline__ float pade_tanh_half_fast(float z) {
-    const float w = z * z;
-    const float p = z * fmaf(w, fmaf(w, fmaf(w, 0.0078125f, 11.8125f), 2165.625f), 67567.5f);
-    const float q = fmaf(w, fmaf(w, fmaf(w, 0.4375f, 196.875f), 15592.5f), 135135.0f);
-    return fmaxf(-1.0f, fminf(1.0f, p * __builtin_amdgcn_rcpf(q)));
-}
-
 template <bool FAST>
 __device__ __forceinline__ float pade_tanh(float x) {
     if constexpr (FAST) return pade_tanh_fast(x);
     else return pade_tanh_exact(x);
+}
+
+// sigmoid(z) = (tanh(z / 2) + 1) / 2 with the Pade tanh above, fast form.
+// Substituting x = z / 2 (w = z^2 = 4 x^2) and halving the numerator scales
+// every coefficient by a power of two (exact in float), so p / q = tanh(z/2) / 2;
+// the + 1/2 is the addend of the multiply-add with the reciprocal, and the
+// clamp of tanh to [-1, 1] becomes a clamp of the sigmoid to [0, 1], upper
+// bound first as in the reference (a NaN quotient, for |z| beyond ~3e6,
+// gives 1).  Within an ulp of halving the clamped tanh.
+__device__ __forceinline__ float pade_sigmoid_fast(float z) {
+    const float w = z * z;
+    const float p = z * fmaf(w, fmaf(w, fmaf(w, 0.00390625f, 5.90625f), 1082.8125f), 33783.75f);
+    const float q = fmaf(w, fmaf(w, fmaf(w, 0.4375f, 196.875f), 15592.5f), 135135.0f);
+    return fmaxf(0.0f, fminf(1.0f, fmaf(p, __builtin_amdgcn_rcpf(q), 0.5f)));
 }
 
 template <bool FAST>
@@ -79,7 +82,7 @@ __device__ __forceinline__ float pade_sigmoid(float x) {
     // pade_tanh is clamped to [-1, 1], so (t + 1) * 0.5 already lies in [0, 1]:
     // the reference's outer clamp (kernels.cu:16) never changes the value and
     // is not evaluated.
-    if constexpr (FAST) return fmaf(pade_tanh_half_fast(x), 0.5f, 0.5f);
+    if constexpr (FAST) return pade_sigmoid_fast(x);
     else return (pade_tanh_exact(x * 0.5f) + 1.0f) * 0.5f;
 }
 
