@@ -120,6 +120,8 @@ STREAM_SHAPES = [
     ((4, 32, 32, 128, 32), False, True),   # cpg 4: forward composed, backward streamed
     ((1, 64, 128, 256, 32), True, False),  # backward merges 2 records per lane: composed
     ((1, 128, 128, 128, 8), True, False),  # forward merges 2 records per lane; backward too large
+    ((1, 8, 16, 128, 16), True, True),     # one forward tile, two backward tiles per sample
+    ((3, 8, 16, 128, 16), True, True),
 ]
 
 

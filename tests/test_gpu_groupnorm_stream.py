@@ -36,6 +36,9 @@ SHAPES = [
     (1, 128, 128, 128, 8),   # cpg 16: forward merges 2 records per lane; backward too large
     (1, 64, 128, 128, 32),   # cpg 4: forward merges 2 records per lane; backward too large -> register/generic
     (1, 128, 128, 128, 32),  # cpg 4: neither direction fits the streaming plan
+    (1, 8, 16, 128, 16),     # one forward tile and two backward tiles per sample
+    (2, 8, 16, 128, 16),     # the same, two samples
+    (1, 8, 8, 128, 16),      # one backward tile; the forward does not stream
 ]
 
 
