@@ -244,6 +244,21 @@ RedPlan red_plan(int B, int HW, int C, bool vec) {
 
 size_t red_workspace(const RedPlan& p, int B, int C) { return p.S > 1 ? (size_t)B * p.S * C : 0; }
 
+// An upper bound of b * S over every batch b <= B (S = the plan's segments):
+// S <= ceil(2048 / b) and S <= smax, so b S <= min(b smax, 2047 + b), which
+// grows with b.  (b S itself does not: 102 ceil(2048 / 102) = 2142 >
+// 103 ceil(2048 / 103) = 2060.)  A workspace sized with it for a batch
+// therefore serves every smaller batch of the same HW and C.
+long long red_rows_bound(int B, int HW, int C, bool vec) {
+    const int CU = C / (vec ? 4 : 1);
+    int CL = 1;
+    while (CL * 2 <= CU && CL * 2 <= 64) CL *= 2;
+    const long long RP = kTpb / CL;
+    const long long smax = (HW + 8 * RP - 1) / (8 * RP);
+    const long long a = (long long)B * (smax > 1 ? smax : 1), c = 2047LL + B;
+    return a < c ? a : c;
+}
+
 // Reductions: out[b, c] = sum over HW of (x) [kRedSum] or of (g2 x) with
 // gin = g2 (cond + 1) [kRedModBwd].  ws: caller workspace or null (scratch).
 template <int MODE>
@@ -343,10 +358,12 @@ void launch_spatial_reduce_sum_ws(float* out, const float* in, int batch, int HW
 
 size_t nnhip_spatial_reduce_workspace(int batch, int HW, int C) {
     if (batch <= 0 || HW <= 0 || C <= 0) return 0;
-    // the larger of the two layouts (vector and scalar), so one size serves both
-    const RedPlan pv = red_plan(batch, HW, C, true), ps = red_plan(batch, HW, C, false);
-    const size_t a = red_workspace(pv, batch, C), b = red_workspace(ps, batch, C);
-    return a > b ? a : b;
+    // Both layouts (vector and scalar) and every batch up to `batch` (callers
+    // size the workspace for their largest batch).  A bound of `batch` rows
+    // means one segment per sample at every batch: no workspace.
+    const long long rv = red_rows_bound(batch, HW, C, true), rs = red_rows_bound(batch, HW, C, false);
+    const long long rows = rv > rs ? rv : rs;
+    return rows <= batch ? 0 : (size_t)rows * C;
 }
 
 }  // extern "C"

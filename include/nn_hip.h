@@ -226,7 +226,7 @@ void launch_spatial_modulate_act_forward(float* out, const float* in, const floa
    grad_cond[b,c] = sum over hw of g2 * in.  Replaces the pair
    launch_activation_backward + launch_spatial_modulate_backward
    (src/cond_conv_residual.c:46-49).  `workspace` (may be NULL: library scratch)
-   holds nnhip_spatial_reduce_workspace(batch, H*W, C) floats. */
+   holds nnhip_spatial_reduce_workspace(b, H*W, C) floats for some b >= batch. */
 void launch_spatial_modulate_act_backward(float* grad_in, float* grad_cond,
     const float* grad_out, const float* in, const float* cond,
     int batch, int H, int W, int C, Activation act, float* workspace, hipStream_t s);
@@ -268,6 +268,8 @@ void launch_transpose(float* out, const float* in, int rows, int cols, hipStream
 /* launch_spatial_reduce_sum with a lent workspace (may be NULL). */
 void launch_spatial_reduce_sum_ws(float* out, const float* in, int batch, int HW, int C,
     float* workspace, hipStream_t s);
+/* Floats of workspace for the two launchers above, enough for every batch up
+   to `batch` at the same HW and C (0 when none needs one). */
 size_t nnhip_spatial_reduce_workspace(int batch, int HW, int C);
 
 /* y = act(GroupNorm(x)) in one HBM pass over x.  Replaces the caller sequence

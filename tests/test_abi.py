@@ -144,3 +144,21 @@ def test_zero_sized_calls_are_no_ops(nn):
     L.launch_mp_fourier(null, null, null, null, 0, 16, None)
     L.launch_im2col(null, null, 0, 4, 4, 2, 3, 1, 1, 4, 4, None)
     assert L.last_error()[0] == 0
+
+
+@pytest.mark.parametrize("hw,c", [(2048, 128), (1024, 128), (4096, 256), (49, 6), (5000, 3), (7, 192)])
+def test_spatial_workspace_grows_with_batch(nn, hw, c):
+    """A workspace sized for a batch must serve every smaller batch (the host
+    modules size theirs for the largest batch), so the reported size may never
+    fall as the batch grows; the segment count per sample alone does not give
+    that (b * ceil(2048 / b) is 2142 at b = 102 and 2060 at b = 103)."""
+    L = nn.lib()
+    sizes = [L.nnhip_spatial_reduce_workspace(b, hw, c) for b in range(1, 300)]
+    assert all(a <= b for a, b in zip(sizes, sizes[1:])), sizes
+
+
+@pytest.mark.parametrize("c", [4, 48, 64, 256, 1000])
+def test_layernorm_workspace_grows_with_batch(nn, c):
+    L = nn.lib()
+    sizes = [L.nnhip_layernorm_backward_workspace(b, c) for b in list(range(1, 200)) + [4095, 4096, 4097, 65536]]
+    assert all(a <= b for a, b in zip(sizes, sizes[1:])), sizes

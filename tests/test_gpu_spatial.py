@@ -89,12 +89,64 @@ def test_spatial_modulate_act_fused(L, orc, rng, shape, act):
     assert_bits_equal(gin.download(shape=x.shape), gin_ref, "grad_in")
     g2 = orc.act_backward(g, orc.spatial_modulate(x, c), act)
     assert rel_err(gc.download(shape=(B, C)), gc_ref, floor=_sum_floor(g2 * x)) <= TOL
-    # a lent workspace gives the same bits as the library scratch
-    ws = L.alloc(max(1, L.nnhip_spatial_reduce_workspace(B, HW, C)))
-    gc2 = L.alloc(B * C)
-    L.launch_spatial_modulate_act_backward(gin.p, gc2.p, gd.p, xd.p, cd.p, B, HW, 1, C, act, ws.p, None)
+    # a lent workspace gives the same bits as the library scratch, also reused
+    ws = _zeroed(L, L.nnhip_spatial_reduce_workspace(B, HW, C))
+    for rep in range(2):
+        gin2, gc2 = L.alloc(x.size), L.alloc(B * C)
+        L.launch_spatial_modulate_act_backward(gin2.p, gc2.p, gd.p, xd.p, cd.p, B, HW, 1, C, act, ws.p, None)
+        L.sync()
+        assert_bits_equal(gc2.download(), gc.download(), f"grad_cond ws vs scratch, launch {rep}")
+        assert_bits_equal(gin2.download(), gin.download(), f"grad_in ws vs scratch, launch {rep}")
+
+
+def _zeroed(L, n):
+    a = L.alloc(max(1, n))
+    a.fill_bytes(0)
+    return a
+
+
+@pytest.mark.parametrize("shape", SHAPES + [(1, 64 * 64, 256), (40, 256, 64)], ids=lambda s: "x".join(map(str, s)))
+def test_spatial_reduce_sum_lent_workspace(L, orc, rng, shape):
+    """launch_spatial_reduce_sum_ws gives the pool path's sums bit for bit,
+    launch after launch on one workspace."""
+    B, HW, C = shape
+    print(f"[case] spatial reduce lent workspace {shape}", flush=True)
+    x, _, _ = _inputs(rng, B, HW, C)
+    xd, ref = L.to_device(x), L.alloc(B * C)
+    L.launch_spatial_reduce_sum(ref.p, xd.p, B, HW, C, None)
     L.sync()
-    assert_bits_equal(gc2.download(), gc.download(), "grad_cond ws vs scratch")
+    want = ref.download()
+    assert rel_err(want.reshape(B, C), orc.spatial_reduce_sum(x), floor=_sum_floor(x)) <= TOL
+    ws = _zeroed(L, L.nnhip_spatial_reduce_workspace(B, HW, C))
+    for rep in range(3):
+        out = L.alloc(B * C)
+        L.launch_spatial_reduce_sum_ws(out.p, xd.p, B, HW, C, ws.p, None)
+        L.sync()
+        assert_bits_equal(out.download(), want, f"launch {rep}")
+    assert L.last_error()[0] == 0
+
+
+def test_spatial_workspace_serves_smaller_batches(L, rng):
+    """A workspace sized for a batch serves every smaller batch: at HW = 2048,
+    C = 128 a batch of 102 takes 102 x 21 segment rows, more than 103 x 20 at
+    the batch of 103 the workspace was sized for.  Sentinels past the end stay
+    untouched and the sums match the pool path bit for bit."""
+    print("[case] spatial workspace across batches", flush=True)
+    HW, C, Bmax = 2048, 128, 103
+    n_ws = L.nnhip_spatial_reduce_workspace(Bmax, HW, C)
+    guard = 4096
+    ws = L.alloc(n_ws + guard)
+    ws.upload(np.concatenate([np.zeros(n_ws, np.float32), np.full(guard, 7.25, np.float32)]))
+    x, c, g = _inputs(rng, Bmax, HW, C)
+    xd, cd, gd = L.to_device(x), L.to_device(c), L.to_device(g)
+    for B in (Bmax, 102, 1, 102):
+        gin_r, gc_r, gin_w, gc_w = L.alloc(B * HW * C), L.alloc(B * C), L.alloc(B * HW * C), L.alloc(B * C)
+        L.launch_spatial_modulate_act_backward(gin_r.p, gc_r.p, gd.p, xd.p, cd.p, B, HW, 1, C, 5, None, None)
+        L.launch_spatial_modulate_act_backward(gin_w.p, gc_w.p, gd.p, xd.p, cd.p, B, HW, 1, C, 5, ws.p, None)
+        L.sync()
+        assert_bits_equal(gc_w.download(), gc_r.download(), f"grad_cond B={B}")
+        assert_bits_equal(gin_w.download(), gin_r.download(), f"grad_in B={B}")
+    assert np.all(ws.download()[n_ws:] == np.float32(7.25)), "wrote past the workspace"
 
 
 def test_spatial_misaligned_pointers_take_the_scalar_path(L, orc, rng):
