@@ -22,8 +22,17 @@ __global__ __launch_bounds__(256) void gns_colsum(float* __restrict__ gshift, co
     const int b = i / C, c = i % C;
     const int cb = c / CHW, cl = c % CHW;
     const float* p = colpart + ((size_t)(b * (C / CHW) + cb) * T) * CHW + cl;
+    // kB tiles in flight (predicated at the end), added in tile order
+    constexpr int kB = 16;
     float a = 0.0f;
-    for (int t = 0; t < T; ++t) a += p[(size_t)t * CHW];
+    for (int t = 0; t < T; t += kB) {
+        float v[kB];
+#pragma unroll
+        for (int u = 0; u < kB; ++u) v[u] = t + u < T ? p[(size_t)(t + u) * CHW] : 0.0f;
+#pragma unroll
+        for (int u = 0; u < kB; ++u)
+            if (t + u < T) a += v[u];
+    }
     gshift[i] = a;
 }
 

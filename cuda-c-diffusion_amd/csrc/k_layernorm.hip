@@ -335,25 +335,24 @@ __global__ __launch_bounds__(kTpb) void ln_colsum2(float* __restrict__ og, float
     const int c = blockIdx.x * kWave + lane;
     float sg = 0.0f, sb = 0.0f;
     if (c < C) {
-        // kB rows of each in flight, added in row order
+        // kB rows of each in flight (a short last batch too: its loads are
+        // predicated, not left to a loop of one load each), added in row order
         constexpr int kB = 8;
-        int p = wid;
-        for (; p + (kB - 1) * kNw < P; p += kB * kNw) {
+        for (int p = wid; p < P; p += kB * kNw) {
             float vg[kB], vb[kB];
 #pragma unroll
             for (int u = 0; u < kB; ++u) {
-                vg[u] = pg[(size_t)(p + u * kNw) * C + c];
-                vb[u] = pb[(size_t)(p + u * kNw) * C + c];
+                const bool in = p + u * kNw < P;
+                vg[u] = in ? pg[(size_t)(p + u * kNw) * C + c] : 0.0f;
+                vb[u] = in ? pb[(size_t)(p + u * kNw) * C + c] : 0.0f;
             }
 #pragma unroll
             for (int u = 0; u < kB; ++u) {
-                sg += vg[u];
-                sb += vb[u];
+                if (p + u * kNw < P) {
+                    sg += vg[u];
+                    sb += vb[u];
+                }
             }
-        }
-        for (; p < P; p += kNw) {
-            sg += pg[(size_t)p * C + c];
-            sb += pb[(size_t)p * C + c];
         }
     }
     lg[wid][lane] = sg;

@@ -163,18 +163,18 @@ __global__ __launch_bounds__(kTpb) void spatial_segments_sum(float* __restrict__
     if (i >= (long long)B * C) return;
     const long long b = i / C, c = i % C;
     const float* p = part + b * S * C + c;
-    // kB segments in flight, added in segment order
-    constexpr int kB = 8;
-    float t = p[0];
-    int s = 1;
-    for (; s + kB <= S; s += kB) {
+    // kB segments in flight (a short last batch too: predicated loads, not a
+    // loop of one load each), added in segment order from the first
+    constexpr int kB = 16;
+    float t = 0.0f;
+    for (int s = 0; s < S; s += kB) {
         float v[kB];
 #pragma unroll
-        for (int u = 0; u < kB; ++u) v[u] = p[(size_t)(s + u) * C];
+        for (int u = 0; u < kB; ++u) v[u] = s + u < S ? p[(size_t)(s + u) * C] : 0.0f;
 #pragma unroll
-        for (int u = 0; u < kB; ++u) t += v[u];
+        for (int u = 0; u < kB; ++u)
+            if (s + u < S) t = s + u == 0 ? v[0] : t + v[u];
     }
-    for (; s < S; ++s) t += p[(size_t)s * C];
     out[i] = t;
 }
 
