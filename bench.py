@@ -494,6 +494,48 @@ def run_suite(L, nn, reps, with_cpu=True):
     _row("spatial_reduce_sum", "DDPM block [256,64,64,256] -> [256,256]",
          T.median_us(lambda: L.launch_spatial_reduce_sum(gemb.p, xa.p, 256, 64 * 64, 256, stream), max(5, reps // 4)),
          4 * n4, cpu=cpu(lambda: orc.spatial_reduce_sum(h16), 16.0, "16 of 256 samples x 16, 1 thread"))
+    # the DDPM block's GN2 with the embedding add and its gradient's pixel sum
+    # folded in (src/conv_residual.c:33-37, 51-55), against the same work as
+    # separate launches (spatial_add in place, then GN2; GN2 backward, then
+    # spatial_reduce_sum)
+    Bs, HWs, Cs, Gs = 256, 64 * 64, 256, 32
+    gms = dev(1 + 0.1 * rng.standard_normal(Cs))
+    bts = dev(0.1 * rng.standard_normal(Cs))
+    mus, rss, ggs, gbs = L.alloc(Bs * Gs), L.alloc(Bs * Gs), L.alloc(Cs), L.alloc(Cs)
+    fws = L.alloc(max(1, L.nnhip_groupnorm_forward_workspace(Bs, HWs, Cs, Gs)))
+    bws = L.alloc(max(1, L.nnhip_groupnorm_shift_backward_workspace(Bs, HWs, Cs, Gs)))
+    fws.fill_bytes(0)
+    bws.fill_bytes(0)
+    rs_reps = max(5, reps // 4)
+    _row("gn_silu_shift_fwd", "DDPM block GN2 [256,64,64,256] G32, + emb[256,256] fused",
+         T.median_us(lambda: L.launch_groupnorm_act_shift_forward_ws(ya.p, mus.p, rss.p, xa.p, emb.p, gms.p, bts.p, Bs,
+                                                                     HWs, Cs, Gs, 1e-5, 3, fws.p, stream), rs_reps),
+         8 * n4)
+
+    L.nnhip_copy_f32(ga.p, xa.p, n4, stream)  # the reference adds in place: a copy of x to add into
+
+    def shift_fwd_ref():
+        L.launch_spatial_add(ga.p, emb.p, Bs, 64, 64, Cs, stream)
+        L.launch_groupnorm_act_forward_ws(ya.p, mus.p, rss.p, ga.p, gms.p, bts.p, Bs, HWs, Cs, Gs, 1e-5, 3, fws.p,
+                                          stream)
+    _row("gn_silu_shift_fwd_ref", "DDPM block GN2, separate launches (spatial_add in place, then GN+SiLU)",
+         T.median_us(shift_fwd_ref, rs_reps), 8 * n4, "same algorithmic bytes as the fused row")
+    dys = ya  # any seeded gradient of the activated output
+    _row("gn_silu_shift_bwd", "DDPM block GN2 backward + pixel sum of dx, fused",
+         T.median_us(lambda: L.launch_groupnorm_act_shift_backward_ws(ga.p, gemb.p, ggs.p, gbs.p, dys.p, xa.p, emb.p,
+                                                                      gms.p, bts.p, mus.p, rss.p, Bs, HWs, Cs, Gs, 3,
+                                                                      bws.p, stream), rs_reps),
+         12 * n4)
+    rws = L.alloc(max(1, L.nnhip_spatial_reduce_workspace(Bs, HWs, Cs)))
+
+    def shift_bwd_ref():
+        L.launch_groupnorm_act_backward_ws(ga.p, ggs.p, gbs.p, dys.p, xa.p, gms.p, bts.p, mus.p, rss.p, Bs, HWs, Cs,
+                                           Gs, 3, bws.p, stream)
+        L.launch_spatial_reduce_sum_ws(gemb.p, ga.p, Bs, HWs, Cs, rws.p, stream)
+    _row("gn_silu_shift_bwd_ref", "DDPM block GN2 backward, separate launches (GN+SiLU backward, then spatial_reduce_sum)",
+         T.median_us(shift_bwd_ref, rs_reps), 12 * n4, "same algorithmic bytes as the fused row")
+    for ws_ in (fws, bws):
+        assert L.nnhip_groupnorm_workspace_status(ws_.p) == 0, "streaming GroupNorm wait timed out"
     del xa, ga, ya
 
     # cfg5: fused Adam + EMA over the DDPM-UNet-like list
@@ -557,6 +599,59 @@ def run_calibration(L, reps):
     L.dll.nnhip_stream_destroy(stream)
 
 
+SWEEP_BATCHES = (16, 32, 64, 128, 192, 256)
+
+
+def run_batch_sweep(L, reps):
+    """The north-star launches (GN(32)+SiLU forward and backward, lent
+    workspaces) and the plain SiLU streams of the same bytes
+    (launch_activation_forward/backward) at [B, 64, 64, 256] for several B,
+    with a least-squares line t(B) = slope * B + fixed per kernel: the slope is
+    the streaming rate once a launch runs, the intercept its fixed cost
+    (start-up, pipeline fill and drain, end-of-launch sums).  One JSON line per
+    batch, then one per kernel for the fit."""
+    HW, C, G = 4096, 256, 32
+    bmax = max(SWEEP_BATCHES)
+    n = bmax * HW * C
+    rng = np.random.default_rng(SEED)
+    xd = L.to_device(rng.standard_normal(n, dtype=np.float32))
+    dyd = L.to_device(rng.standard_normal(n, dtype=np.float32))
+    yd, dxd = L.alloc(n), L.alloc(n)
+    gd = L.to_device((1 + 0.1 * rng.standard_normal(C)).astype(np.float32))
+    bd = L.to_device((0.1 * rng.standard_normal(C)).astype(np.float32))
+    mu, rs, gg, gb = L.alloc(bmax * G), L.alloc(bmax * G), L.alloc(C), L.alloc(C)
+    stream = L.dll.nnhip_stream_create()
+    T = _Timer(L, stream)
+    rows = []
+    for B in SWEEP_BATCHES:
+        fws = L.alloc(max(1, L.nnhip_groupnorm_forward_workspace(B, HW, C, G)))
+        bws = L.alloc(max(1, L.nnhip_groupnorm_backward_workspace(B, HW, C, G)))
+        fws.fill_bytes(0)
+        bws.fill_bytes(0)
+        m = B * HW * C
+        t = {
+            "gns_fwd": T.median_us(lambda: L.launch_groupnorm_act_forward_ws(
+                yd.p, mu.p, rs.p, xd.p, gd.p, bd.p, B, HW, C, G, 1e-5, 3, fws.p, stream), reps),
+            "gns_bwd": T.median_us(lambda: L.launch_groupnorm_act_backward_ws(
+                dxd.p, gg.p, gb.p, dyd.p, xd.p, gd.p, bd.p, mu.p, rs.p, B, HW, C, G, 3, bws.p, stream), reps),
+            "act_fwd": T.median_us(lambda: L.launch_activation_forward(yd.p, xd.p, m, 3, stream), reps),
+            "act_bwd": T.median_us(lambda: L.launch_activation_backward(dxd.p, dyd.p, xd.p, m, 3, stream), reps),
+        }
+        assert L.nnhip_groupnorm_workspace_status(fws.p) == 0 and L.nnhip_groupnorm_workspace_status(bws.p) == 0
+        rows.append((B, t))
+        print(json.dumps({"batch": B, "us": {k: round(v, 2) for k, v in t.items()}}), flush=True)
+        fws.close()
+        bws.close()
+    bs = np.array([b for b, _ in rows], dtype=np.float64)
+    for k in ("gns_fwd", "gns_bwd", "act_fwd", "act_bwd"):
+        ts = np.array([t[k] for _, t in rows])
+        slope, fixed = np.polyfit(bs, ts, 1)
+        bytes_per_sample = (8 if k.endswith("fwd") else 12) * HW * C
+        print(json.dumps({"kernel": k, "us_per_sample": round(float(slope), 4), "fixed_us": round(float(fixed), 2),
+                          "slope_GB_s": round(bytes_per_sample / (slope * 1e-6) / 1e9, 1)}), flush=True)
+    L.dll.nnhip_stream_destroy(stream)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -569,6 +664,9 @@ def main() -> int:
                     help="time every hot-path row at its BASELINE config (one JSON line per row) instead")
     ap.add_argument("--calibrate", action="store_true",
                     help="run the 1 GiB -> 1 GiB calibration copy (for scaling rocprofv3 FETCH/WRITE_SIZE) instead")
+    ap.add_argument("--batch-sweep", action="store_true",
+                    help="time the north-star launches and the plain SiLU streams over batches and fit "
+                         "per-sample and fixed costs instead")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one GPU "
@@ -590,6 +688,10 @@ def main() -> int:
         return 0
     if args.calibrate:
         run_calibration(L, max(1, args.steps))
+        return 0
+    if args.batch_sweep:
+        log(f"[sweep] device {info}")
+        run_batch_sweep(L, max(5, args.steps))
         return 0
     B, H, W, C, G = args.batch, 64, 64, 256, 32
     HW = H * W
