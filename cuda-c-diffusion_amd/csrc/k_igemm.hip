@@ -255,14 +255,26 @@ __global__ __launch_bounds__(kTpb, 2) void igemm_fwd(float* __restrict__ Y, cons
 // workgroups per 128 x 128 output tile; split z writes its fixed-order partial
 // tile to part[z], and a second launch adds the S partials in split order.
 //
-// Per stage a workgroup stages 32 rows of A (its 128 k columns) and of dY
-// (its 128 n columns) in LDS as [32 m][32 float4 chunks], chunk index xor 8
-// on odd rows.  MFMA operands come straight from that layout: lane l reads
-// A[m = 2 p + l / 32][k = its row] and dY[m = 2 p + l / 32][n = its column],
-// so the two half-waves read different rows that the swizzle puts in
-// different bank halves.
+// Per stage a workgroup stages 32 pixel rows m of A (its 128 k columns) and
+// of dY (its BN n columns) in LDS transposed: per column, 8 float4 chunks of
+// 4 consecutive m (tslot).  A lane's MFMA operands then run along the pixel
+// reduction in one 128-bit read: in quad Q of the stage, lane l reads pixels
+// 8 Q + 4 (l / 32) .. + 3 of its column (k, or n, = l % 32 of a 32-column
+// block), and component c feeds the c-th MFMA, which pairs pixels 8 Q + c and
+// 8 Q + 4 + c of the two half-waves (any pairing gives the same sum, as long
+// as A and dY use the same one; this one is fixed).  Each loader thread
+// gathers 4 consecutive pixel rows of one 4-column chunk (one pixel decode,
+// then steps along the output row) and transposes them in registers into 4
+// chunk writes.
 // ---------------------------------------------------------------------------
 constexpr int kWgM = 32;  // m rows per stage
+
+// float4 slot of (column, chunk of 4 m) in a [columns][8] transposed tile.
+// The xor with (col ^ col / 8) mod 8 puts the 16 columns that a 16-lane group
+// reads (consecutive columns, one chunk) on 16 distinct bank quads, and the
+// columns 4 ch + i that a loader instruction writes (ch = 16 consecutive
+// lanes) on at most two lanes per quad.
+__device__ __forceinline__ int tslot(int col, int mc) { return col * 8 + (mc ^ ((col ^ (col >> 3)) & 7)); }
 
 // XCD-aware tile order.  Workgroups are dispatched round-robin over the
 // device's 8 XCDs (workgroup L on XCD L % 8), each with its own L2.  Tile
@@ -275,16 +287,15 @@ __device__ __forceinline__ int xcd_order(int L, int total) {
     return x * q + min(x, r) + j;
 }
 
-__device__ __forceinline__ int wslot(int m, int chunk) { return m * 32 + (chunk ^ ((m & 1) << 3)); }
-
 template <int BN>
 __global__ __launch_bounds__(kTpb, 2) void igemm_wgrad(float* __restrict__ part, const float* __restrict__ X,
     const float* __restrict__ dY, ConvShape sh, int rows_per_split) {
-    constexpr int UT = BN / 64;       // 32-column accumulator tiles per wave
-    constexpr int DCH = BN / 4;       // float4 chunks per dY row
-    constexpr int DQ = kWgM * DCH / kTpb;  // dY loads per thread
-    __shared__ float4 As[2][kWgM * 32];
-    __shared__ float4 Ds[2][kWgM * DCH];
+    constexpr int UT = BN / 64;               // 32-column accumulator tiles per wave
+    constexpr int DCH = BN / 4;               // float4 chunks per dY row
+    constexpr int DTHR = DCH * (kWgM / 4);    // dY loader threads: (n chunk, group of 4 rows)
+    static_assert(kWgM == 32 && DTHR <= kTpb && kTpb == 32 * (kWgM / 4), "loader roles");
+    __shared__ float4 As[2][128 * 8];
+    __shared__ float4 Ds[2][BN * 8];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int wk = w >> 1, wn = w & 1;
     // tile (k tile, n tile, split z), k tile fastest, in XCD-aware order
@@ -293,37 +304,54 @@ __global__ __launch_bounds__(kTpb, 2) void igemm_wgrad(float* __restrict__ part,
     const int k0 = (tl % KT) * 128, n0 = ((tl / KT) % NT) * BN, z = tl / (KT * NT);
     const int mbeg = z * rows_per_split;
     const int mend = min(sh.M, mbeg + rows_per_split);
-    // loader roles: A chunk ch (fixed k = k0 + 4 ch) of rows r0 + 8 q; dY chunk
-    // dch (fixed n = n0 + 4 dch) of rows dr0 + (kTpb / DCH) q
-    const int ch = tid & 31, r0 = tid >> 5;
-    const int dch = tid % DCH, dr0 = tid / DCH;
+    // loader roles: A chunk ch (k = k0 + 4 ch .. + 3) of the stage's pixel rows
+    // 4 g .. 4 g + 3; dY chunk dch (n = n0 + 4 dch .. + 3) of rows 4 dg .. + 3
+    const int ch = tid & 31, g = tid >> 5;
+    const int dch = tid % DCH, dg = tid / DCH;
+    const bool dld = tid < DTHR;
     const int kc = k0 + 4 * ch;
     const bool kok = kc < sh.KKC;
     const int tap = kok ? kc / sh.Cin : 0, ci = kok ? kc - tap * sh.Cin : 0;
     const int kh = tap / sh.K, kw = tap - kh * sh.K;
     const float* dcol = dY + n0 + 4 * dch;
+    const uint32_t Wo = (uint32_t)sh.Wo, Ho = (uint32_t)sh.Ho;
 
-    float4 ra[4], rd[DQ];
-    bool aok[4], dok[DQ];
-    auto load = [&](int ms) {
+    // Two register sets: the stage two ahead is loaded while the next one is
+    // written to LDS, so a load has two stages of MFMA work to arrive.  Every
+    // lane loads (rows past the end, padding and the idle dY loaders of a
+    // 64-column tile read a valid address and are zeroed when stored): a
+    // branch around a load would make the compiler's later waits drain the
+    // whole vector-memory counter.
+    struct Regs {
+        float4 a[4], d[4];
+        bool aok[4], dok[4];
+    };
+    Regs R0, R1;
+    auto load = [&](int ms, Regs& R) {
+        // decode the first of the 4 rows once, then step along the output row
+        const int m0 = ms + 4 * g;
+        uint32_t t, ow, b, oh;
+        sh.wo.divmod((uint32_t)(m0 < sh.M ? m0 : 0), t, ow);
+        sh.ho.divmod(t, b, oh);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const int m = ms + r0 + 8 * q;
-            const bool mok = m < mend;
-            const int mm = mok ? m : 0;
-            uint32_t t, ow, b, oh;
-            sh.wo.divmod((uint32_t)mm, t, ow);
-            sh.ho.divmod(t, b, oh);
             const int ih = (int)oh * sh.stride - sh.pad + kh, iw = (int)ow * sh.stride - sh.pad + kw;
-            aok[q] = mok & kok & ((unsigned)ih < (unsigned)sh.H) & ((unsigned)iw < (unsigned)sh.W);
-            const int p = aok[q] ? ((int)b * sh.H + ih) * sh.W + iw : 0;
-            ra[q] = ld4(X + (size_t)p * sh.Cin + ci);
+            R.aok[q] = (m0 + q < mend) & kok & ((unsigned)ih < (unsigned)sh.H) & ((unsigned)iw < (unsigned)sh.W);
+            const int p = R.aok[q] ? ((int)b * sh.H + ih) * sh.W + iw : 0;
+            R.a[q] = ld4(X + (size_t)p * sh.Cin + ci);
+            if (++ow == Wo) {
+                ow = 0;
+                if (++oh == Ho) {
+                    oh = 0;
+                    ++b;
+                }
+            }
         }
 #pragma unroll
-        for (int q = 0; q < DQ; ++q) {
-            const int m = ms + dr0 + (kTpb / DCH) * q;
-            dok[q] = m < mend;
-            rd[q] = ld4(dcol + (size_t)(dok[q] ? m : 0) * sh.Cout);
+        for (int q = 0; q < 4; ++q) {
+            const int m = ms + 4 * dg + q;
+            R.dok[q] = dld & (m < mend);
+            R.d[q] = ld4(dcol + (size_t)(R.dok[q] ? m : 0) * sh.Cout);
         }
     };
     auto mask4 = [](float4 v, bool ok) {
@@ -334,14 +362,18 @@ __global__ __launch_bounds__(kTpb, 2) void igemm_wgrad(float* __restrict__ part,
         v.w = __uint_as_float(__float_as_uint(v.w) & mk);
         return v;
     };
-    // dY rows hold DCH chunks; the odd-row xor 8 keeps the two half-waves'
-    // rows in different bank halves as for A (DCH >= 16)
-    auto dslot = [](int m, int chunk) { return m * DCH + (chunk ^ ((m & 1) << 3)); };
-    auto store = [&](int buf) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) As[buf][wslot(r0 + 8 * q, ch)] = mask4(ra[q], aok[q]);
-#pragma unroll
-        for (int q = 0; q < DQ; ++q) Ds[buf][dslot(dr0 + (kTpb / DCH) * q, dch)] = mask4(rd[q], dok[q]);
+    // 4 rows x 4 columns in registers -> 4 column chunks (rows 4 gg .. + 3)
+    auto put = [&](float4* tile, int col0, int gg, const float4 (&v)[4], const bool (&ok)[4]) {
+        const float4 r0 = mask4(v[0], ok[0]), r1 = mask4(v[1], ok[1]), r2 = mask4(v[2], ok[2]),
+                     r3 = mask4(v[3], ok[3]);
+        tile[tslot(col0 + 0, gg)] = make_float4(r0.x, r1.x, r2.x, r3.x);
+        tile[tslot(col0 + 1, gg)] = make_float4(r0.y, r1.y, r2.y, r3.y);
+        tile[tslot(col0 + 2, gg)] = make_float4(r0.z, r1.z, r2.z, r3.z);
+        tile[tslot(col0 + 3, gg)] = make_float4(r0.w, r1.w, r2.w, r3.w);
+    };
+    auto store = [&](int buf, const Regs& R) {
+        put(As[buf], 4 * ch, g, R.a, R.aok);
+        if (dld) put(Ds[buf], 4 * dch, dg, R.d, R.dok);
     };
     f32x16 acc[2][UT];
 #pragma unroll
@@ -349,58 +381,83 @@ __global__ __launch_bounds__(kTpb, 2) void igemm_wgrad(float* __restrict__ part,
 #pragma unroll
         for (int u = 0; u < UT; ++u) acc[t][u] = (f32x16){};
     const int fr = lane & 31, fh = lane >> 5;
-    const float* Af = reinterpret_cast<const float*>(&As[0][0]);
-    const float* Df = reinterpret_cast<const float*>(&Ds[0][0]);
-    // element (m, col) of a staged tile: float4 slot of its chunk, then the component
-    auto elem = [](int m, int col) { return wslot(m, col >> 2) * 4 + (col & 3); };
-    auto delem = [&](int m, int col) { return dslot(m, col >> 2) * 4 + (col & 3); };
-    // Operands of m pair p, and their MFMAs.  Two operand register sets: the
-    // reads of pair p + 2 are issued right after the MFMAs of pair p (the
-    // scheduling barriers keep them there), so each pair's reads have the
-    // next pair's MFMAs to arrive.
-    auto wfrag = [&](int buf, int p, float (&a)[2], float (&d)[UT]) {
-        const int abase = buf * kWgM * 32 * 4, dbase = buf * kWgM * DCH * 4;
-        const int m = 2 * p + fh;
+    // Operands of quad Q (pixels 8 Q .. 8 Q + 7) and their MFMAs.  Two operand
+    // register sets: the reads of quad Q + 2 are issued right after the MFMAs
+    // of quad Q (the scheduling barriers keep them there), so each quad's
+    // reads have the next quad's 4 x 2 x UT MFMAs to arrive.
+    auto qfrag = [&](int buf, int Q, float4 (&a)[2], float4 (&d)[UT]) {
+        const int mc = 2 * Q + fh;
 #pragma unroll
-        for (int t = 0; t < 2; ++t) a[t] = Af[abase + elem(m, wk * 64 + 32 * t + fr)];
+        for (int t = 0; t < 2; ++t) a[t] = As[buf][tslot(wk * 64 + 32 * t + fr, mc)];
 #pragma unroll
-        for (int u = 0; u < UT; ++u) d[u] = Df[dbase + delem(m, wn * (BN / 2) + 32 * u + fr)];
+        for (int u = 0; u < UT; ++u) d[u] = Ds[buf][tslot(wn * (BN / 2) + 32 * u + fr, mc)];
     };
-    auto wmfma = [&](const float (&a)[2], const float (&d)[UT]) {
+    // component-major: the 2 x UT accumulators in turn, so consecutive MFMAs
+    // never wait for each other's result
+    auto qmfma = [&](const float4 (&a)[2], const float4 (&d)[UT]) {
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
-            for (int u = 0; u < UT; ++u) acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t], d[u], acc[t][u], 0, 0, 0);
+            for (int u = 0; u < UT; ++u) acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t].x, d[u].x, acc[t][u], 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int u = 0; u < UT; ++u) acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t].y, d[u].y, acc[t][u], 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int u = 0; u < UT; ++u) acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t].z, d[u].z, acc[t][u], 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int u = 0; u < UT; ++u) acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t].w, d[u].w, acc[t][u], 0, 0, 0);
     };
     auto compute = [&](int buf) {
-        float a0[2], d0[UT], a1[2], d1[UT];
-        wfrag(buf, 0, a0, d0);
-        wfrag(buf, 1, a1, d1);
+        float4 a0[2], d0[UT], a1[2], d1[UT];
+        qfrag(buf, 0, a0, d0);
+        qfrag(buf, 1, a1, d1);
         __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int p = 0; p < kWgM / 2; p += 2) {
-            wmfma(a0, d0);
-            __builtin_amdgcn_sched_barrier(0);
-            if (p + 2 < kWgM / 2) wfrag(buf, p + 2, a0, d0);
-            __builtin_amdgcn_sched_barrier(0);
-            wmfma(a1, d1);
-            __builtin_amdgcn_sched_barrier(0);
-            if (p + 3 < kWgM / 2) wfrag(buf, p + 3, a1, d1);
-            __builtin_amdgcn_sched_barrier(0);
-        }
+        qmfma(a0, d0);
+        __builtin_amdgcn_sched_barrier(0);
+        qfrag(buf, 2, a0, d0);
+        __builtin_amdgcn_sched_barrier(0);
+        qmfma(a1, d1);
+        __builtin_amdgcn_sched_barrier(0);
+        qfrag(buf, 3, a1, d1);
+        __builtin_amdgcn_sched_barrier(0);
+        qmfma(a0, d0);
+        __builtin_amdgcn_sched_barrier(0);
+        qmfma(a1, d1);
+        __builtin_amdgcn_sched_barrier(0);
     };
+    // Stages: prologue, a branch-free steady loop over pairs of stages (stage
+    // st computes from LDS buffer st % 2 while R[st % 2] receives stage st + 2
+    // and R[(st + 1) % 2] goes to the other buffer; the second load of a pair
+    // is clamped to the last stage, a harmless reload), then the one or two
+    // stages left.
     const int nst = (mend - mbeg + kWgM - 1) / kWgM;
     if (nst > 0) {
-        load(mbeg);
-        store(0);
+        load(mbeg, R0);
+        if (nst > 1) load(mbeg + kWgM, R1);
+        store(0, R0);
         __syncthreads();
-        for (int st = 0; st + 1 < nst; ++st) {
-            load(mbeg + (st + 1) * kWgM);
-            compute(st & 1);
-            store((st + 1) & 1);
+        int st = 0;
+        for (; st + 2 < nst; st += 2) {
+            load(mbeg + (st + 2) * kWgM, R0);
+            compute(0);
+            store(1, R1);
+            __syncthreads();
+            load(mbeg + min(st + 3, nst - 1) * kWgM, R1);
+            compute(1);
+            store(0, R0);
             __syncthreads();
         }
-        compute((nst - 1) & 1);
+        compute(0);
+        if (st + 1 < nst) {
+            store(1, R1);
+            __syncthreads();
+            compute(1);
+        }
     }
     // partial tile: D[k][n], rows k = k0 + wk 64 + 32 t + 8 (r / 4) + 4 h + r % 4
     float* pb = part + (size_t)z * sh.KKC * sh.Cout + (size_t)(k0 + wk * 64 + 4 * fh) * sh.Cout + n0 + wn * (BN / 2) + fr;
