@@ -1,4 +1,4 @@
-"""The fused diffusion blocks (host/conv_residual.c, host/cond_conv_residual.c)
+"""The fused diffusion blocks (conv_residual and cond_conv_residual, host/blocks.c)
 against the reference's composition of the same launchers with the same
 parameters (reference src/conv_residual.c:21-66, src/cond_conv_residual.c:
 22-62): out, grad_in, every parameter gradient and the embedding gradient.
