@@ -416,19 +416,17 @@ def run_suite(L, nn, reps, with_cpu=True):
     KKC = K * K * Ci
     conv_flops = 2.0 * Bn * H * Wd * Co * KKC
     Wt = dev(rng.standard_normal(KKC * Co) / np.sqrt(KKC))
-    WTt, bias_c = L.alloc(KKC * Co), dev(0.1 * rng.standard_normal(Co))
+    bias_c = dev(0.1 * rng.standard_normal(Co))
     yc, gyc, gxc, gwc = L.alloc(Bn * H * Wd * Co), dev(rng.standard_normal(Bn * H * Wd * Co)), \
         L.alloc(Bn * H * Wd * Ci), L.alloc(KKC * Co)
     wgws = L.alloc(max(1, L.nnhip_conv2d_wgrad_workspace(Bn, Ci, Co, K, H, Wd)))
 
     def conv_fwd():
-        L.launch_transpose(WTt.p, Wt.p, KKC, Co, stream)
-        L.launch_conv2d_forward_implicit(yc.p, im.p, WTt.p, bias_c.p, None, Bn, H, Wd, Ci, Co, K, 1, 1, H, Wd,
-                                         stream)
+        L.launch_conv2d_forward_implicit(yc.p, im.p, Wt.p, bias_c.p, None, Bn, H, Wd, Ci, Co, K, 1, 1, H, Wd, stream)
     hWt = (hn(KKC, Co) / np.sqrt(KKC)).astype(f32)
     hgy = hn(16 * H * Wd, Co)
     conv_cpu_note = f"16 of 128 images x 8: oracle im2col + numpy float32 matmul ({os.cpu_count()} host cores)"
-    _row("conv_fwd_implicit", "cfg3 3x3 128->128, + bias (transpose + implicit GEMM)", T.median_us(conv_fwd, reps),
+    _row("conv_fwd_implicit", "cfg3 3x3 128->128, + bias (implicit GEMM)", T.median_us(conv_fwd, reps),
          4 * (Bn * H * Wd * (Ci + Co) + KKC * Co), "matrix-core bound", flops=conv_flops,
          cpu=cpu(lambda: orc.im2col(him, K, 1, 1) @ hWt, 8.0, conv_cpu_note))
     _row("conv_wgrad_implicit", "cfg3 dW = im2col(x)^T dy (split-M + fixed-order sum)",
@@ -438,9 +436,8 @@ def run_suite(L, nn, reps, with_cpu=True):
          cpu=cpu(lambda: orc.im2col(him, K, 1, 1).T @ hgy, 8.0, conv_cpu_note))
 
     def conv_dgrad():
-        L.launch_conv2d_flip_weights(WTt.p, Wt.p, K, Ci, Co, stream)
-        L.launch_conv2d_forward_implicit(gxc.p, gyc.p, WTt.p, None, None, Bn, H, Wd, Co, Ci, K, 1, 1, H, Wd, stream)
-    _row("conv_dgrad_implicit", "cfg3 dx = conv(dy, flipped kernel) (flip + implicit GEMM)", T.median_us(conv_dgrad, reps),
+        L.launch_conv2d_input_grad_implicit(gxc.p, gyc.p, Wt.p, None, Bn, H, Wd, Ci, Co, K, 1, stream)
+    _row("conv_dgrad_implicit", "cfg3 dx = conv(dy, flipped kernel) (implicit GEMM)", T.median_us(conv_dgrad, reps),
          4 * (Bn * H * Wd * (Ci + Co) + KKC * Co), "matrix-core bound", flops=conv_flops,
          cpu=cpu(lambda: orc.col2im(hgy @ hWt.T, him.shape, K, 1, 1), 8.0,
                  f"16 of 128 images x 8: numpy float32 matmul + oracle col2im ({os.cpu_count()} host cores)"))

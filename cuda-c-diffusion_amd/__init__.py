@@ -82,11 +82,11 @@ _SIGS = {
     "nnhip_spatial_reduce_workspace": (SZ, [I, I, I], False),
     "launch_conv2d_forward_implicit": (None, [P, P, P, P, P] + [I] * 10 + [P], True),
     "nnhip_conv2d_implicit_supported": (I, [I, I], False),
-    "launch_transpose": (None, [P, P, I, I, P], True),
+    "launch_conv2d_input_grad_implicit": (None, [P, P, P, P] + [I] * 7 + [P], True),
+    "nnhip_conv2d_input_grad_implicit_supported": (I, [I] * 5, False),
     "launch_conv2d_weight_grad_implicit": (None, [P, P, P] + [I] * 10 + [P, P], True),
     "nnhip_conv2d_wgrad_implicit_supported": (I, [I, I], False),
     "nnhip_conv2d_wgrad_workspace": (SZ, [I] * 6, False),
-    "launch_conv2d_flip_weights": (None, [P, P, I, I, I, P], True),
     # launch layer (nn_hip.h)
     "launch_add_bias": (None, [P, P, I, I, P], True),
     "launch_bias_grad": (None, [P, P, I, I, P], True),

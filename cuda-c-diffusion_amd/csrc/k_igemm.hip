@@ -1,24 +1,34 @@
 // k_igemm.hip -- NHWC convolution forward as an implicit GEMM on the fp32
 // matrix cores (v_mfma_f32_32x32x2f32), replacing im2col + GEMM + bias/gain
 // pass of the reference's conv2d forward (src/conv2d.c:17-34: launch_im2col,
-// gemm_forward, launch_add_bias or launch_scale_by_scalar).
+// gemm_forward, launch_add_bias or launch_scale_by_scalar), and the stride-1
+// input gradient as the same kernel over dy with the kernel flipped
+// (replacing gemm_dX + col2im, src/conv2d.c:48-65).
 //
-//   Y[m, n] = sum_k A[m, k] WT[n, k]  (+ bias[n] | * gain[0])
+//   Y[m, n] = sum_k A[m, k] Wt[k, n]  (+ bias[n] | * gain[0])
 //   m = (b, oh, ow), k = (kh, kw, ci), A[m, k] = X[b, oh s + kh - p, ow s + kw - p, ci]
-//   (0 outside the image), WT = the [K*K*C_in, C_out] weight transposed.
+//   (0 outside the image), Wt = the reference's [K*K*C_in, C_out] weight.
 //
 // The im2col matrix is never written: each workgroup gathers its A tile from X
 // directly (a k-slice of 32 channels of one (kh, kw) is 128 contiguous bytes
-// of one input pixel).
+// of one input pixel).  The weight is read in the reference's layout too, with
+// no transposed or flipped copy: the forward stages its [32 k][BN n] slice as
+// it lies in Wt and reads the B operand 32 bits at a time; the input
+// gradient's operand B[ci][(kh, kw, co)] = Wt[((K-1-kh) K + (K-1-kw)) C_in +
+// ci][co] is k-contiguous and is staged like A.
 //
 // Workgroup tile 128 (m) x BN (n, 128 or 64), k in slices of 32; 4 waves of
 // 64 x BN/2, each a 2 x BN/64 grid of 32 x 32 MFMA accumulators.  Per slice a
-// thread loads 4 float4 of A and 4 of WT into registers, the slice before it
-// computes from LDS, then the registers go to the other LDS buffer (two
-// buffers of 2 x 16 KB; two workgroups fit a CU).  LDS tiles are [128 rows][8
-// float4 chunks] with the chunk index xor-swizzled by the row (slot()), so the
-// 128-bit fragment reads of a wave (32 rows, one chunk per half-wave) and the
-// tile writes are both free of bank conflicts.
+// thread loads 4 float4 of A and up to 4 of the weight into registers, the
+// slice before it computes from LDS, then the registers go to the other LDS
+// buffer (two buffers of 2 x 16 KB; two workgroups fit a CU).  A tiles (and
+// the input gradient's B) are [128 rows][8 float4 chunks of 4 k] with the
+// chunk index xor-swizzled by the row (slot()), so the 128-bit fragment reads
+// of a wave (32 rows, one chunk per half-wave) and the tile writes are free of
+// bank conflicts.  The forward's B tile is [32 k][BN n], each row rotated by
+// 32 n on alternate groups of 4 rows (kslot()), so the two half-waves of a
+// 32-bit fragment read (rows k and k + 4, 32 consecutive n each) use
+// disjoint banks.
 //
 // Lane layout of v_mfma_f32_32x32x2f32 (checked on the device): lane l supplies
 // A[l % 32][l / 32] and B[l / 32][l % 32]; accumulator register r of lane l
@@ -56,13 +66,26 @@ __device__ __forceinline__ int slot(int row, int chunk) {
     return row * 8 + (chunk ^ (row & 7) ^ ((row >> 3) & 1));
 }
 
-enum { kEpiNone = 0, kEpiBias = 1, kEpiGain = 2 };
+// float offset of (k, n) in a [32][BN] B tile: rows 4..7 of every 8 rotated by 32
+template <int BN>
+__device__ __forceinline__ int kslot(int k, int n) {
+    return k * BN + ((n + 32 * ((k >> 2) & 1)) & (BN - 1));
+}
 
-template <int EPI, int BN>
+enum { kEpiNone = 0, kEpiBias = 1, kEpiGain = 2 };
+// Source of operand B: the forward's weight Wt[k][n], or the input gradient's
+// flipped weight (sh is then the gradient's convolution: C_in = the layer's
+// C_out, C_out = the layer's C_in, so Wt is [K*K*sh.Cout][sh.Cin]).
+enum { kWFwd = 0, kWFlip = 1 };
+
+template <int EPI, int BN, int WSRC>
 __global__ __launch_bounds__(kTpb, 2) void igemm_fwd(float* __restrict__ Y, const float* __restrict__ X,
-    const float* __restrict__ WT, const float* __restrict__ bias, const float* __restrict__ gain, ConvShape sh) {
+    const float* __restrict__ Wt, const float* __restrict__ bias, const float* __restrict__ gain, ConvShape sh) {
     constexpr int UT = BN / 64;  // 32-column accumulator tiles per wave
-    constexpr int BQ = BN / 32;  // WT rows loaded per thread
+    // weight float4 loaded per thread: a 4 x 4 block (forward) or BN / 32
+    // rows of one chunk (flipped)
+    constexpr int BQ = WSRC == kWFwd ? 4 : BN / 32;
+    constexpr int NQ = BN / 4;   // forward: n quads of the tile
     __shared__ float4 As[2][kBM * 8];
     __shared__ float4 Bs[2][BN * 8];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -84,8 +107,15 @@ __global__ __launch_bounds__(kTpb, 2) void igemm_fwd(float* __restrict__ Y, cons
         ihb[q] = (int)oh * sh.stride - sh.pad;
         iwb[q] = (int)ow * sh.stride - sh.pad;
     }
-    const float* wrow = WT + (size_t)(n0 + r0) * sh.KKC + ch * 4;
-    const size_t wstep = (size_t)32 * sh.KKC;
+    // forward weight roles: n quad n4, k rows 4 kq .. 4 kq + 3 of the slice
+    // (with BN = 64 the second half of the workgroup repeats the first's
+    // loads and stores nothing: every lane loads, see below)
+    const int n4 = tid % NQ, kq = (tid / NQ) % 8;
+    const bool bput = NQ * 8 >= kTpb || tid < NQ * 8;
+    const float* wq = Wt + (size_t)(4 * kq) * sh.Cout + n0 + 4 * n4;
+    // flipped weight: row n0 + r0 + 32 q of the tap's [C_in][C_out] block
+    const float* wrow = Wt + (size_t)(n0 + r0) * sh.Cin + ch * 4;
+    const int KK = sh.K * sh.K;
 
     // Every lane loads (a padding position reads channel ci of pixel 0 and is
     // zeroed when stored): a branch around a load would make the compiler's
@@ -100,15 +130,19 @@ __global__ __launch_bounds__(kTpb, 2) void igemm_fwd(float* __restrict__ Y, cons
     Regs R0, R1;
     auto load = [&](int kt, Regs& R) {
         const int k0 = kt * kBK;
-        const int khw = k0 / sh.Cin, ci = k0 - khw * sh.Cin + ch * 4;
+        const int khw = k0 / sh.Cin, cs = k0 - khw * sh.Cin, ci = cs + ch * 4;
         const int kh = khw / sh.K, kw = khw - kh * sh.K;
+        // flipped weight: the slice's channels cs.. of tap KK-1-khw, a
+        // uniform offset from each lane's row (held in a scalar register)
+        const int wfo = __builtin_amdgcn_readfirstlane((KK - 1 - khw) * sh.Cout * sh.Cin + cs);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int ih = ihb[q] + kh, iw = iwb[q] + kw;
             R.ok[q] = rok[q] & ((unsigned)ih < (unsigned)sh.H) & ((unsigned)iw < (unsigned)sh.W);
             const int p = R.ok[q] ? pix[q] + ih * sh.W + iw : 0;
             R.a[q] = ld4(X + (size_t)p * sh.Cin + ci);
-            if (q < BQ) R.b[q] = ld4(wrow + q * wstep + k0);
+            if constexpr (WSRC == kWFwd) R.b[q] = ld4(wq + (size_t)(k0 + q) * sh.Cout);
+            else if (q < BQ) R.b[q] = ld4(wrow + wfo + 32 * q * sh.Cin);
         }
     };
     // Padding is zeroed by masking the bits (a select of whole float4 values
@@ -123,7 +157,18 @@ __global__ __launch_bounds__(kTpb, 2) void igemm_fwd(float* __restrict__ Y, cons
             v.z = __uint_as_float(__float_as_uint(R.a[q].z) & mk);
             v.w = __uint_as_float(__float_as_uint(R.a[q].w) & mk);
             As[buf][slot(r0 + 32 * q, ch)] = v;
-            if (q < BQ) Bs[buf][slot(r0 + 32 * q, ch)] = R.b[q];
+            if constexpr (WSRC == kWFlip) {
+                if (q < BQ) Bs[buf][slot(r0 + 32 * q, ch)] = R.b[q];
+            }
+        }
+        // forward: k rows 4 kq + i, n 4 n4 .. 4 n4 + 3, as loaded
+        if constexpr (WSRC == kWFwd) {
+            if (bput) {
+                float* bs = reinterpret_cast<float*>(&Bs[buf][0]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    *reinterpret_cast<float4*>(bs + kslot<BN>(4 * kq + i, 4 * n4)) = R.b[i];
+            }
         }
     };
 
@@ -152,8 +197,21 @@ __global__ __launch_bounds__(kTpb, 2) void igemm_fwd(float* __restrict__ Y, cons
         const int c = 2 * kq + fh;
 #pragma unroll
         for (int t = 0; t < 2; ++t) a[t] = As[buf][slot(wm * 64 + 32 * t + fr, c)];
+        if constexpr (WSRC == kWFwd) {
+            // component j of b[u] = B[k = 4 c + j][n]: rows 8 kq + 4 fh + j
+            const float* bs = reinterpret_cast<const float*>(&Bs[buf][0]);
 #pragma unroll
-        for (int u = 0; u < UT; ++u) b[u] = Bs[buf][slot(wn * (BN / 2) + 32 * u + fr, c)];
+            for (int u = 0; u < UT; ++u) {
+                const int n = wn * (BN / 2) + 32 * u + fr;
+                b[u].x = bs[kslot<BN>(4 * c + 0, n)];
+                b[u].y = bs[kslot<BN>(4 * c + 1, n)];
+                b[u].z = bs[kslot<BN>(4 * c + 2, n)];
+                b[u].w = bs[kslot<BN>(4 * c + 3, n)];
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < UT; ++u) b[u] = Bs[buf][slot(wn * (BN / 2) + 32 * u + fr, c)];
+        }
     };
     auto mfmas = [&](const float4 (&a)[2], const float4 (&b)[UT]) {
 #pragma unroll
@@ -513,38 +571,6 @@ WgradPlan wgrad_plan(int M, int KKC, int Cout) {
     return p;
 }
 
-// WF[ci][(kh', kw', co)] = Wt[((K-1-kh') K + (K-1-kw')) C_in + ci][co]: the
-// weight of the stride-1 input gradient, which is then a forward convolution
-// of dy with the flipped kernel and padding K-1-pad.
-__global__ __launch_bounds__(256) void flip_weights_kernel(float* __restrict__ WF, const float* __restrict__ Wt,
-    int K, int Cin, int Cout) {
-    const long long n = (long long)K * K * Cin * Cout;
-    for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long long)gridDim.x * 256) {
-        const int co = (int)(i % Cout);
-        const long long r = i / Cout;                 // (ci, tap')
-        const int tap = (int)(r % (K * K)), ci = (int)(r / (K * K));
-        const int src_tap = K * K - 1 - tap;          // (K-1-kh') K + (K-1-kw')
-        WF[i] = Wt[((size_t)src_tap * Cin + ci) * Cout + co];
-    }
-}
-
-// out[c][r] = in[r][c] for a row-major [rows, cols] matrix (32 x 32 LDS tiles).
-__global__ __launch_bounds__(256) void transpose_kernel(float* __restrict__ out, const float* __restrict__ in,
-    int rows, int cols) {
-    __shared__ float tile[32][33];
-    const int c0 = blockIdx.x * 32, r0 = blockIdx.y * 32;
-    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
-    for (int k = ty; k < 32; k += 8) {
-        const int r = r0 + k, c = c0 + tx;
-        if (r < rows && c < cols) tile[k][tx] = in[(size_t)r * cols + c];
-    }
-    __syncthreads();
-    for (int k = ty; k < 32; k += 8) {
-        const int c = c0 + k, r = r0 + tx;
-        if (r < rows && c < cols) out[(size_t)c * rows + r] = tile[tx][k];
-    }
-}
-
 }  // namespace
 
 extern "C" {
@@ -553,17 +579,7 @@ int nnhip_conv2d_implicit_supported(int C_in, int C_out) {
     return C_in > 0 && C_out > 0 && C_in % kBK == 0 && C_out % kBNmin == 0;
 }
 
-void launch_transpose(float* out, const float* in, int rows, int cols, hipStream_t s) {
-    const char* what = "launch_transpose";
-    NNK_REQUIRE(rows >= 0 && cols >= 0, what, "%s: bad shape %d x %d", what, rows, cols);
-    if ((long long)rows * cols == 0) return;
-    NNK_REQUIRE(out && in && out != in, what, "%s: null or aliased pointers", what);
-    const dim3 grid((unsigned)((cols + 31) / 32), (unsigned)((rows + 31) / 32));
-    transpose_kernel<<<grid, 256, 0, s>>>(out, in, rows, cols);
-    nnk_after_launch(what, s);
-}
-
-void launch_conv2d_forward_implicit(float* Y, const float* X, const float* WT, const float* bias,
+void launch_conv2d_forward_implicit(float* Y, const float* X, const float* Wt, const float* bias,
     const float* gain, int batch, int H, int W, int C_in, int C_out, int K, int stride, int pad, int H_out,
     int W_out, hipStream_t s) {
     const char* what = "launch_conv2d_forward_implicit";
@@ -577,16 +593,16 @@ void launch_conv2d_forward_implicit(float* Y, const float* X, const float* WT, c
         what, "%s: tensor exceeds the 32-bit index range", what);
     NNK_REQUIRE(!(bias && gain), what, "%s: bias and gain are exclusive", what);
     if (batch == 0) return;
-    NNK_REQUIRE(Y && X && WT, what, "%s: null pointer", what);
-    NNK_REQUIRE(aligned16(X) && aligned16(WT), what, "%s: X and WT must be 16-byte aligned", what);
+    NNK_REQUIRE(Y && X && Wt, what, "%s: null pointer", what);
+    NNK_REQUIRE(aligned16(X) && aligned16(Wt), what, "%s: x and the weight must be 16-byte aligned", what);
     ConvShape sh{batch, H, W, C_in, C_out, K, stride, pad, H_out, W_out, batch * H_out * W_out, K * K * C_in,
         FastDiv((uint32_t)W_out), FastDiv((uint32_t)H_out)};
     const int BN = tile_n(C_out);
     const dim3 grid((unsigned)((sh.M + kBM - 1) / kBM), (unsigned)(C_out / BN));
-#define NNK_IGEMM_FWD(BN_)                                                                    \
-    if (bias) igemm_fwd<kEpiBias, BN_><<<grid, kTpb, 0, s>>>(Y, X, WT, bias, nullptr, sh);   \
-    else if (gain) igemm_fwd<kEpiGain, BN_><<<grid, kTpb, 0, s>>>(Y, X, WT, nullptr, gain, sh); \
-    else igemm_fwd<kEpiNone, BN_><<<grid, kTpb, 0, s>>>(Y, X, WT, nullptr, nullptr, sh);
+#define NNK_IGEMM_FWD(BN_)                                                                               \
+    if (bias) igemm_fwd<kEpiBias, BN_, kWFwd><<<grid, kTpb, 0, s>>>(Y, X, Wt, bias, nullptr, sh);       \
+    else if (gain) igemm_fwd<kEpiGain, BN_, kWFwd><<<grid, kTpb, 0, s>>>(Y, X, Wt, nullptr, gain, sh);  \
+    else igemm_fwd<kEpiNone, BN_, kWFwd><<<grid, kTpb, 0, s>>>(Y, X, Wt, nullptr, nullptr, sh);
     if (BN == 128) {
         NNK_IGEMM_FWD(128)
     } else {
@@ -596,14 +612,39 @@ void launch_conv2d_forward_implicit(float* Y, const float* X, const float* WT, c
     nnk_after_launch(what, s);
 }
 
-void launch_conv2d_flip_weights(float* WF, const float* Wt, int K, int C_in, int C_out, hipStream_t s) {
-    const char* what = "launch_conv2d_flip_weights";
-    NNK_REQUIRE(K > 0 && C_in > 0 && C_out > 0, what, "%s: bad shape", what);
-    NNK_REQUIRE(WF && Wt && WF != Wt, what, "%s: null or aliased pointers", what);
-    const long long n = (long long)K * K * C_in * C_out;
-    long long blocks = (n + 255) / 256;
-    if (blocks > 8192) blocks = 8192;
-    flip_weights_kernel<<<(unsigned)blocks, 256, 0, s>>>(WF, Wt, K, C_in, C_out);
+int nnhip_conv2d_input_grad_implicit_supported(int C_in, int C_out, int K, int stride, int pad) {
+    return stride == 1 && K > 0 && pad >= 0 && pad <= K - 1 && nnhip_conv2d_implicit_supported(C_out, C_in);
+}
+
+void launch_conv2d_input_grad_implicit(float* dX, const float* dY, const float* Wt, const float* gain, int batch,
+    int H, int W, int C_in, int C_out, int K, int pad, hipStream_t s) {
+    const char* what = "launch_conv2d_input_grad_implicit";
+    NNK_REQUIRE(batch >= 0 && H > 0 && W > 0 && K > 0 && pad >= 0, what, "%s: bad geometry", what);
+    NNK_REQUIRE(nnhip_conv2d_input_grad_implicit_supported(C_in, C_out, K, 1, pad), what,
+        "%s: needs pad <= K - 1, C_out %% %d == 0 and C_in %% %d == 0 (C_in=%d C_out=%d K=%d pad=%d)", what, kBK,
+        kBNmin, C_in, C_out, K, pad);
+    const int Ho = H + 2 * pad - K + 1, Wo = W + 2 * pad - K + 1;
+    NNK_REQUIRE(Ho > 0 && Wo > 0, what, "%s: empty output for this geometry", what);
+    NNK_REQUIRE((long long)batch * H * W * C_in < (1LL << 31) && (long long)batch * Ho * Wo * C_out < (1LL << 31),
+        what, "%s: tensor exceeds the 32-bit index range", what);
+    if (batch == 0) return;
+    NNK_REQUIRE(dX && dY && Wt, what, "%s: null pointer", what);
+    NNK_REQUIRE(aligned16(dY) && aligned16(Wt), what, "%s: dy and the weight must be 16-byte aligned", what);
+    // dx = the stride-1 convolution of dy (Ho x Wo x C_out) with the flipped
+    // kernel and padding K-1-pad, whose output is H x W x C_in
+    ConvShape sh{batch, Ho, Wo, C_out, C_in, K, 1, K - 1 - pad, H, W, batch * H * W, K * K * C_out,
+        FastDiv((uint32_t)W), FastDiv((uint32_t)H)};
+    const int BN = tile_n(C_in);
+    const dim3 grid((unsigned)((sh.M + kBM - 1) / kBM), (unsigned)(C_in / BN));
+#define NNK_IGEMM_DGRAD(BN_)                                                                                  \
+    if (gain) igemm_fwd<kEpiGain, BN_, kWFlip><<<grid, kTpb, 0, s>>>(dX, dY, Wt, nullptr, gain, sh);           \
+    else igemm_fwd<kEpiNone, BN_, kWFlip><<<grid, kTpb, 0, s>>>(dX, dY, Wt, nullptr, nullptr, sh);
+    if (BN == 128) {
+        NNK_IGEMM_DGRAD(128)
+    } else {
+        NNK_IGEMM_DGRAD(64)
+    }
+#undef NNK_IGEMM_DGRAD
     nnk_after_launch(what, s);
 }
 

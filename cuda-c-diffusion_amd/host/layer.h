@@ -23,7 +23,7 @@
 #define LAYER_MAX_BUFS 16
 #define LAYER_MAX_PARAMS 3
 #define LAYER_MAX_SUBS 6
-#define LAYER_MAX_DIMS 12
+#define LAYER_MAX_DIMS 16
 
 typedef struct Layer Layer;
 

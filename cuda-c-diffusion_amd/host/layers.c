@@ -313,14 +313,15 @@ Module* sinusoidal_create(int num_channels, float max_period)
  * counts allow it (C_in % 32 == 0, C_out % 64 == 0), bias or gain in its
  * epilogue; otherwise im2col + rocBLAS + the bias/gain pass, as the
  * reference.  Backward: the weight gradient as an implicit GEMM (C_in % 4,
- * C_out % 64), the stride-1 input gradient as the implicit forward of
+ * C_out % 64), the stride-1 input gradient as the implicit convolution of
  * grad_out with the flipped kernel (C_out % 32, C_in % 64); otherwise
  * im2col + rocBLAS and the gather col2im, which needs no memset of grad_in.
+ * The implicit kernels read the weight in its own layout.
  * NNHIP_CONV_PATH=gemm forces the reference's sequence.
  * ------------------------------------------------------------------------ */
 
-enum { CB_W, CB_GW, CB_AUX, CB_GAUX, CB_COL, CB_WT, CB_WF, CB_WGWS, CB_WNWS };
-enum { CD_CIN, CD_COUT, CD_K, CD_S, CD_P, CD_HI, CD_WI, CD_HO, CD_WO, CD_MP, CD_WGRAD };
+enum { CB_W, CB_GW, CB_AUX, CB_GAUX, CB_COL, CB_WGWS, CB_WNWS };
+enum { CD_CIN, CD_COUT, CD_K, CD_S, CD_P, CD_HI, CD_WI, CD_HO, CD_WO, CD_MP, CD_FWD, CD_WGRAD, CD_DGRAD };
 
 static int conv_gemm_forced(void)
 {
@@ -334,9 +335,8 @@ static void conv_fwd(Layer* L, const float* in, float* out, int batch, Context* 
     const int kg = d[CD_K] * d[CD_K] * d[CD_CIN], rows = batch * d[CD_HO] * d[CD_WO];
     float *w = L->buf[CB_W], *aux = L->buf[CB_AUX];
     if (d[CD_MP]) launch_weight_normalize(w, kg, d[CD_COUT], L->k[0], ctx->stream);
-    if (L->buf[CB_WT] && !conv_gemm_forced()) {
-        launch_transpose(L->buf[CB_WT], w, kg, d[CD_COUT], ctx->stream);
-        launch_conv2d_forward_implicit(out, in, L->buf[CB_WT], d[CD_MP] ? NULL : aux, d[CD_MP] ? aux : NULL, batch,
+    if (d[CD_FWD] && !conv_gemm_forced()) {
+        launch_conv2d_forward_implicit(out, in, w, d[CD_MP] ? NULL : aux, d[CD_MP] ? aux : NULL, batch,
             d[CD_HI], d[CD_WI], d[CD_CIN], d[CD_COUT], d[CD_K], d[CD_S], d[CD_P], d[CD_HO], d[CD_WO], ctx->stream);
         return;
     }
@@ -372,11 +372,10 @@ static void conv_bwd(Layer* L, const float* in, const float* out, const float* g
     }
     if (!grad_in) return;
     const float* gain = d[CD_MP] ? L->buf[CB_AUX] : NULL;
-    if (L->buf[CB_WF] && !forced) {
+    if (d[CD_DGRAD] && !forced) {
         /* stride 1: dx = conv(dy, flipped kernel, pad K-1-pad), times the gain in mp mode */
-        launch_conv2d_flip_weights(L->buf[CB_WF], w, d[CD_K], d[CD_CIN], d[CD_COUT], ctx->stream);
-        launch_conv2d_forward_implicit(grad_in, grad_out, L->buf[CB_WF], NULL, gain, batch, d[CD_HO], d[CD_WO],
-            d[CD_COUT], d[CD_CIN], d[CD_K], 1, d[CD_K] - 1 - d[CD_P], d[CD_HI], d[CD_WI], ctx->stream);
+        launch_conv2d_input_grad_implicit(grad_in, grad_out, w, gain, batch, d[CD_HI], d[CD_WI], d[CD_CIN],
+            d[CD_COUT], d[CD_K], d[CD_P], ctx->stream);
         return;
     }
     nn_gemm_dX(ctx->blas, 1.0f, w, grad_out, col, rows, kg, d[CD_COUT]);
@@ -405,19 +404,16 @@ Module* conv2d_create(Context* ctx, int C_in, int C_out, int K, int stride, int 
     d[CD_HO] = Ho;
     d[CD_WO] = Wo;
     d[CD_MP] = mp_mode != 0;
+    d[CD_FWD] = nnhip_conv2d_implicit_supported(C_in, C_out);
     d[CD_WGRAD] = nnhip_conv2d_wgrad_implicit_supported(C_in, C_out);
+    d[CD_DGRAD] = nnhip_conv2d_input_grad_implicit_supported(C_in, C_out, K, stride, pad);
     L->k[0] = 1e-4f;
-    /* the input gradient of a stride-1 convolution is a forward convolution
-       of grad_out (C_out channels in, C_in out) with padding K-1-pad >= 0 */
-    const int dgrad_implicit = stride == 1 && pad <= K - 1 && nnhip_conv2d_implicit_supported(C_out, C_in);
     const int aux_n = mp_mode ? 1 : C_out;
     layer_buf(L, nw, 0);
     layer_buf(L, nw, 0);
     layer_buf(L, (size_t)aux_n, 1);
     layer_buf(L, (size_t)aux_n, 0);
     layer_buf(L, (size_t)max_batch * Ho * Wo * kg, 0);
-    layer_buf(L, nnhip_conv2d_implicit_supported(C_in, C_out) ? nw : 0, 0);
-    layer_buf(L, dgrad_implicit ? nw : 0, 0);
     layer_buf(L, d[CD_WGRAD] ? nnhip_conv2d_wgrad_workspace(max_batch, C_in, C_out, K, Ho, Wo) : 0, 0);
     layer_buf(L, mp_mode ? nnhip_weight_normalize_backward_workspace(C_out) : 0, 1);
     layer_param(L, CB_W, CB_GW, (int)nw);

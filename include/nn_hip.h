@@ -234,12 +234,12 @@ void launch_spatial_modulate_act_backward(float* grad_in, float* grad_cond,
 /* NHWC convolution forward as an implicit GEMM on the matrix cores: the
    im2col matrix is gathered tile by tile from x, never written.  Replaces the
    reference's launch_im2col + gemm_forward + launch_add_bias /
-   launch_scale_by_scalar (src/conv2d.c:17-34).  WT is the [K*K*C_in, C_out]
-   weight transposed to [C_out, K*K*C_in] (launch_transpose); y [batch*H_out*W_out,
-   C_out] = conv + bias[n] (bias non-NULL) or conv * gain[0] (gain non-NULL) or
-   conv.  Needs C_in % 32 == 0 and C_out % 64 == 0
-   (nnhip_conv2d_implicit_supported); x and WT 16-byte aligned. */
-void launch_conv2d_forward_implicit(float* y, const float* x, const float* WT, const float* bias,
+   launch_scale_by_scalar (src/conv2d.c:17-34).  Wt is the reference's
+   [K*K*C_in, C_out] weight, read as it is; y [batch*H_out*W_out, C_out] =
+   conv + bias[n] (bias non-NULL) or conv * gain[0] (gain non-NULL) or conv.
+   Needs C_in % 32 == 0 and C_out % 64 == 0 (nnhip_conv2d_implicit_supported);
+   x and Wt 16-byte aligned. */
+void launch_conv2d_forward_implicit(float* y, const float* x, const float* Wt, const float* bias,
     const float* gain, int batch, int H, int W, int C_in, int C_out, int K, int stride, int pad,
     int H_out, int W_out, hipStream_t s);
 int nnhip_conv2d_implicit_supported(int C_in, int C_out);
@@ -256,14 +256,17 @@ void launch_conv2d_weight_grad_implicit(float* gW, const float* x, const float* 
 int nnhip_conv2d_wgrad_implicit_supported(int C_in, int C_out);
 size_t nnhip_conv2d_wgrad_workspace(int batch, int C_in, int C_out, int K, int H_out, int W_out);
 
-/* WF [C_in, K*K*C_out] from the [K*K*C_in, C_out] weight Wt, kernel flipped:
-   WF[ci][(kh, kw, co)] = Wt[((K-1-kh) K + (K-1-kw)) C_in + ci][co].  With it the
-   stride-1 input gradient is launch_conv2d_forward_implicit(dx, dy, WF, ...)
-   over the H_out x W_out x C_out gradient with padding K-1-pad. */
-void launch_conv2d_flip_weights(float* WF, const float* Wt, int K, int C_in, int C_out, hipStream_t s);
-
-/* out[c, r] = in[r, c] for a row-major [rows, cols] matrix (out != in). */
-void launch_transpose(float* out, const float* in, int rows, int cols, hipStream_t s);
+/* Input gradient of a stride-1 convolution as an implicit GEMM on the
+   matrix cores: dx [batch, H, W, C_in] (overwritten) = the convolution of dy
+   [batch, H_out, W_out, C_out] (H_out = H + 2 pad - K + 1) with the kernel of
+   the [K*K*C_in, C_out] weight Wt flipped and padding K-1-pad, times gain[0]
+   when gain is non-NULL.  Replaces the reference's gemm_dX +
+   cudaMemsetAsync + launch_col2im (src/conv2d.c:48-65) for stride 1.  Needs
+   pad <= K-1, C_out % 32 == 0 and C_in % 64 == 0
+   (nnhip_conv2d_input_grad_implicit_supported); dy and Wt 16-byte aligned. */
+void launch_conv2d_input_grad_implicit(float* dx, const float* dy, const float* Wt, const float* gain,
+    int batch, int H, int W, int C_in, int C_out, int K, int pad, hipStream_t s);
+int nnhip_conv2d_input_grad_implicit_supported(int C_in, int C_out, int K, int stride, int pad);
 
 /* launch_spatial_reduce_sum with a lent workspace (may be NULL). */
 void launch_spatial_reduce_sum_ws(float* out, const float* in, int batch, int HW, int C,
