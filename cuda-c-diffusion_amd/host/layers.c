@@ -317,7 +317,10 @@ Module* sinusoidal_create(int num_channels, float max_period)
  * grad_out with the flipped kernel (C_out % 32, C_in % 64); otherwise
  * im2col + rocBLAS and the gather col2im, which needs no memset of grad_in.
  * The implicit kernels read the weight in its own layout.
- * NNHIP_CONV_PATH=gemm forces the reference's sequence.
+ * NNHIP_CONV_PATH=gemm forces the reference's sequence.  Its im2col matrix
+ * (max_batch * H_out * W_out * K*K*C_in floats, 604 MB at cfg3) is allocated
+ * only for a path the implicit kernels do not take, or when the variable is
+ * set as the module is created; forcing the sequence later is refused.
  * ------------------------------------------------------------------------ */
 
 enum { CB_W, CB_GW, CB_AUX, CB_GAUX, CB_COL, CB_WGWS, CB_WNWS };
@@ -329,13 +332,22 @@ static int conv_gemm_forced(void)
     return e && strcmp(e, "gemm") == 0;
 }
 
+/* the reference's sequence asked for at this call (needs the im2col buffer) */
+static int conv_gemm_path(const Layer* L)
+{
+    if (!conv_gemm_forced()) return 0;
+    NN_ASSERT(L->buf[CB_COL], "conv2d: NNHIP_CONV_PATH=gemm must be set when the module is created "
+                              "(its im2col buffer is allocated then)");
+    return 1;
+}
+
 static void conv_fwd(Layer* L, const float* in, float* out, int batch, Context* ctx)
 {
     const int* d = L->dim;
     const int kg = d[CD_K] * d[CD_K] * d[CD_CIN], rows = batch * d[CD_HO] * d[CD_WO];
     float *w = L->buf[CB_W], *aux = L->buf[CB_AUX];
     if (d[CD_MP]) launch_weight_normalize(w, kg, d[CD_COUT], L->k[0], ctx->stream);
-    if (d[CD_FWD] && !conv_gemm_forced()) {
+    if (d[CD_FWD] && !conv_gemm_path(L)) {
         launch_conv2d_forward_implicit(out, in, w, d[CD_MP] ? NULL : aux, d[CD_MP] ? aux : NULL, batch,
             d[CD_HI], d[CD_WI], d[CD_CIN], d[CD_COUT], d[CD_K], d[CD_S], d[CD_P], d[CD_HO], d[CD_WO], ctx->stream);
         return;
@@ -353,7 +365,7 @@ static void conv_bwd(Layer* L, const float* in, const float* out, const float* g
     (void)out;
     const int* d = L->dim;
     const int kg = d[CD_K] * d[CD_K] * d[CD_CIN], rows = batch * d[CD_HO] * d[CD_WO];
-    const int forced = conv_gemm_forced();
+    const int forced = conv_gemm_path(L);
     float *w = L->buf[CB_W], *gw = L->buf[CB_GW], *col = L->buf[CB_COL];
     if (d[CD_WGRAD] && !forced) {
         launch_conv2d_weight_grad_implicit(gw, in, grad_out, batch, d[CD_HI], d[CD_WI], d[CD_CIN], d[CD_COUT],
@@ -413,7 +425,9 @@ Module* conv2d_create(Context* ctx, int C_in, int C_out, int K, int stride, int 
     layer_buf(L, nw, 0);
     layer_buf(L, (size_t)aux_n, 1);
     layer_buf(L, (size_t)aux_n, 0);
-    layer_buf(L, (size_t)max_batch * Ho * Wo * kg, 0);
+    /* the im2col matrix, for the paths the implicit kernels do not take */
+    const int need_col = !d[CD_FWD] || !d[CD_WGRAD] || !d[CD_DGRAD] || conv_gemm_forced();
+    layer_buf(L, need_col ? (size_t)max_batch * Ho * Wo * kg : 0, 0);
     layer_buf(L, d[CD_WGRAD] ? nnhip_conv2d_wgrad_workspace(max_batch, C_in, C_out, K, Ho, Wo) : 0, 0);
     layer_buf(L, mp_mode ? nnhip_weight_normalize_backward_workspace(C_out) : 0, 1);
     layer_param(L, CB_W, CB_GW, (int)nw);

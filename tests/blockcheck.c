@@ -315,6 +315,9 @@ double nn_convcheck(int B, int H, int W, int Cin, int Cout, int K, int stride, i
     float* out_ms)
 {
     nn_context_init(&g, 17ull, (hipStream_t)0);
+    /* created with the reference's sequence forced, so that it has the im2col
+       buffer both paths below need */
+    setenv("NNHIP_CONV_PATH", "gemm", 1);
     Module* conv = conv2d_create(&g, Cin, Cout, K, stride, pad, H, W, B, mp, 1.0f);
     if (!mp) {
         ParamList pl;
