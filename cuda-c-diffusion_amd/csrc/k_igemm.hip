@@ -625,7 +625,8 @@ void launch_conv2d_input_grad_implicit(float* dX, const float* dY, const float* 
         kBNmin, C_in, C_out, K, pad);
     const int Ho = H + 2 * pad - K + 1, Wo = W + 2 * pad - K + 1;
     NNK_REQUIRE(Ho > 0 && Wo > 0, what, "%s: empty output for this geometry", what);
-    NNK_REQUIRE((long long)batch * H * W * C_in < (1LL << 31) && (long long)batch * Ho * Wo * C_out < (1LL << 31),
+    NNK_REQUIRE((long long)batch * H * W * C_in < (1LL << 31) && (long long)batch * Ho * Wo * C_out < (1LL << 31) &&
+                    (long long)K * K * C_in * C_out < (1LL << 31),
         what, "%s: tensor exceeds the 32-bit index range", what);
     if (batch == 0) return;
     NNK_REQUIRE(dX && dY && Wt, what, "%s: null pointer", what);

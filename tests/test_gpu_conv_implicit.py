@@ -198,3 +198,5 @@ def test_conv_input_grad_implicit_refusals(L, nn):
         L.launch_conv2d_input_grad_implicit(dummy.p, dummy.p, dummy.p, None, 1, 4, 4, 128, 128, 3, 3, None)
     with pytest.raises(nn.NnHipError):
         L.launch_conv2d_input_grad_implicit(dummy.p, dummy.p, dummy.p, None, 1, 4, 4, 96, 128, 3, 1, None)
+    with pytest.raises(nn.NnHipError):  # a weight of 2^31 elements or more
+        L.launch_conv2d_input_grad_implicit(dummy.p, dummy.p, dummy.p, None, 1, 4, 4, 16384, 16384, 3, 1, None)
