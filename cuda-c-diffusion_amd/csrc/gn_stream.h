@@ -258,10 +258,14 @@ struct Work {
 // has arrived at the end (and so has read it), stores the new value.  The
 // tag is therefore unique per launch on the workspace also when the launch
 // is replayed from a captured graph with the same arguments.
-__device__ __forceinline__ unsigned launch_epoch(const Work& wk) {
-    const unsigned e = __hip_atomic_load(wk.ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+__device__ __forceinline__ unsigned epoch_word(const Work& wk) {
+    return __hip_atomic_load(wk.ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned epoch_of(unsigned word) {
+    const unsigned e = word + 1u;
     return e ? e : 1u;
 }
+__device__ __forceinline__ unsigned launch_epoch(const Work& wk) { return epoch_of(epoch_word(wk)); }
 __device__ __forceinline__ void publish_epoch(const Work& wk, unsigned epoch) {
     __hip_atomic_store(wk.ep, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -385,9 +389,9 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
     const int c0 = cb * CW4 * 4 + col * 4;      // first channel of this lane
     const uint32_t voff = (uint32_t)(row0 * sh.C + c0) * 4u;
     const uint32_t row_bytes = (uint32_t)sh.C * 4u;
-    const float4 gm = ld4(gamma + c0), bt = ld4(beta + c0);
-    settle(gm);
-    settle(bt);
+    // gamma and beta of this lane's channels, loaded once the first tile's
+    // loads are out (at the tile loop's start)
+    float4 gm = make_float4(0.0f, 0.0f, 0.0f, 0.0f), bt = gm;
     const float nthr = (float)(NV * 4);
     const unsigned epoch = launch_epoch(wk);
     const unsigned long long tag = (unsigned long long)epoch << 32;
@@ -591,8 +595,18 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
         records_prefetch(j - 1);
         pb ^= 1;
     };
+    // gamma and beta are loaded right before the first two tiles' loads and
+    // settled (so that their first use in the loop does not wait for the
+    // staged tiles) only after those are issued: the tile loads no longer
+    // wait for a round trip, and the settle waits for gamma and beta alone
+    // (loads complete in order).
+    gm = ld4(gamma + c0);
+    bt = ld4(beta + c0);
+    __builtin_amdgcn_sched_barrier(0);  // keep them above the tile loads
     issue(0, 0);
     issue(1, 1);
+    settle(gm);
+    settle(bt);
     vm_wait<NV + SH>();
     take(S0, 0);
     issue(2, 0);
@@ -694,7 +708,8 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
     const int gglob = cb * GT + gl;             // global group index of this lane
     const uint32_t voff = (uint32_t)(row0 * sh.C + c0) * 4u;
     const uint32_t row_bytes = (uint32_t)sh.C * 4u;
-    // gamma and beta of this lane's channels: held in registers, or, where
+    // gamma and beta of this lane's channels: held in registers (loaded once
+    // the first tile's loads are out, at the tile loop's start), or, where
     // the tile loop needs those registers (the shift's column sums), read
     // from LDS in each phase A
     constexpr bool kAffineLds = SHIFT;
@@ -706,14 +721,18 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
             affine[1][tid] = ACT != ACT_IDENTITY ? ld4(beta + cb * CW4 * 4 + tid * 4) : gm_r;
         }
         __syncthreads();
-    } else {
-        gm_r = ld4(gamma + c0);
-        if constexpr (ACT != ACT_IDENTITY) bt_r = ld4(beta + c0);
-        settle(gm_r);
-        settle(bt_r);
     }
-    const unsigned epoch = launch_epoch(wk);
-    const unsigned long long tag = (unsigned long long)epoch << 32;
+    // The launch's tag: its word is loaded here and used only from take_epoch
+    // on, which the tile loop calls after the first tiles' loads are issued
+    // (the scheduler would otherwise consume it right after the load and
+    // hold those loads back by its round trip).
+    unsigned ep_word = epoch_word(wk), epoch = 0u;
+    unsigned long long tag = 0ull;
+    auto take_epoch = [&]() {
+        asm volatile("" : "+v"(ep_word));
+        epoch = epoch_of(ep_word);
+        tag = (unsigned long long)epoch << 32;
+    };
     const WaitFail wf{wk.err, wk.hflag};
     // A spin limit of 0 lets no wait succeed: the launch flags itself as
     // timed out (the error path, forced from the host for its tests).
@@ -969,9 +988,21 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
             rs1 = rs_j;
         };
         int pb = 0;
+        // round 0's statistics and (in registers) gamma and beta right before
+        // the first two tiles' loads, settled after those are issued (see the
+        // forward)
         load_stats(0);
+        if constexpr (!kAffineLds) {
+            gm_r = ld4(gamma + c0);
+            if constexpr (ACT != ACT_IDENTITY) bt_r = ld4(beta + c0);
+        }
         issue(0, 0);
         issue(1, 1);
+        take_epoch();
+        if constexpr (!kAffineLds) {
+            settle(gm_r);
+            settle(bt_r);
+        }
         vm_wait<2 * NV + SH>();
         take(v, 0);
         issue(2, 0);
@@ -1036,6 +1067,8 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
             __syncthreads();
         }
     }
+
+    if (w >= nt) take_epoch();
 
     // dgamma/dbeta partials of this workgroup: lanes with equal column own the
     // same 4 channels; sum over the wave's rows, then over the waves in order.
