@@ -13,7 +13,10 @@
 // are combined across workgroups without anyone blocking on them:
 //
 //   tile       = TP pixel rows x CW4 float4 columns (a column block) of one
-//                sample; it covers GT = CW4 / (cpg/4) whole groups.
+//                sample; it covers GT = CW4 / (cpg/4) whole groups.  In the
+//                forward the rows of pixel tile t are t, t + T, t + 2T, ...
+//                (T tiles per sample), so the tiles streamed together read
+//                neighbouring rows; the backward's tiles are row blocks.
 //   grid       = P persistent workgroups (as many as the device holds at
 //                once), P a multiple of the tiles per sample, so workgroup w
 //                always owns the same (column block, pixel tile) position and
@@ -365,6 +368,9 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
 #pragma clang fp contract(fast)
     constexpr int NW = Gm::NW, NV = Gm::NV, GT = Gm::GT, TPB = Gm::TPB, CW4 = Gm::CW4;
     static_assert(NV == 4 && TPB * 16 == 16384, "stage slots as lds_take4 reads them");
+    // Tile rows interleaved one by one (RC = 1): same-box A/B at the
+    // north-star shape 365 -> 347 us against contiguous tiles.
+    constexpr int RC = 1;
     // Two stage buffers: the tiles of the next two rounds, written by
     // direct-to-LDS loads (round j takes buffer j % 2).  The tiles awaiting
     // phase B stay in registers.
@@ -387,7 +393,18 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
     const int cb = (w / T) % NCB;               // fixed column block of this workgroup
     const int t = w % T;                        // fixed pixel tile of this workgroup
     const int c0 = cb * CW4 * 4 + col * 4;      // first channel of this lane
-    const uint32_t voff = (uint32_t)(row0 * sh.C + c0) * 4u;
+    // The rows of a tile: RC consecutive rows at a time, tile t taking chunk t
+    // of every T chunks.  The T tiles of a sample and column block partition
+    // its rows for any RC, and the statistics merge over all of them; with
+    // RC = 1 the tiles a team streams at once read neighbouring rows rather
+    // than T separate blocks.
+    static_assert(RC == Gm::TP || Gm::RSTEP % RC == 0, "row chunks");
+    // local row r of tile t -> sample row (r / RC) T RC + t RC + r % RC
+    const int lrow = (row0 / RC) * T * RC + row0 % RC;  // this lane's first row, tile 0
+    constexpr bool kContig = RC == Gm::TP;
+    const uint32_t voff = (uint32_t)(lrow * sh.C + c0) * 4u;
+    const uint32_t rstep_rows = (uint32_t)(kContig ? Gm::RSTEP : Gm::RSTEP * T);
+    const uint32_t rstep_bytes = rstep_rows * (uint32_t)sh.C * 4u;
     const uint32_t row_bytes = (uint32_t)sh.C * 4u;
     // gamma and beta of this lane's channels, loaded once the first tile's
     // loads are out (at the tile loop's start)
@@ -446,11 +463,11 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
         const bool real = real_of(j);
         const __amdgpu_buffer_rsrc_t r =
             sample_rsrc(x + (size_t)(real ? b0 + j * spr : 0) * sh.HW * sh.C, real ? sh.sample_bytes : 0u);
-        const uint32_t base = (uint32_t)(t * Gm::TP) * row_bytes;
+        const uint32_t base = (uint32_t)(t * RC) * row_bytes;
         issue_shift(j);
 #pragma unroll
         for (int k = 0; k < NV; ++k)
-            dma16<NT>(r, &stage[sb][k * TPB + wid_s * kWave], voff, base + (uint32_t)(k * Gm::RSTEP) * row_bytes);
+            dma16<NT>(r, &stage[sb][k * TPB + wid_s * kWave], voff, base + (uint32_t)k * rstep_bytes);
     };
     auto take = [&](float4 (&v)[NV], int j) {
         if constexpr (SHIFT)
@@ -552,7 +569,7 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
         s0.y = fmaf(-sc.y, mean, bt.y);
         s0.z = fmaf(-sc.z, mean, bt.z);
         s0.w = fmaf(-sc.w, mean, bt.w);
-        float* ys = y + (size_t)b * sh.HW * sh.C + (size_t)(t * Gm::TP + row0) * sh.C + c0;
+        float* ys = y + (size_t)b * sh.HW * sh.C + (size_t)(lrow + t * RC) * sh.C + c0;
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
             float4 o;
@@ -560,7 +577,7 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
             o.y = act_fwd<ACT>(fmaf(v[k].y, sc.y, s0.y));
             o.z = act_fwd<ACT>(fmaf(v[k].z, sc.z, s0.z));
             o.w = act_fwd<ACT>(fmaf(v[k].w, sc.w, s0.w));
-            stS<NT>(ys + (size_t)(k * Gm::RSTEP) * sh.C, o);
+            stS<NT>(ys + (size_t)(k * rstep_rows) * sh.C, o);
         }
     };
 
@@ -681,6 +698,10 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
 #pragma clang fp contract(fast)
     constexpr int NW = Gm::NW, NV = Gm::NV, GT = Gm::GT, TPB = Gm::TPB, CW4 = Gm::CW4;
     static_assert(NV == 2 && TPB * 16 == 16384, "stage slots (x then dy) as lds_take4 reads them");
+    // Tile rows contiguous (one chunk of TP rows).  Measured against the
+    // forward's interleaved rows at the north-star shape (same-box A/B): rows in
+    // chunks of 16, 4, 2 and 1 gave 524, 535, 526 and 540 us against 508 us.
+    constexpr int RC = Gm::TP;
     // Two stage buffers (x then dy of the tiles of the next two rounds,
     // direct-to-LDS loads); the tiles awaiting phase B (xhat, g) stay in
     // registers.
@@ -706,7 +727,18 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
     const int t = w % T;
     const int c0 = cb * CW4 * 4 + col * 4;
     const int gglob = cb * GT + gl;             // global group index of this lane
-    const uint32_t voff = (uint32_t)(row0 * sh.C + c0) * 4u;
+    // The rows of a tile: RC consecutive rows at a time, tile t taking chunk t
+    // of every T chunks.  The T tiles of a sample and column block partition
+    // its rows for any RC, and the statistics merge over all of them; with
+    // RC = 1 the tiles a team streams at once read neighbouring rows rather
+    // than T separate blocks.
+    static_assert(RC == Gm::TP || Gm::RSTEP % RC == 0, "row chunks");
+    // local row r of tile t -> sample row (r / RC) T RC + t RC + r % RC
+    const int lrow = (row0 / RC) * T * RC + row0 % RC;  // this lane's first row, tile 0
+    constexpr bool kContig = RC == Gm::TP;
+    const uint32_t voff = (uint32_t)(lrow * sh.C + c0) * 4u;
+    const uint32_t rstep_rows = (uint32_t)(kContig ? Gm::RSTEP : Gm::RSTEP * T);
+    const uint32_t rstep_bytes = rstep_rows * (uint32_t)sh.C * 4u;
     const uint32_t row_bytes = (uint32_t)sh.C * 4u;
     // gamma and beta of this lane's channels: held in registers (loaded once
     // the first tile's loads are out, at the tile loop's start), or, where
@@ -776,15 +808,14 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
         const uint32_t bytes = real ? sh.sample_bytes : 0u;
         const __amdgpu_buffer_rsrc_t rx = sample_rsrc(x + so, bytes);
         const __amdgpu_buffer_rsrc_t rd = sample_rsrc(dy + so, bytes);
-        const uint32_t base = (uint32_t)(t * Gm::TP) * row_bytes;
+        const uint32_t base = (uint32_t)(t * RC) * row_bytes;
         issue_shift(j);
 #pragma unroll
         for (int k = 0; k < NV; ++k)
-            dma16<NT>(rx, &stage[sb][k * TPB + wid_s * kWave], voff, base + (uint32_t)(k * Gm::RSTEP) * row_bytes);
+            dma16<NT>(rx, &stage[sb][k * TPB + wid_s * kWave], voff, base + (uint32_t)k * rstep_bytes);
 #pragma unroll
         for (int k = 0; k < NV; ++k)
-            dma16<NT>(rd, &stage[sb][(NV + k) * TPB + wid_s * kWave], voff,
-                base + (uint32_t)(k * Gm::RSTEP) * row_bytes);
+            dma16<NT>(rd, &stage[sb][(NV + k) * TPB + wid_s * kWave], voff, base + (uint32_t)k * rstep_bytes);
     };
     auto take = [&](float4 (&v)[2 * NV], int j) {
         if constexpr (SHIFT)
@@ -929,7 +960,7 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
         // dx = rs * ((g - m1) - xhat * m2) = g * rs + (xhat * (-rs m2) + (-rs m1))
         const float2 st = stat[pb][gl];
         const float a1 = -rsv * st.x, a2 = -rsv * st.y;
-        float* dxs = dx + (size_t)b * sh.HW * sh.C + (size_t)(t * Gm::TP + row0) * sh.C + c0;
+        float* dxs = dx + (size_t)b * sh.HW * sh.C + (size_t)(lrow + t * RC) * sh.C + c0;
         float4 cs = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
@@ -940,7 +971,7 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
             o.y = fmaf(g.y, rsv, fmaf(xh.y, a2, a1));
             o.z = fmaf(g.z, rsv, fmaf(xh.z, a2, a1));
             o.w = fmaf(g.w, rsv, fmaf(xh.w, a2, a1));
-            stS<NT>(dxs + (size_t)(k * Gm::RSTEP) * sh.C, o);
+            stS<NT>(dxs + (size_t)(k * rstep_rows) * sh.C, o);
             if constexpr (SHIFT) {
                 cs.x += o.x;
                 cs.y += o.y;
