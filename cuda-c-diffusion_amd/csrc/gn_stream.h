@@ -314,6 +314,16 @@ __device__ __forceinline__ void for_xor_levels(int n, F f) {
     if (n > 32) f(xlevel<32>{});
 }
 
+// A run-time tree size as a scalar the compiler cannot see through, taken
+// inside the tile loop: the level tests above then stay scalar compares and
+// branches on it.  In the forward's loop the tests were otherwise hoisted
+// out as lane masks, which ran out of scalar registers and came back
+// through vector-lane spills (four vector instructions per level and round).
+__device__ __forceinline__ int lpg_scalar(int n) {
+    asm volatile("" : "+s"(n));
+    return n;
+}
+
 // Lanes that share this lane's group inside a wave: the column bits inside
 // the group (levels 1 .. CPG4 / 2), then the row bits of the wave (CW4 .. 32).
 template <class Gm, class F>
@@ -546,11 +556,12 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
                 }
             }
         }
-        for_xor_levels(LPG, [&](auto o) {
-            xmerge_eq<decltype(o)::value>(m, q, n);
-            n *= 2.0f;
+        // at level o each partial covers ntile * RPL * o values (a constant);
+        // the group's total, HW * cpg, is a power of two, so q * inv_n is q / n
+        for_xor_levels(lpg_scalar(LPG), [&](auto o) {
+            xmerge_eq<decltype(o)::value>(m, q, ntile * (float)(RPL * decltype(o)::value));
         });
-        if (merger && rj == 0) stat[pb][rg] = make_float2(m, rsqrtf(q / n + eps));
+        if (merger && rj == 0) stat[pb][rg] = make_float2(m, rsqrtf(q * sh.inv_n + eps));
         lds_barrier();
         const float2 st = stat[pb][gl];
         const float mean = st.x, rs = st.y;
