@@ -557,10 +557,16 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
             }
         }
         // at level o each partial covers ntile * RPL * o values (a constant);
-        // the group's total, HW * cpg, is a power of two, so q * inv_n is q / n
-        for_xor_levels(lpg_scalar(LPG), [&](auto o) {
-            xmerge_eq<decltype(o)::value>(m, q, ntile * (float)(RPL * decltype(o)::value));
-        });
+        // the group's total, HW * cpg, is a power of two, so q * inv_n is q / n.
+        // A wave with no merging lane skips the tree (its values go unused);
+        // the test is on scalars, so each wave runs the tree whole or not at
+        // all.  Not with SHIFT: there the branch costs the loop vector-lane
+        // spills of scalar registers.  Not without an activation: there the
+        // loop is not short of vector issue, and the skip measured no gain.
+        if (SHIFT || ACT == ACT_IDENTITY || wid_s * kWave < GT * LPG)
+            for_xor_levels(lpg_scalar(LPG), [&](auto o) {
+                xmerge_eq<decltype(o)::value>(m, q, ntile * (float)(RPL * decltype(o)::value));
+            });
         if (merger && rj == 0) stat[pb][rg] = make_float2(m, rsqrtf(q * sh.inv_n + eps));
         lds_barrier();
         const float2 st = stat[pb][gl];
