@@ -400,6 +400,58 @@ def test_mp_fourier_special_values_and_unit_power(orc, rng):
     assert abs(float(np.mean(out.astype(np.float64) ** 2)) - 1.0) < 0.02
 
 
+def test_mp_fourier_closed_form_products(orc):
+    """out[b,k] = sqrt(2) cos(2 pi x[b] f[k]) at phase 0, with x[b] f[k] an exact
+    number of eighth (and one sixteenth) turns, so every entry is a closed-form
+    constant: 0, +-1, +-sqrt(2) or sqrt(2) cos(pi/8).  Batch 5 != C 4 and both
+    x and f vary, so an oracle that dropped x, added x + f or read x[k] f[b]
+    misses this table (reference src/kernels.cu:385-394)."""
+    r2, c16 = np.sqrt(2.0), np.sqrt(2.0) * np.cos(np.pi / 8)
+    x = np.array([0.25, 0.5, 0.125, 0.75, -0.25], np.float32)
+    f = np.array([1.0, 2.0, 4.0, 0.5], np.float32)
+    want = np.array([
+        [0.0, -r2, r2, 1.0],      # x f = 1/4, 1/2, 1, 1/8 turns
+        [-r2, r2, r2, 0.0],       # 1/2, 1, 2, 1/4
+        [1.0, 0.0, -r2, c16],     # 1/8, 1/4, 1/2, 1/16
+        [0.0, -r2, r2, -1.0],     # 3/4, 3/2, 3, 3/8
+        [0.0, -r2, r2, 1.0],      # -1/4, -1/2, -1, -1/8
+    ])
+    # The float argument 6.28318530718f * (x f + phase) is off 2 pi (x f + phase)
+    # by at most ~1.6e-6 rad at 3.75 turns, hence the 5e-6 tolerance on entries
+    # of size sqrt(2); every planted mistake moves an entry by O(1).
+    out = orc.mp_fourier(x, f, np.zeros(4, np.float32))
+    assert out.shape == (5, 4)
+    np.testing.assert_allclose(out, want, atol=5e-6)
+    # the phase adds whole and fractional turns to x f
+    ph = np.array([0.25, 0.5, 0.75, 0.0], np.float32)
+    want_ph = np.array([
+        [-r2, r2, 0.0, 1.0],      # 1/2, 1, 7/4, 1/8 turns
+        [0.0, -r2, 0.0, 0.0],     # 3/4, 3/2, 11/4, 1/4
+        [-1.0, 0.0, 0.0, c16],    # 3/8, 3/4, 5/4, 1/16
+        [r2, r2, 0.0, -1.0],      # 1, 2, 15/4, 3/8
+        [r2, r2, 0.0, 1.0],       # 0, 0, -1/4, -1/8
+    ])
+    out = orc.mp_fourier(x, f, ph)
+    np.testing.assert_allclose(out, want_ph, atol=5e-6)
+
+
+def test_mp_fourier_rows_follow_x_columns_follow_f(orc, rng):
+    """Permuting x permutes the output rows, permuting (f, phase) together
+    permutes its columns, bit for bit; changing one x changes only its row."""
+    x = rng.standard_normal(7).astype(np.float32)
+    f = rng.standard_normal(11).astype(np.float32)
+    ph = rng.uniform(0, 1, 11).astype(np.float32)
+    out = orc.mp_fourier(x, f, ph)
+    px, pf = rng.permutation(7), rng.permutation(11)
+    assert np.array_equal(orc.mp_fourier(x[px], f, ph), out[px])
+    assert np.array_equal(orc.mp_fourier(x, f[pf], ph[pf]), out[:, pf])
+    x2 = x.copy()
+    x2[3] += np.float32(0.37)
+    out2 = orc.mp_fourier(x2, f, ph)
+    rows = np.any(out2 != out, axis=1)
+    assert rows.tolist() == [False, False, False, True, False, False, False]
+
+
 def test_sinusoidal_special_values(orc):
     C, L = 256, float(np.float32(np.log(10000.0)))
     out = orc.sinusoidal(np.zeros(1, np.float32), C, L)
