@@ -46,6 +46,7 @@ LL = C.c_longlong
 _SIGS = {
     # runtime plumbing (nn_hip_rt.h)
     "nnhip_get_last_error": (I, [C.c_char_p, I], False),
+    "nnhip_launch_allocations": (C.c_ulonglong, [], False),
     "nnhip_device_count": (I, [], False),
     "nnhip_set_device": (I, [I], False),
     "nnhip_device_info": (I, [C.c_char_p, I], False),
@@ -124,6 +125,7 @@ _SIGS = {
     "launch_groupnorm_act_shift_forward_ws": (None, [P, P, P, P, P, P, P, I, I, I, I, F, I, P, P], True),
     "launch_groupnorm_act_shift_backward_ws": (None, [P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, P, P], True),
     "nnhip_groupnorm_shift_backward_workspace": (SZ, [I, I, I, I], False),
+    "nnhip_groupnorm_shift_supported": (I, [I, I, I, I, I], False),
     "launch_layernorm_backward_ws": (None, [P, P, P, P, P, P, P, P, I, I, P, P], True),
     "launch_col2im_set": (None, [P, P, I, I, I, I, I, I, I, I, I, P], True),
     "nnhip_multi_tensor_plan_create": (P, [P, I], True),

@@ -1248,3 +1248,7 @@ bool nnk_gns_forward(int act, float* y, float* mu, float* rstd, const float* x, 
 bool nnk_gns_backward(int act, float* dx, float* ggamma, float* gbeta, const float* dy, const float* x,
     const float* gamma, const float* beta, const float* mu, const float* rstd, const float* shift, float* gshift,
     int B, int HW, int C, int G, float* ws, hipStream_t s);
+// Whether nnk_gns_forward / nnk_gns_backward have a kernel for a shift on this
+// shape and activation (the grid's fit on the device aside).
+bool nnk_gns_shift_forward_shape_ok(int act, int B, int HW, int C, int G);
+bool nnk_gns_shift_backward_shape_ok(int act, int B, int HW, int C, int G);

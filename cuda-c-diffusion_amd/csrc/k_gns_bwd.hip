@@ -50,7 +50,7 @@ bool launch(const Plan& p, float* dx, float* ggamma, float* gbeta, const float* 
     Shape sh = p.sh;
     Work wk;
     wk.err = reinterpret_cast<unsigned*>(ws);
-    unsigned* hf = nnk_wait_flag(s);
+    unsigned* hf = nnk_wait_flag();
     wk.hflag = hf ? hf : wk.err;
     wk.ep = reinterpret_cast<unsigned*>(ws) + 1;
     wk.count = reinterpret_cast<unsigned*>(reinterpret_cast<char*>(ws) + kCountOffset);
@@ -85,8 +85,7 @@ bool by_shape(const Plan& p, float* dx, float* ggamma, float* gbeta, const float
                         shift, gshift, ws, s);
     // With a shift, one record per merging lane: with two, the tile loop runs
     // out of registers and would spill inside the loop (a spill reload is a
-    // full wait on the staged loads); the launcher composes the plain kernel
-    // on a pooled x + shift instead.
+    // full wait on the staged loads); the launcher refuses those shapes.
     NNK_GNS_BWD_CASE(1, 1)
     NNK_GNS_BWD_CASE(2, 1)
     NNK_GNS_BWD_CASE(4, 1)
@@ -100,6 +99,11 @@ bool by_shape(const Plan& p, float* dx, float* ggamma, float* gbeta, const float
 }
 
 }  // namespace
+
+bool nnk_gns_shift_backward_shape_ok(int act, int B, int HW, int C, int G) {
+    const Plan p = make_plan(true, B, HW, C, G);
+    return p.ok && act == ACT_SILU && p.rpl == 1;  // the SHIFT cases of by_shape
+}
 
 bool nnk_gns_backward(int act, float* dx, float* ggamma, float* gbeta, const float* dy, const float* x,
     const float* gamma, const float* beta, const float* mu, const float* rstd, const float* shift, float* gshift,

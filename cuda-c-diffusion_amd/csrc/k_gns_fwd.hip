@@ -24,7 +24,7 @@ bool launch(const Plan& p, float* y, float* mu, float* rstd, const float* x, con
     Shape sh = p.sh;
     Work wk;
     wk.err = reinterpret_cast<unsigned*>(ws);
-    unsigned* hf = nnk_wait_flag(s);
+    unsigned* hf = nnk_wait_flag();
     wk.hflag = hf ? hf : wk.err;
     wk.ep = reinterpret_cast<unsigned*>(ws) + 1;
     wk.count = reinterpret_cast<unsigned*>(reinterpret_cast<char*>(ws) + kCountOffset);
@@ -47,8 +47,7 @@ bool by_shape(const Plan& p, float* y, float* mu, float* rstd, const float* x, c
                   : launch<ACT, CPG4, RPL, false, SHIFT>(p, y, mu, rstd, x, gamma, beta, shift, eps, ws, s);
     // With a shift, 8 or 16 channels per group: at 4 the tile loop runs out
     // of registers and would spill inside the loop (a spill reload is a full
-    // wait on the staged loads); the launcher composes the plain kernel on a
-    // pooled x + shift instead.
+    // wait on the staged loads); the launcher refuses those shapes.
     if constexpr (SHIFT) {
         NNK_GNS_FWD_CASE(2, 1)
         NNK_GNS_FWD_CASE(2, 2)
@@ -68,13 +67,17 @@ bool by_shape(const Plan& p, float* y, float* mu, float* rstd, const float* x, c
 
 }  // namespace
 
+bool nnk_gns_shift_forward_shape_ok(int act, int B, int HW, int C, int G) {
+    const Plan p = make_plan(false, B, HW, C, G);
+    return p.ok && act == ACT_SILU && (p.cpg4 == 2 || p.cpg4 == 4);  // the SHIFT cases of by_shape
+}
+
 bool nnk_gns_forward(int act, float* y, float* mu, float* rstd, const float* x, const float* gamma,
     const float* beta, const float* shift, int B, int HW, int C, int G, float eps, float* ws, hipStream_t s) {
     const Plan p = make_plan(false, B, HW, C, G);
     if (!p.ok || !ws) return false;
     bool launched = false;
-    // with a shift: SiLU only (the DDPM block's GN2); other activations take
-    // the launcher's composed path
+    // with a shift: SiLU only (the DDPM block's GN2)
     if (shift)
         launched = act == ACT_SILU &&
             by_shape<ACT_SILU, true>(p, y, mu, rstd, x, gamma, beta, shift, eps, ws, s);

@@ -268,9 +268,8 @@ bool want_stream(bool bwd, int B, int HW, int C, int G, bool reg_ok) {
 // the per-tile column sums (plain floats past the epoch-tagged region, which
 // alone needs clearing).
 template <class F>
-bool try_stream(bool bwd, int B, int HW, int C, int G, bool reg_ok, float* ws, hipStream_t s, const char* what,
-    F launch, bool shift = false) {
-    if (!want_stream(bwd, B, HW, C, G, reg_ok)) return false;
+bool run_stream(bool bwd, int B, int HW, int C, int G, float* ws, hipStream_t s, const char* what, F launch,
+    bool shift = false) {
     const nnk::gns::Plan p = nnk::gns::make_plan(bwd, B, HW, C, G);
     float* w = ws;
     if (!w) {
@@ -281,6 +280,12 @@ bool try_stream(bool bwd, int B, int HW, int C, int G, bool reg_ok, float* ws, h
     const bool ok = launch(w);
     if (!ws) nnk_scratch_release(w, s);
     return ok;
+}
+
+template <class F>
+bool try_stream(bool bwd, int B, int HW, int C, int G, bool reg_ok, float* ws, hipStream_t s, const char* what,
+    F launch, bool shift = false) {
+    return want_stream(bwd, B, HW, C, G, reg_ok) && run_stream(bwd, B, HW, C, G, ws, s, what, launch, shift);
 }
 
 // Offset (floats) of the register path's channel partials in a backward
@@ -320,6 +325,20 @@ void gn_forward_impl(const char* what, float* y, float* mu, float* rstd, const f
     nnk_after_launch(what, s);
 }
 
+// Whether a backward on these pointers and this shape takes the streaming
+// kernels (the choice gn_backward_impl makes; it falls back to the register
+// or generic path only if the streaming launch itself is refused).
+bool bwd_stream_selected(const float* dx, const float* dy, const float* x, const float* gamma, const float* beta,
+    int B, int HW, int C, int G, int act) {
+    const bool stream_aligned = aligned16(x) && aligned16(dy) && aligned16(dx) && aligned16(gamma) &&
+        (act == ACT_IDENTITY || aligned16(beta));
+    if (!stream_aligned) return false;
+    int cfg = -1;
+    const bool reg_ok =
+        reg_v4pp(C / G, HW, x, dy, dx, gamma, cfg) != 0 && (act == ACT_IDENTITY || aligned16(beta));
+    return want_stream(true, B, HW, C, G, reg_ok);
+}
+
 // ws: a lent workspace (nullptr: draw from the stream's pool block).
 // reg_ws: where the register and generic paths keep their 2 * B * C channel
 // partials (nullptr: in ws past its streaming region, or in the pool block).
@@ -337,20 +356,13 @@ void gn_backward_impl(const char* what, float* dx, float* ggamma, float* gbeta, 
     NNK_REQUIRE(dx && dy && x && gamma && mu && rstd, what, "%s: null pointer", what);
     NNK_REQUIRE(act == ACT_IDENTITY || beta, what, "%s: beta is required with an activation", what);
     NNK_REQUIRE(ws == nullptr || aligned16(ws), what, "%s: workspace must be 16-byte aligned", what);
-    {
-        const bool stream_aligned = aligned16(x) && aligned16(dy) && aligned16(dx) && aligned16(gamma) &&
-            (act == ACT_IDENTITY || aligned16(beta));
-        int cfg = -1;
-        const bool reg_ok = reg_v4pp(C / G, HW, x, dy, dx, gamma, cfg) != 0 &&
-            (act == ACT_IDENTITY || aligned16(beta));
-        if (stream_aligned &&
-            try_stream(true, B, HW, C, G, reg_ok, ws, s, what, [&](float* w) {
-                return nnk_gns_backward(act, dx, ggamma, gbeta, dy, x, gamma, beta, mu, rstd, nullptr, nullptr, B,
-                    HW, C, G, w, s);
-            })) {
-            nnk_after_launch(what, s);
-            return;
-        }
+    if (bwd_stream_selected(dx, dy, x, gamma, beta, B, HW, C, G, act) &&
+        run_stream(true, B, HW, C, G, ws, s, what, [&](float* w) {
+            return nnk_gns_backward(act, dx, ggamma, gbeta, dy, x, gamma, beta, mu, rstd, nullptr, nullptr, B, HW,
+                C, G, w, s);
+        })) {
+        nnk_after_launch(what, s);
+        return;
     }
     float* scratch = reg_ws ? reg_ws : ws;
     const size_t part_off = (ws && !reg_ws) ? reg_partials_offset(B, HW, C, G) : 0;
@@ -382,45 +394,43 @@ void gn_backward_impl(const char* what, float* dx, float* ggamma, float* gbeta, 
     nnk_after_launch(what, s);
 }
 
-// x + shift[b, c] into a block of the stream's pool: the input of the
-// composition that the shift launchers fall back to (the reference's
-// broadcast add, src/conv_residual.c:34, one rounding per element).
-float* shifted_copy(const float* x, const float* shift, int B, int HW, int C, hipStream_t s, const char* what) {
-    const size_t n = (size_t)B * HW * C;
-    float* xs = nnk_scratch_acquire(n, s, what);
-    if (!xs) return nullptr;
-    const hipError_t e = hipMemcpyAsync(xs, x, n * sizeof(float), hipMemcpyDeviceToDevice, s);
-    if (e != hipSuccess) {
-        nnk_set_error((int)e, "%s: copy of the input: %s", what, hipGetErrorString(e));
-        nnk_scratch_release(xs, s);
-        return nullptr;
-    }
-    launch_spatial_add(xs, shift, B, HW, 1, C, s);
-    return xs;
+// Whether the shift launchers run their fused kernels on this shape, given
+// 16-byte aligned pointers: a streaming plan with a shift kernel for it, and
+// the path policy choosing the streaming kernels (as for the plain launchers).
+bool shift_fused(bool bwd, int B, int HW, int C, int G, int act) {
+    if (B <= 0 || HW <= 0 || C <= 0 || G <= 0 || C % G != 0) return false;
+    if (!(bwd ? nnk_gns_shift_backward_shape_ok(act, B, HW, C, G) : nnk_gns_shift_forward_shape_ok(act, B, HW, C, G)))
+        return false;
+    const void* aligned = reinterpret_cast<const void*>(uintptr_t(256));
+    int cfg = -1;
+    const bool reg_ok = reg_v4pp(C / G, HW, aligned, aligned, aligned, aligned, cfg) != 0;
+    return want_stream(bwd, B, HW, C, G, reg_ok);
 }
 
+// The shift launchers only ever run the fused kernels, on the caller's
+// workspace: a shape those kernels do not take is refused (the caller adds
+// the shift itself, as the reference does, and calls the plain launchers).
 void gn_shift_forward_impl(const char* what, float* y, float* mu, float* rstd, const float* x, const float* shift,
     const float* gamma, const float* beta, int B, int HW, int C, int G, float eps, int act, float* ws,
     hipStream_t s) {
     if (!shape_ok(what, B, HW, C, G)) return;
     NNK_REQUIRE(valid_act(act), what, "%s: unknown activation %d", what, act);
     if (B == 0) return;
-    NNK_REQUIRE(y && mu && rstd && x && shift && gamma && beta, what, "%s: null pointer", what);
-    NNK_REQUIRE(ws == nullptr || aligned16(ws), what, "%s: workspace must be 16-byte aligned", what);
-    int cfg = -1;
-    const bool reg_ok = reg_v4pp(C / G, HW, x, y, gamma, beta, cfg) != 0;
-    const bool stream_aligned =
-        aligned16(x) && aligned16(y) && aligned16(gamma) && aligned16(beta) && aligned16(shift);
-    if (stream_aligned && try_stream(false, B, HW, C, G, reg_ok, ws, s, what, [&](float* w) {
+    NNK_REQUIRE(y && mu && rstd && x && shift && gamma && beta && ws, what, "%s: null pointer", what);
+    NNK_REQUIRE(aligned16(x) && aligned16(y) && aligned16(gamma) && aligned16(beta) && aligned16(shift) &&
+            aligned16(ws),
+        what, "%s: pointers must be 16-byte aligned", what);
+    NNK_REQUIRE(shift_fused(false, B, HW, C, G, act), what,
+        "%s: [%d, %d, %d] G=%d, activation %d is not taken by the fused shift kernels "
+        "(nnhip_groupnorm_shift_supported); add the shift with launch_spatial_add and call "
+        "launch_groupnorm_act_forward_ws", what, B, HW, C, G, act);
+    if (!run_stream(false, B, HW, C, G, ws, s, what, [&](float* w) {
             return nnk_gns_forward(act, y, mu, rstd, x, gamma, beta, shift, B, HW, C, G, eps, w, s);
         })) {
-        nnk_after_launch(what, s);
+        nnk_set_error(hipErrorLaunchFailure, "%s: the persistent grid does not fit the device", what);
         return;
     }
-    float* xs = shifted_copy(x, shift, B, HW, C, s, what);
-    if (!xs) return;
-    gn_forward_impl(what, y, mu, rstd, xs, gamma, beta, B, HW, C, G, eps, act, ws, s);
-    nnk_scratch_release(xs, s);
+    nnk_after_launch(what, s);
 }
 
 void gn_shift_backward_impl(const char* what, float* dx, float* gshift, float* ggamma, float* gbeta,
@@ -428,37 +438,27 @@ void gn_shift_backward_impl(const char* what, float* dx, float* gshift, float* g
     const float* rstd, int B, int HW, int C, int G, int act, float* ws, hipStream_t s) {
     if (!shape_ok(what, B, HW, C, G)) return;
     NNK_REQUIRE(valid_act(act), what, "%s: unknown activation %d", what, act);
-    NNK_REQUIRE(ggamma && gbeta, what, "%s: null pointer", what);
+    NNK_REQUIRE(ggamma && gbeta && ws, what, "%s: null pointer", what);
     if (B == 0) {
         gn_backward_impl(what, dx, ggamma, gbeta, dy, x, gamma, beta, mu, rstd, B, HW, C, G, act, ws, s);
         return;
     }
-    NNK_REQUIRE(dx && gshift && dy && x && shift && gamma && mu && rstd, what, "%s: null pointer", what);
-    NNK_REQUIRE(act == ACT_IDENTITY || beta, what, "%s: beta is required with an activation", what);
-    NNK_REQUIRE(ws == nullptr || aligned16(ws), what, "%s: workspace must be 16-byte aligned", what);
-    {
-        const bool stream_aligned = aligned16(x) && aligned16(dy) && aligned16(dx) && aligned16(gamma) &&
-            aligned16(shift) && (act == ACT_IDENTITY || aligned16(beta));
-        int cfg = -1;
-        const bool reg_ok = reg_v4pp(C / G, HW, x, dy, dx, gamma, cfg) != 0 &&
-            (act == ACT_IDENTITY || aligned16(beta));
-        if (stream_aligned &&
-            try_stream(
-                true, B, HW, C, G, reg_ok, ws, s, what,
-                [&](float* w) {
-                    return nnk_gns_backward(act, dx, ggamma, gbeta, dy, x, gamma, beta, mu, rstd, shift, gshift,
-                        B, HW, C, G, w, s);
-                },
-                true)) {
-            nnk_after_launch(what, s);
-            return;
-        }
+    NNK_REQUIRE(dx && gshift && dy && x && shift && gamma && beta && mu && rstd, what, "%s: null pointer", what);
+    NNK_REQUIRE(aligned16(x) && aligned16(dy) && aligned16(dx) && aligned16(gamma) && aligned16(beta) &&
+            aligned16(shift) && aligned16(ws),
+        what, "%s: pointers must be 16-byte aligned", what);
+    NNK_REQUIRE(shift_fused(true, B, HW, C, G, act), what,
+        "%s: [%d, %d, %d] G=%d, activation %d is not taken by the fused shift kernels "
+        "(nnhip_groupnorm_shift_supported); call launch_groupnorm_act_backward_ws on x + shift and "
+        "launch_spatial_reduce_sum_ws on its dx", what, B, HW, C, G, act);
+    if (!run_stream(true, B, HW, C, G, ws, s, what, [&](float* w) {
+            return nnk_gns_backward(act, dx, ggamma, gbeta, dy, x, gamma, beta, mu, rstd, shift, gshift, B, HW, C,
+                G, w, s);
+        })) {
+        nnk_set_error(hipErrorLaunchFailure, "%s: the persistent grid does not fit the device", what);
+        return;
     }
-    float* xs = shifted_copy(x, shift, B, HW, C, s, what);
-    if (!xs) return;
-    gn_backward_impl(what, dx, ggamma, gbeta, dy, xs, gamma, beta, mu, rstd, B, HW, C, G, act, ws, s);
-    nnk_scratch_release(xs, s);
-    launch_spatial_reduce_sum(gshift, dx, B, HW, C, s);
+    nnk_after_launch(what, s);
 }
 
 }  // namespace
@@ -577,7 +577,11 @@ void launch_groupnorm_act_backward_noalloc(float* dx, float* ggamma, float* gbet
     int batch, int HW, int C, int G, Activation act, hipStream_t s) {
     const char* what = "launch_groupnorm_act_backward_noalloc";
     if (!shape_ok(what, batch, HW, C, G)) return;
-    const size_t stream_bytes = reg_partials_offset(batch, HW, C, G) * sizeof(float);
+    // The streaming kernels' workspace counts only when they will run; the
+    // register and generic paths (also the streaming path's fallback) keep
+    // their 2 * batch * C channel partials in the second region.
+    const bool stream = batch > 0 && bwd_stream_selected(dx, dy, x, gamma, beta, batch, HW, C, G, (int)act);
+    const size_t stream_bytes = stream ? reg_partials_offset(batch, HW, C, G) * sizeof(float) : 0;
     const size_t partial_bytes = (size_t)2 * batch * C * sizeof(float);
     NNK_REQUIRE(stream_bytes <= kNoAllocStreamBytes && partial_bytes <= kNoAllocPartialBytes, what,
         "%s: [%d, %d, %d] G=%d needs %zu + %zu bytes of scratch, more than its %zu + %zu (use "
@@ -606,6 +610,11 @@ void launch_groupnorm_act_shift_backward_ws(float* dx, float* gshift, float* gga
     const float* rstd, int batch, int HW, int C, int G, Activation act, float* workspace, hipStream_t s) {
     gn_shift_backward_impl("launch_groupnorm_act_shift_backward_ws", dx, gshift, ggamma, gbeta, dy, x, shift,
         gamma, beta, mu, rstd, batch, HW, C, G, (int)act, workspace, s);
+}
+
+int nnhip_groupnorm_shift_supported(int batch, int HW, int C, int G, Activation act) {
+    return (shift_fused(false, batch, HW, C, G, (int)act) ? 1 : 0) |
+        (shift_fused(true, batch, HW, C, G, (int)act) ? 2 : 0);
 }
 
 size_t nnhip_groupnorm_shift_backward_workspace(int batch, int HW, int C, int G) {

@@ -459,10 +459,10 @@ void nnk_scratch_forget_stream(hipStream_t s);
 // kernel, so that the sequence can be captured in a graph).
 void nnk_clear_workspace(float* ws, size_t n_floats, hipStream_t s);
 // Device address of the process-wide host-mapped word that a streaming
-// kernel's bounded wait sets when it gives up (see WaitFail), allocated by
-// the first call outside stream capture; nullptr before that or when it
-// could not be allocated.
-unsigned* nnk_wait_flag(hipStream_t s);
+// kernel's bounded wait sets when it gives up (see WaitFail).  It is
+// allocated when the library is loaded, never by a launcher; nullptr when
+// that allocation failed (no device at load time).
+unsigned* nnk_wait_flag();
 
 #define NNK_REQUIRE(cond, what, ...)                         \
     do {                                                     \

@@ -64,15 +64,39 @@ bool nnk_capturing(hipStream_t s) {
     return s && hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
 }
 
+// Allocations the launch layer makes by itself (the scratch pools, their
+// blocks and the wait flag below), counted for tests of the allocation-free
+// entry points.  Explicit requests (nnhip_malloc, multi-tensor plans, module
+// arenas) are not counted.
+namespace {
+unsigned long long g_hidden_allocs = 0;  // updated under a lock or at load
+}
+
 // The process-wide word that a streaming kernel's bounded wait sets when it
 // gives up: host memory mapped into the device's address space (coherent, so
-// the kernel's system-scope store is visible to the host once it is done),
-// allocated on first use and kept until the process ends.
+// the kernel's system-scope store is visible to the host once it is done).
+// It is allocated once, when the library is loaded, and kept until the
+// process ends, so that no launcher allocates it (the allocation-free entry
+// point included).  Without a device at load time it stays absent and wait
+// failures are reported through the workspace's own word only.
 namespace {
-std::mutex g_wait_flag_mu;
 unsigned* g_wait_flag_host = nullptr;
 unsigned* g_wait_flag_dev = nullptr;
-bool g_wait_flag_failed = false;
+
+__attribute__((constructor)) void create_wait_flag() {
+    void* p = nullptr;
+    void* d = nullptr;
+    if (hipHostMalloc(&p, 64, hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess || !p ||
+        hipHostGetDevicePointer(&d, p, 0) != hipSuccess || !d) {
+        (void)hipGetLastError();
+        if (p) (void)hipHostFree(p);
+        return;
+    }
+    memset(p, 0, 64);
+    ++g_hidden_allocs;
+    g_wait_flag_dev = static_cast<unsigned*>(d);
+    __atomic_store_n(&g_wait_flag_host, static_cast<unsigned*>(p), __ATOMIC_RELEASE);
+}
 
 // Move a wait failure the device has flagged into the error record.
 void take_wait_flag() {
@@ -84,27 +108,7 @@ void take_wait_flag() {
 }
 }  // namespace
 
-unsigned* nnk_wait_flag(hipStream_t s) {
-    std::lock_guard<std::mutex> lock(g_wait_flag_mu);
-    // allocated outside stream capture only (a capture that comes first
-    // reports wait failures through the workspace word alone)
-    if (!g_wait_flag_dev && !g_wait_flag_failed && !nnk_capturing(s)) {
-        void* p = nullptr;
-        void* d = nullptr;
-        if (hipHostMalloc(&p, 64, hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess || !p ||
-            hipHostGetDevicePointer(&d, p, 0) != hipSuccess || !d) {
-            (void)hipGetLastError();
-            if (p) (void)hipHostFree(p);
-            g_wait_flag_failed = true;
-            nnk_path_note("host-mapped wait flag: allocation failed; wait failures are reported per workspace only");
-        } else {
-            memset(p, 0, 64);
-            g_wait_flag_dev = static_cast<unsigned*>(d);
-            __atomic_store_n(&g_wait_flag_host, static_cast<unsigned*>(p), __ATOMIC_RELEASE);
-        }
-    }
-    return g_wait_flag_dev;
-}
+unsigned* nnk_wait_flag() { return g_wait_flag_dev; }
 
 void nnk_after_launch(const char* what, hipStream_t s) {
     hipError_t e = hipGetLastError();
@@ -168,6 +172,7 @@ hipMemPool_t scratch_pool(int dev, const char* what) {
         hipMemPool_t pool = nullptr;
         hipError_t e = hipMemPoolCreate(&pool, &props);
         if (e == hipSuccess) {
+            ++g_hidden_allocs;
             uint64_t keep = UINT64_MAX;
             e = hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
             if (e != hipSuccess) (void)hipMemPoolDestroy(pool);
@@ -188,6 +193,7 @@ void* pool_alloc(hipMemPool_t pool, size_t bytes, hipStream_t s, const char* wha
         nnk_set_error((int)e, "%s: scratch of %zu bytes: %s", what, bytes, hipGetErrorString(e));
         return nullptr;
     }
+    ++g_hidden_allocs;  // callers hold g_scratch_mu
     return p;
 }
 }  // namespace
@@ -294,6 +300,11 @@ int nnhip_get_last_error(char* buf, int buflen) {
     g_err.code = 0;
     g_err.msg[0] = '\0';
     return code;
+}
+
+unsigned long long nnhip_launch_allocations(void) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    return g_hidden_allocs;
 }
 
 int nnhip_device_count(void) {

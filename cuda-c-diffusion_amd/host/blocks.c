@@ -16,7 +16,9 @@
  *     and their gradients never exist;
  *   * the DDPM block's embedding broadcast add is folded into GN2 (its input
  *     h + c is formed inside the GroupNorm kernels, never stored) and the
- *     embedding gradient's pixel sum into GN2's backward;
+ *     embedding gradient's pixel sum into GN2's backward, wherever the fused
+ *     shift kernels take the shape; elsewhere GN2 adds c into h in place and
+ *     sums the gradient's pixels itself, as the reference does;
  *   * the EDM block's modulation gradient is a parallel reduction into a lent
  *     workspace;
  *   * the arena holds only what the backward reads (the inputs of the

@@ -75,13 +75,17 @@ void layer_fill_value(Layer* L, int b, size_t n, float value);
 
 /* A fused GroupNorm+activation layer whose input may carry a per-(sample,
    channel) shift: an ordinary spatial_groupnorm_act module (same parameters,
-   ParamList and vtable) whose backward workspace also fits the shift path.
+   ParamList and vtable) whose workspaces also fit the shift path.
    groupnorm_shift_forward / _backward run it on x + shift[b, c] (shift
-   [batch, C], never added in memory): y = act(GN(x + shift)); g_x = the
-   gradient of x + shift, g_shift[b, c] = its sum over the pixels (both
-   overwritten; the parameter gradients too, as in the plain backward). */
+   [batch, C]): y = act(GN(x + shift)); g_x = the gradient of x + shift,
+   g_shift[b, c] = its sum over the pixels (both overwritten; the parameter
+   gradients too, as in the plain backward).  Where the fused shift kernels
+   take the batch, x + shift is formed in registers and x is left as it is;
+   elsewhere the forward adds the shift into x in place, as the reference
+   block does.  Either way the backward must be given the same x, shift and
+   batch as the most recent forward. */
 Module* spatial_groupnorm_act_shift_create(int C, int num_groups, int H, int W, int max_batch, Activation act);
-void groupnorm_shift_forward(Module* gn, const float* x, const float* shift, float* y, int batch, Context* ctx);
+void groupnorm_shift_forward(Module* gn, float* x, const float* shift, float* y, int batch, Context* ctx);
 void groupnorm_shift_backward(Module* gn, const float* x, const float* shift, const float* g_y, float* g_x,
     float* g_shift, int batch, Context* ctx);
 

@@ -61,8 +61,8 @@ Module* activation_create(int dim, Activation act)
  * backward, as in the reference.
  * ------------------------------------------------------------------------ */
 
-enum { NB_GAMMA, NB_BETA, NB_GGAMMA, NB_GBETA, NB_MU, NB_RSTD, NB_BWS, NB_FWS };
-enum { ND_C, ND_G, ND_HW };
+enum { NB_GAMMA, NB_BETA, NB_GGAMMA, NB_GBETA, NB_MU, NB_RSTD, NB_BWS, NB_FWS, NB_RED };
+enum { ND_C, ND_G, ND_HW, ND_SHIFT_MODULE, ND_SHIFT_FUSED };
 
 static void ln_fwd(Layer* L, const float* in, float* out, int batch, Context* ctx)
 {
@@ -99,8 +99,9 @@ static const LayerKind kGroupNormAct = {"groupnorm_act", gn_fwd, gn_bwd};
 
 /* gamma, beta and their gradients, statistics of `rows` rows, the lent
    workspaces (zero-filled: their first word is the wait-timeout flag of the
-   streaming GroupNorm).  gamma = 1, beta = 0. */
-static Module* affine_norm(Layer* L, int C, size_t rows, size_t bws, size_t fws)
+   streaming GroupNorm; `red` is a spatial-reduction workspace, 0 for none).
+   gamma = 1, beta = 0. */
+static Module* affine_norm(Layer* L, int C, size_t rows, size_t bws, size_t fws, size_t red)
 {
     L->dim[ND_C] = C;
     L->k[0] = 1e-5f;
@@ -112,6 +113,7 @@ static Module* affine_norm(Layer* L, int C, size_t rows, size_t bws, size_t fws)
     layer_buf(L, rows, 0);
     layer_buf(L, bws, 1);
     layer_buf(L, fws, 1);
+    layer_buf(L, red, 1);
     layer_param(L, NB_GAMMA, NB_GGAMMA, C);
     layer_param(L, NB_BETA, NB_GBETA, C);
     Module* m = layer_end(L);
@@ -122,7 +124,7 @@ static Module* affine_norm(Layer* L, int C, size_t rows, size_t bws, size_t fws)
 Module* layernorm_create(int dim, int max_batch)
 {
     Layer* L = layer_begin(&kLayerNorm, dim, dim, max_batch);
-    return affine_norm(L, dim, (size_t)max_batch, nnhip_layernorm_backward_workspace(max_batch, dim), 0);
+    return affine_norm(L, dim, (size_t)max_batch, nnhip_layernorm_backward_workspace(max_batch, dim), 0, 0);
 }
 
 static Module* groupnorm_make(const LayerKind* kind, int C, int num_groups, int H, int W, int max_batch,
@@ -133,13 +135,17 @@ static Module* groupnorm_make(const LayerKind* kind, int C, int num_groups, int 
     L->act = act;
     L->dim[ND_G] = num_groups;
     L->dim[ND_HW] = H * W;
+    L->dim[ND_SHIFT_MODULE] = shift;
     /* workspaces sized for max_batch serve every smaller batch; a forward that
-       needs none gets no buffer (the launcher then works without one) */
+       needs none gets no buffer (the launcher then works without one).  A
+       shift module also keeps a spatial-reduction workspace for the batches
+       the fused shift kernels do not take. */
     const int HW = H * W;
     return affine_norm(L, C, (size_t)max_batch * num_groups,
         shift ? nnhip_groupnorm_shift_backward_workspace(max_batch, HW, C, num_groups)
               : nnhip_groupnorm_backward_workspace(max_batch, HW, C, num_groups),
-        nnhip_groupnorm_forward_workspace(max_batch, HW, C, num_groups));
+        nnhip_groupnorm_forward_workspace(max_batch, HW, C, num_groups),
+        shift ? nnhip_spatial_reduce_workspace(max_batch, HW, C) : 0);
 }
 
 Module* spatial_groupnorm_create(int C, int num_groups, int H, int W, int max_batch)
@@ -157,13 +163,25 @@ Module* spatial_groupnorm_act_shift_create(int C, int num_groups, int H, int W, 
     return groupnorm_make(&kGroupNormAct, C, num_groups, H, W, max_batch, act, 1);
 }
 
-void groupnorm_shift_forward(Module* gn, const float* x, const float* shift, float* y, int batch, Context* ctx)
+/* The fused shift launchers when they take the batch (both directions, so
+   that forward and backward agree); otherwise the reference's sequence, the
+   in-place broadcast add followed by the plain module (src/conv_residual.c:34-37)
+   and, backward, the plain module and the pixel sum (:53-55).  The forward
+   records which one ran; the backward follows it. */
+void groupnorm_shift_forward(Module* gn, float* x, const float* shift, float* y, int batch, Context* ctx)
 {
     Layer* L = as_layer(gn);
     NN_ASSERT(batch <= L->max_batch, L->kind->name);
-    launch_groupnorm_act_shift_forward_ws(y, L->buf[NB_MU], L->buf[NB_RSTD], x, shift, L->buf[NB_GAMMA],
-        L->buf[NB_BETA], batch, L->dim[ND_HW], L->dim[ND_C], L->dim[ND_G], L->k[0], L->act, L->buf[NB_FWS],
-        ctx->stream);
+    NN_ASSERT(L->dim[ND_SHIFT_MODULE], "groupnorm_shift_forward: not a shift module");
+    const int HW = L->dim[ND_HW], C = L->dim[ND_C], G = L->dim[ND_G];
+    L->dim[ND_SHIFT_FUSED] = nnhip_groupnorm_shift_supported(batch, HW, C, G, L->act) == 3;
+    if (L->dim[ND_SHIFT_FUSED]) {
+        launch_groupnorm_act_shift_forward_ws(y, L->buf[NB_MU], L->buf[NB_RSTD], x, shift, L->buf[NB_GAMMA],
+            L->buf[NB_BETA], batch, HW, C, G, L->k[0], L->act, L->buf[NB_FWS], ctx->stream);
+    } else {
+        launch_spatial_add(x, shift, batch, HW, 1, C, ctx->stream);
+        gn_fwd(L, x, y, batch, ctx);
+    }
 }
 
 void groupnorm_shift_backward(Module* gn, const float* x, const float* shift, const float* g_y, float* g_x,
@@ -171,9 +189,16 @@ void groupnorm_shift_backward(Module* gn, const float* x, const float* shift, co
 {
     Layer* L = as_layer(gn);
     NN_ASSERT(batch <= L->max_batch, L->kind->name);
-    launch_groupnorm_act_shift_backward_ws(g_x, g_shift, L->buf[NB_GGAMMA], L->buf[NB_GBETA], g_y, x, shift,
-        L->buf[NB_GAMMA], L->buf[NB_BETA], L->buf[NB_MU], L->buf[NB_RSTD], batch, L->dim[ND_HW], L->dim[ND_C],
-        L->dim[ND_G], L->act, L->buf[NB_BWS], ctx->stream);
+    NN_ASSERT(L->dim[ND_SHIFT_MODULE], "groupnorm_shift_backward: not a shift module");
+    const int HW = L->dim[ND_HW], C = L->dim[ND_C], G = L->dim[ND_G];
+    if (L->dim[ND_SHIFT_FUSED]) {
+        launch_groupnorm_act_shift_backward_ws(g_x, g_shift, L->buf[NB_GGAMMA], L->buf[NB_GBETA], g_y, x, shift,
+            L->buf[NB_GAMMA], L->buf[NB_BETA], L->buf[NB_MU], L->buf[NB_RSTD], batch, HW, C, G, L->act,
+            L->buf[NB_BWS], ctx->stream);
+    } else {
+        gn_bwd(L, x, NULL, g_y, g_x, batch, ctx);  /* x holds x + shift since the forward */
+        launch_spatial_reduce_sum_ws(g_shift, g_x, batch, HW, C, L->buf[NB_RED], ctx->stream);
+    }
 }
 
 /* ------------------------------------------------------------------------

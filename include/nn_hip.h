@@ -322,7 +322,7 @@ void launch_layernorm_backward_ws(float* grad_in, float* ggamma, float* gbeta,
    (src/conv_residual.c:34-37); x is not modified and x + shift is not stored
    (each element is the same single fp32 sum the add would store).
    `workspace` as for launch_groupnorm_act_forward_ws
-   (nnhip_groupnorm_forward_workspace floats). */
+   (nnhip_groupnorm_forward_workspace floats); required. */
 void launch_groupnorm_act_shift_forward_ws(float* y, float* mu, float* rstd,
     const float* x, const float* shift, const float* gamma, const float* beta,
     int batch, int HW, int C, int G, float eps, Activation act,
@@ -335,15 +335,22 @@ void launch_groupnorm_act_shift_forward_ws(float* y, float* mu, float* rstd,
    from launch_spatial_reduce_sum's (per 64-pixel tile, then over the tiles);
    dx, ggamma and gbeta are those of launch_groupnorm_act_backward on
    x + shift.  `workspace` holds nnhip_groupnorm_shift_backward_workspace
-   floats.  The persistent kernels take SiLU: the forward at 8 or 16 channels
-   per group, the backward at 4 (up to 2048 pixels) or 8 or 16 (up to 4096).
-   Other activations and shapes compose the separate launches on a
-   batch*HW*C temporary from the stream's pool. */
+   floats; required. */
 void launch_groupnorm_act_shift_backward_ws(float* dx, float* gshift, float* ggamma, float* gbeta,
     const float* dy, const float* x, const float* shift, const float* gamma, const float* beta,
     const float* mu, const float* rstd,
     int batch, int HW, int C, int G, Activation act,
     float* workspace, hipStream_t s);
+/* The two shift launchers run persistent fused kernels only, and allocate
+   nothing.  They take SiLU on 16-byte aligned pointers: the forward at 8 or
+   16 channels per group, the backward at 4 (up to 2048 pixels) or 8 or 16 (up
+   to 4096), where the GroupNorm path policy picks the streaming kernels (from
+   4 Mi elements, or NNHIP_GN_PATH=stream).  Any other case is refused with an
+   error and nothing is launched; the caller then adds the shift itself
+   (launch_spatial_add) and uses the plain launchers, as the reference does.
+   Returns bit 0 set when the forward takes the shape, bit 1 when the
+   backward does (3: both). */
+int nnhip_groupnorm_shift_supported(int batch, int HW, int C, int G, Activation act);
 size_t nnhip_groupnorm_shift_backward_workspace(int batch, int HW, int C, int G);
 
 /* Large GroupNorm launches use persistent workgroups that exchange per-tile

@@ -23,6 +23,14 @@ extern "C" {
    it; the message is copied into buf when buf != NULL. */
 int nnhip_get_last_error(char* buf, int buflen);
 
+/* Number of allocations the launch layer has made by itself since the
+   library was loaded: its scratch pools and their blocks (the launchers
+   without a workspace argument draw them) and the host-mapped wait flag
+   (made once, at load).  Allocations a caller asks for (nnhip_malloc,
+   multi-tensor plans, module arenas) are not counted.  For tests of the
+   allocation-free entry points. */
+unsigned long long nnhip_launch_allocations(void);
+
 /* ---- device ---- */
 int nnhip_device_count(void);
 int nnhip_set_device(int dev);

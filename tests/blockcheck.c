@@ -8,11 +8,16 @@
  * Here those sequences are rebuilt from separate modules and launchers, given
  * the fused block's parameters (same ParamList order and sizes), and both are
  * run forward and backward on the same input and embedding.  Reported: the
- * largest relative difference (max |a - b| / max(|b|, rms(b))) over out,
- * grad_in, every parameter gradient and the embedding gradient.  Needs a GPU.
+ * largest relative difference (max |a - b| / max(|b|, rms(b), floor)) over
+ * out, grad_in, every parameter gradient and the embedding gradient, where
+ * `floor` is 0 except for the DDPM embedding path's reduced outputs, whose
+ * floor is the scale sqrt(sum terms^2) of the terms they add (per tensor, the
+ * largest over its entries).  Each tensor's difference is printed on stderr.
+ * Needs a GPU.
  */
 #define _POSIX_C_SOURCE 200809L
 #include <math.h>
+#include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -27,7 +32,10 @@ static float* dev_normal(size_t n, float std)
     return p;
 }
 
-static double rel_diff(const float* da, const float* db, size_t n)
+/* max |a - b| / max(|b|, rms(b), floor): `floor` is the scale of the terms a
+   reduced output sums (0 for none), so that a sum which cancels to rounding
+   noise is measured against the size of what it adds up. */
+static double rel_diff_floor(const float* da, const float* db, size_t n, double extra)
 {
     float* a = (float*)malloc(n * sizeof(float));
     float* b = (float*)malloc(n * sizeof(float));
@@ -35,7 +43,7 @@ static double rel_diff(const float* da, const float* db, size_t n)
     NN_HIP_CHECK(hipMemcpy(b, db, n * sizeof(float), hipMemcpyDeviceToHost));
     double ss = 0.0;
     for (size_t i = 0; i < n; ++i) ss += (double)b[i] * b[i];
-    const double floor = n ? sqrt(ss / (double)n) : 0.0;
+    const double floor = fmax(n ? sqrt(ss / (double)n) : 0.0, extra);
     double worst = 0.0;
     for (size_t i = 0; i < n; ++i) {
         const double d = fabs((double)a[i] - b[i]) / fmax(fmax(fabs((double)b[i]), floor), 1e-30);
@@ -44,6 +52,15 @@ static double rel_diff(const float* da, const float* db, size_t n)
     free(a);
     free(b);
     return worst;
+}
+
+static double rel_diff(const float* da, const float* db, size_t n) { return rel_diff_floor(da, db, n, 0.0); }
+
+static float* to_host(const float* d, size_t n)
+{
+    float* h = (float*)malloc(n * sizeof(float));
+    NN_HIP_CHECK(hipMemcpy(h, d, n * sizeof(float), hipMemcpyDeviceToHost));
+    return h;
 }
 
 /* Reference-structure DDPM block state. */
@@ -69,7 +86,9 @@ static void copy_params(Module* dst, Module* src)
     param_list_free(&b);
 }
 
-static double grads_diff(Module* a, Module* b)
+/* Largest difference over the parameter gradients; floors[k] (or 0 when
+   floors is NULL or k is past nfloors) is parameter k's term scale. */
+static double grads_diff(Module* a, Module* b, const double* floors, int nfloors)
 {
     ParamList pa, pb;
     param_list_init(&pa);
@@ -78,12 +97,22 @@ static double grads_diff(Module* a, Module* b)
     b->parameters(b, &pb);
     double worst = 0.0;
     for (int k = 0; k < pa.count; ++k) {
-        const double d = rel_diff(pa.items[k].grad, pb.items[k].grad, (size_t)pa.items[k].size);
+        const double f = floors && k < nfloors ? floors[k] : 0.0;
+        const double d = rel_diff_floor(pa.items[k].grad, pb.items[k].grad, (size_t)pa.items[k].size, f);
+        fprintf(stderr, "  parameter %d (%d floats) gradient: %.3e (term floor %.3e)\n", k, pa.items[k].size, d, f);
         if (d > worst) worst = d;
     }
     param_list_free(&pa);
     param_list_free(&pb);
     return worst;
+}
+
+/* Prints one compared tensor's difference (stderr, which the test runner shows
+   on failure) and returns the larger of it and `worst`. */
+static double report(const char* what, double d, double worst)
+{
+    fprintf(stderr, "  %s: %.3e\n", what, d);
+    return d > worst ? d : worst;
 }
 
 /* Parameters of a composite made of sub-modules, in the given order. */
@@ -186,13 +215,62 @@ double nn_blockcheck_ddpm(int B, int H, int W, int C, int G, int emb, int reps, 
         if (rep && ms < best[1]) best[1] = ms;
         NN_HIP_CHECK(hipMemcpy(ge_r, g.cond[slot].grad, (size_t)B * emb * sizeof(float), hipMemcpyDeviceToDevice));
     }
-    double worst = rel_diff(y_f, y_r, (size_t)n);
-    double d = rel_diff(gx_f, gx_r, (size_t)n);
-    if (d > worst) worst = d;
-    d = grads_diff(fused, &view);
-    if (d > worst) worst = d;
-    d = rel_diff(ge_f, ge_r, (size_t)B * emb);
-    if (d > worst) worst = d;
+    /* Term scales of the embedding path's reduced outputs, from the gradient
+       dh of GN2's input (r.gh2, [B, HW, C]): dc[b, c] sums dh over the pixels
+       (scale s[b, c] = sqrt(sum dh^2)); conv1's and the projection's bias
+       gradients sum dc over the samples, the projection's weight gradient
+       sums e[b, i] dc[b, c], the embedding gradient sums dc[b, c] W[i, c].
+       With one channel per group GN2 removes every per-(sample, channel)
+       shift, so these gradients are exactly zero and both sides return
+       rounding noise: only the term scale measures that. */
+    double floors[10] = {0};
+    double worst;
+    {
+        const int HWn = H * W;
+        float* gh = to_host(r.gh2, (size_t)n);
+        float* eh = to_host(e, (size_t)B * emb);
+        ParamList pl;
+        param_list_init(&pl);
+        r.time_proj->parameters(r.time_proj, &pl);
+        float* wh = to_host(pl.items[0].param, (size_t)emb * C);
+        param_list_free(&pl);
+        double* sc = (double*)calloc((size_t)B * C, sizeof(double));
+        for (int b = 0; b < B; ++b)
+            for (int p = 0; p < HWn; ++p)
+                for (int c = 0; c < C; ++c) {
+                    const double v = gh[((size_t)b * HWn + p) * C + c];
+                    sc[(size_t)b * C + c] += v * v;
+                }
+        double fb = 0.0, fw = 0.0, fe = 0.0;
+        for (int c = 0; c < C; ++c) {
+            double t = 0.0;
+            for (int b = 0; b < B; ++b) t += sc[(size_t)b * C + c];
+            fb = fmax(fb, sqrt(t));
+            for (int i = 0; i < emb; ++i) {
+                double u = 0.0;
+                for (int b = 0; b < B; ++b) u += (double)eh[(size_t)b * emb + i] * eh[(size_t)b * emb + i] * sc[(size_t)b * C + c];
+                fw = fmax(fw, sqrt(u));
+            }
+        }
+        for (int b = 0; b < B; ++b)
+            for (int i = 0; i < emb; ++i) {
+                double u = 0.0;
+                for (int c = 0; c < C; ++c) u += sc[(size_t)b * C + c] * (double)wh[(size_t)i * C + c] * wh[(size_t)i * C + c];
+                fe = fmax(fe, sqrt(u));
+            }
+        floors[3] = fb;  /* conv1 bias */
+        floors[4] = fw;  /* projection weight */
+        floors[5] = fb;  /* projection bias */
+        free(sc);
+        free(gh);
+        free(eh);
+        free(wh);
+        fprintf(stderr, "DDPM block [%d, %d, %d, %d] G=%d emb=%d, relative differences:\n", B, H, W, C, G, emb);
+        worst = report("out", rel_diff(y_f, y_r, (size_t)n), 0.0);
+        worst = report("grad_in", rel_diff(gx_f, gx_r, (size_t)n), worst);
+        worst = report("parameter gradients", grads_diff(fused, &view, floors, 10), worst);
+        worst = report("embedding gradient", rel_diff_floor(ge_f, ge_r, (size_t)B * emb, fe), worst);
+    }
     out_ms[0] = best[0];
     out_ms[1] = best[1];
 
@@ -286,13 +364,11 @@ double nn_blockcheck_edm(int B, int H, int W, int C, int emb, float t, int reps,
         if (rep && ms < best[1]) best[1] = ms;
         NN_HIP_CHECK(hipMemcpy(ge_r, g.cond[slot].grad, (size_t)B * emb * sizeof(float), hipMemcpyDeviceToDevice));
     }
-    double worst = rel_diff(y_f, y_r, (size_t)n);
-    double d = rel_diff(gx_f, gx_r, (size_t)n);
-    if (d > worst) worst = d;
-    d = grads_diff(fused, &view);
-    if (d > worst) worst = d;
-    d = rel_diff(ge_f, ge_r, (size_t)B * emb);
-    if (d > worst) worst = d;
+    fprintf(stderr, "EDM block [%d, %d, %d, %d] emb=%d, relative differences:\n", B, H, W, C, emb);
+    double worst = report("out", rel_diff(y_f, y_r, (size_t)n), 0.0);
+    worst = report("grad_in", rel_diff(gx_f, gx_r, (size_t)n), worst);
+    worst = report("parameter gradients", grads_diff(fused, &view, NULL, 0), worst);
+    worst = report("embedding gradient", rel_diff(ge_f, ge_r, (size_t)B * emb), worst);
     out_ms[0] = best[0];
     out_ms[1] = best[1];
     fused->free(fused);

@@ -26,6 +26,7 @@ SHAPES = [
     (2, 9, 9, 16, 4),      # cpg 4, HW = 81
     (1, 64, 64, 256, 32),  # one sample of the north-star shape (1024 threads x 8 float4)
     (2, 100, 100, 8, 2),   # cpg 4, group of 40000 floats: too big for registers -> generic
+    (2, 28, 28, 32, 32),   # cpg 1 (the reference DDPM model's first level) -> generic
 ]
 
 

@@ -16,13 +16,20 @@ pytestmark = pytest.mark.gpu
 
 
 def _backward(L, launcher, x, gamma, beta, dy, mu, rs, G, act):
+    """Runs `launcher`; for the no-allocation entry point also checks that the
+    library made no allocation of its own during the call (its pools, their
+    blocks, the wait flag: nnhip_launch_allocations)."""
     B, HW, C = x.shape
     xd, dyd, dxd = L.to_device(x), L.to_device(dy), L.alloc(x.size)
     gd, bd, mud, rsd = L.to_device(gamma), L.to_device(beta), L.to_device(mu), L.to_device(rs)
     ggd, gbd = L.alloc(C), L.alloc(C)
+    L.sync()
+    allocs = L.nnhip_launch_allocations()
     getattr(L, launcher)(dxd.p, ggd.p, gbd.p, dyd.p, xd.p, gd.p, bd.p, mud.p, rsd.p, B, HW, C, G, act, None)
     L.sync()
     L.check(launcher)
+    if launcher.endswith("_noalloc"):
+        assert L.nnhip_launch_allocations() == allocs, f"{launcher} allocated"
     return dxd.download(shape=x.shape), ggd.download(), gbd.download()
 
 
@@ -40,6 +47,23 @@ def test_noalloc_backward_matches_pool_entry_point(L, orc, rng, monkeypatch, pat
             assert_bits_equal(a, b, f"{what} {B}x{H}x{W}x{C}")
         dx_ref, _, _ = orc.groupnorm_backward(dy, x, gamma, beta, mu, rs, G, act)
         assert rel_err(got[0], dx_ref) <= TOL
+
+
+def test_noalloc_size_check_follows_the_path(L, monkeypatch):
+    """The streaming workspace limit applies only where the streaming kernels
+    run: with the register path forced, the shape the next test refuses
+    (streaming plan about 21 MiB; channel partials 1 MiB) passes the size
+    check and stops at the null-pointer check, so nothing is launched."""
+    print("[case] groupnorm backward noalloc size check on the register path", flush=True)
+    B, HW, C, G = 512, 64 * 64, 256, 32
+    assert L.nnhip_groupnorm_backward_workspace(B, HW, C, G) * 4 > 12 << 20
+    L.sync()
+    assert L.last_error()[0] == 0
+    monkeypatch.setenv("NNHIP_GN_PATH", "reg")
+    L.dll.launch_groupnorm_act_backward_noalloc(None, None, None, None, None, None, None, None, None, B, HW, C, G, 3,
+                                                None)
+    code, msg = L.last_error()
+    assert code != 0 and "null pointer" in msg, (code, msg)
 
 
 def test_noalloc_backward_refuses_oversized_shape(L, rng):
