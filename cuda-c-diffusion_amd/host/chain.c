@@ -10,9 +10,18 @@
  *
  * Here every tensor of the chain lives in one device allocation: link i
  * holds module i and views of its input activation and of the gradient
- * w.r.t. that input; the chain's output follows the links' inputs.
+ * w.r.t. that input; the chain's output follows the links' inputs.  Every
+ * view starts on a 256-byte boundary whatever the widths and max_batch, so
+ * the kernels' 128-bit accesses and alignment requirements hold for each.
  */
 #include "nn_modules.h"
+
+#define CHAIN_ALIGN_FLOATS 64
+
+static size_t chain_round(size_t floats)
+{
+    return (floats + CHAIN_ALIGN_FLOATS - 1) / CHAIN_ALIGN_FLOATS * CHAIN_ALIGN_FLOATS;
+}
 
 typedef struct {
     Module* m;
@@ -42,16 +51,17 @@ Sequential* sequential_create(Module** modules, int n, int max_batch)
     s->max_batch = max_batch;
     s->link = (Link*)calloc((size_t)n, sizeof(Link));
     /* n inputs + 1 output + n input gradients, each max_batch rows */
-    size_t total = (size_t)modules[n - 1]->out_dim;
-    for (int i = 0; i < n; ++i) total += 2 * (size_t)modules[i]->in_dim;
-    s->arena = nn_device_alloc(total * (size_t)max_batch);
+    const size_t mb = (size_t)max_batch;
+    size_t total = chain_round(mb * (size_t)modules[n - 1]->out_dim);
+    for (int i = 0; i < n; ++i) total += 2 * chain_round(mb * (size_t)modules[i]->in_dim);
+    s->arena = nn_device_alloc(total);
     float* at = s->arena;
     for (int i = 0; i < n; ++i) {
         s->link[i].m = modules[i];
         s->link[i].x = at;
-        at += (size_t)max_batch * modules[i]->in_dim;
+        at += chain_round(mb * (size_t)modules[i]->in_dim);
         s->link[i].gx = at;
-        at += (size_t)max_batch * modules[i]->in_dim;
+        at += chain_round(mb * (size_t)modules[i]->in_dim);
     }
     s->y = at;
     return s;

@@ -366,6 +366,18 @@ static int conv_gemm_path(const Layer* L)
     return 1;
 }
 
+/* The implicit-GEMM kernels take 128-bit loads of the activations they
+   gather; a misaligned tensor would make them refuse and leave the output
+   unwritten, so the module stops with a message instead. */
+static void conv_require_aligned(const float* p, const char* what)
+{
+    if (((uintptr_t)p & 15u) != 0) {
+        fprintf(stderr, "conv2d: %s at %p is not 16-byte aligned (the implicit-GEMM path needs it)\n", what,
+            (const void*)p);
+        exit(1);
+    }
+}
+
 static void conv_fwd(Layer* L, const float* in, float* out, int batch, Context* ctx)
 {
     const int* d = L->dim;
@@ -373,6 +385,7 @@ static void conv_fwd(Layer* L, const float* in, float* out, int batch, Context* 
     float *w = L->buf[CB_W], *aux = L->buf[CB_AUX];
     if (d[CD_MP]) launch_weight_normalize(w, kg, d[CD_COUT], L->k[0], ctx->stream);
     if (d[CD_FWD] && !conv_gemm_path(L)) {
+        conv_require_aligned(in, "the forward input");
         launch_conv2d_forward_implicit(out, in, w, d[CD_MP] ? NULL : aux, d[CD_MP] ? aux : NULL, batch,
             d[CD_HI], d[CD_WI], d[CD_CIN], d[CD_COUT], d[CD_K], d[CD_S], d[CD_P], d[CD_HO], d[CD_WO], ctx->stream);
         return;
@@ -393,6 +406,8 @@ static void conv_bwd(Layer* L, const float* in, const float* out, const float* g
     const int forced = conv_gemm_path(L);
     float *w = L->buf[CB_W], *gw = L->buf[CB_GW], *col = L->buf[CB_COL];
     if (d[CD_WGRAD] && !forced) {
+        conv_require_aligned(in, "the forward input");
+        conv_require_aligned(grad_out, "the output gradient");
         launch_conv2d_weight_grad_implicit(gw, in, grad_out, batch, d[CD_HI], d[CD_WI], d[CD_CIN], d[CD_COUT],
             d[CD_K], d[CD_S], d[CD_P], d[CD_HO], d[CD_WO], L->buf[CB_WGWS], ctx->stream);
     } else {
@@ -411,6 +426,7 @@ static void conv_bwd(Layer* L, const float* in, const float* out, const float* g
     const float* gain = d[CD_MP] ? L->buf[CB_AUX] : NULL;
     if (d[CD_DGRAD] && !forced) {
         /* stride 1: dx = conv(dy, flipped kernel, pad K-1-pad), times the gain in mp mode */
+        conv_require_aligned(grad_out, "the output gradient");
         launch_conv2d_input_grad_implicit(grad_in, grad_out, w, gain, batch, d[CD_HI], d[CD_WI], d[CD_CIN],
             d[CD_COUT], d[CD_K], d[CD_P], ctx->stream);
         return;

@@ -3,8 +3,10 @@
  * input gradient and parameter gradients, the ParamList in module order, and
  * the forward input copied into the chain (the caller may reuse its buffer
  * before the backward).  Built into tests/_build/libgradcheck.so;
- * nn_chaincheck_run() returns the number of mismatches (0 = pass).  Needs a
- * GPU. */
+ * nn_chaincheck_run() returns the number of mismatches (0 = pass);
+ * nn_chaincheck_odd_run() does the same for a chain whose first link has an
+ * odd width and an odd batch ahead of an implicit-GEMM convolution, which
+ * needs its input view 16-byte aligned.  Needs a GPU. */
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -95,6 +97,83 @@ int nn_chaincheck_run(void)
     free(gx_hand);
     param_list_free(&pl);
     sequential_free(s);
+    nn_context_destroy(&ctx);
+    return bad;
+}
+
+/* The chain against its modules run by hand on separately allocated tensors:
+   output, input gradient and every parameter gradient bit for bit. */
+static int chain_vs_hand(Context* ctx, Module** mods, int n, int batch)
+{
+    Sequential* s = sequential_create(mods, n, batch);
+    const int in0 = mods[0]->in_dim, outn = mods[n - 1]->out_dim;
+    float* x = upload_random(ctx, batch * in0);
+    float* g = upload_random(ctx, batch * outn);
+    sequential_forward(s, x, batch, ctx);
+    sequential_backward(s, g, batch, ctx);
+    NN_HIP_CHECK(hipDeviceSynchronize());
+    int bad = nnhip_get_last_error(NULL, 0) != 0;
+    float* y_chain = fetch(sequential_output(s), batch * outn);
+    float* gx_chain = fetch(sequential_input_grad(s), batch * in0);
+    ParamList pl;
+    param_list_init(&pl);
+    sequential_parameters(s, &pl);
+    float** pg = (float**)calloc((size_t)pl.count, sizeof(float*));
+    for (int i = 0; i < pl.count; ++i) pg[i] = fetch(pl.items[i].grad, pl.items[i].size);
+
+    float** act = (float**)calloc((size_t)n + 1, sizeof(float*));
+    float** grd = (float**)calloc((size_t)n + 1, sizeof(float*));
+    for (int i = 0; i <= n; ++i) {
+        const int w = i < n ? mods[i]->in_dim : outn;
+        act[i] = nn_device_alloc((size_t)batch * w);
+        grd[i] = nn_device_alloc((size_t)batch * w);
+    }
+    NN_HIP_CHECK(hipMemcpy(act[0], x, (size_t)batch * in0 * sizeof(float), hipMemcpyDeviceToDevice));
+    NN_HIP_CHECK(hipMemcpy(grd[n], g, (size_t)batch * outn * sizeof(float), hipMemcpyDeviceToDevice));
+    for (int i = 0; i < n; ++i) mods[i]->forward(mods[i], act[i], act[i + 1], batch, ctx);
+    for (int i = n - 1; i >= 0; --i) mods[i]->backward(mods[i], act[i], act[i + 1], grd[i + 1], grd[i], batch, ctx);
+    NN_HIP_CHECK(hipDeviceSynchronize());
+    bad += nnhip_get_last_error(NULL, 0) != 0;
+    float* y_hand = fetch(act[n], batch * outn);
+    float* gx_hand = fetch(grd[0], batch * in0);
+    bad += differs("output", y_chain, y_hand, batch * outn);
+    bad += differs("input gradient", gx_chain, gx_hand, batch * in0);
+    for (int i = 0; i < pl.count; ++i) {
+        float* h = fetch(pl.items[i].grad, pl.items[i].size);
+        char what[32];
+        snprintf(what, sizeof what, "parameter gradient %d", i);
+        bad += differs(what, pg[i], h, pl.items[i].size);
+        free(h);
+        free(pg[i]);
+    }
+    for (int i = 0; i <= n; ++i) {
+        (void)hipFree(act[i]);
+        (void)hipFree(grd[i]);
+    }
+    free(act);
+    free(grd);
+    free(pg);
+    free(y_chain);
+    free(gx_chain);
+    free(y_hand);
+    free(gx_hand);
+    param_list_free(&pl);
+    (void)hipFree(x);
+    (void)hipFree(g);
+    sequential_free(s);
+    return bad;
+}
+
+int nn_chaincheck_odd_run(void)
+{
+    /* linear 3 -> 8*8*32 at batch 3: the first link's views hold 9 floats
+       each, so the convolution's input view would start 72 bytes into the
+       arena without the chain's 256-byte rounding */
+    const int batch = 3, H = 8, W = 8, C = 32;
+    Context ctx;
+    nn_context_init(&ctx, 101, 0);
+    Module* mods[2] = {linear_create(&ctx, 3, H * W * C), conv2d_create(&ctx, C, 64, 3, 1, 1, H, W, batch, 0, 1.0f)};
+    const int bad = chain_vs_hand(&ctx, mods, 2, batch);
     nn_context_destroy(&ctx);
     return bad;
 }

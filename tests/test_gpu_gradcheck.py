@@ -28,3 +28,14 @@ def test_sequential_chain_matches_modules_called_by_hand(L):
     gc = ctypes.CDLL(str(LIB))
     gc.nn_chaincheck_run.restype = ctypes.c_int
     assert gc.nn_chaincheck_run() == 0
+
+
+def test_sequential_views_stay_aligned_after_odd_links(L):
+    """A chain whose first link is 3 floats wide at batch 3, ahead of an
+    implicit-GEMM convolution (which needs its input 16-byte aligned): the
+    chain's output and gradients equal the modules run by hand, bit for bit,
+    and no launcher records an error."""
+    print("[case] Sequential with an odd-width link before a conv", flush=True)
+    gc = ctypes.CDLL(str(LIB))
+    gc.nn_chaincheck_odd_run.restype = ctypes.c_int
+    assert gc.nn_chaincheck_odd_run() == 0
