@@ -54,40 +54,67 @@ static int write_list(FILE* f, const ParamList* pl)
     return 0;
 }
 
+/* Payloads are read through one host staging buffer of at most this many
+   floats; a chunk may span several tensors of the list. */
+#define CK_STAGE_FLOATS ((size_t)1 << 22)
+
+/* One list in the layout write_list produces.  The header is validated in
+   file order before any payload is read: the count (-3 when it differs from
+   the model's), then the sizes, where the first entry that differs from the
+   model's tensor gives -4 even if the file also ends early, and a file that
+   ends inside the header or the payloads gives -2.  Payloads are contiguous
+   in the file, so they stream in chunks and are uploaded tensor by tensor. */
 static int read_list(FILE* f, ParamList* pl)
 {
-    int count;
-    if (ck_read(&count, sizeof(int), 1, f)) return -2;
+    int count = 0;
+    if (ck_read(&count, sizeof count, 1, f)) return -2;
     if (count != pl->count) {
-        fprintf(stderr, "checkpoint: param count mismatch (file=%d, model=%d)\n", count, pl->count);
+        fprintf(stderr, "checkpoint: the file lists %d tensors where the model has %d\n", count, pl->count);
         return -3;
     }
-    for (int i = 0; i < count; ++i) {
-        int size;
-        if (ck_read(&size, sizeof(int), 1, f)) return -2;
-        if (size != pl->items[i].size) {
-            fprintf(stderr, "checkpoint: param %d size mismatch (file=%d, model=%d)\n", i, size,
-                pl->items[i].size);
+    int* sizes = (int*)malloc((size_t)(count > 0 ? count : 1) * sizeof(int));
+    const size_t got = fread(sizes, sizeof(int), (size_t)count, f);
+    size_t total = 0;
+    for (size_t i = 0; i < got; ++i) {
+        if (sizes[i] != pl->items[i].size) {
+            fprintf(stderr, "checkpoint: tensor %zu holds %d floats in the file and %d in the model\n", i,
+                sizes[i], pl->items[i].size);
+            free(sizes);
             return -4;
         }
+        total += (size_t)sizes[i];
     }
-    size_t cap = 0;
-    float* buf = NULL;
-    for (int i = 0; i < count; ++i) {
-        const size_t n = (size_t)pl->items[i].size;
-        if (n > cap) {
-            free(buf);
-            buf = (float*)malloc(n * sizeof(float));
-            cap = n;
+    free(sizes);
+    if (got != (size_t)count) return -2;
+
+    const size_t cap = total < CK_STAGE_FLOATS ? total : CK_STAGE_FLOATS;
+    float* stage = (float*)malloc((cap ? cap : 1) * sizeof(float));
+    int t = 0;         /* tensor being filled */
+    size_t done = 0;   /* floats of tensor t already uploaded */
+    size_t left = total;
+    int rc = 0;
+    while (left && !rc) {
+        const size_t chunk = left < cap ? left : cap;
+        if (ck_read(stage, sizeof(float), chunk, f)) {
+            rc = -2;
+            break;
         }
-        if (ck_read(buf, sizeof(float), n, f)) {
-            free(buf);
-            return -2;
+        left -= chunk;
+        for (size_t at = 0; at < chunk;) {
+            while ((size_t)pl->items[t].size == done) { /* skip finished (and empty) tensors */
+                ++t;
+                done = 0;
+            }
+            const size_t want = (size_t)pl->items[t].size - done;
+            const size_t take = chunk - at < want ? chunk - at : want;
+            NN_HIP_CHECK(hipMemcpy(pl->items[t].param + done, stage + at, take * sizeof(float),
+                hipMemcpyHostToDevice));
+            done += take;
+            at += take;
         }
-        NN_HIP_CHECK(hipMemcpy(pl->items[i].param, buf, n * sizeof(float), hipMemcpyHostToDevice));
     }
-    free(buf);
-    return 0;
+    free(stage);
+    return rc;
 }
 
 int checkpoint_save(const char* path, const ParamList* pl)

@@ -157,3 +157,43 @@ int nn_ckpt_test_load_mismatch(const char* path, int size0, int drop_last)
     param_list_free(&pl);
     return rc;
 }
+
+/* Weights round trip of a list with the given tensor sizes: each tensor is
+   filled with a pattern of its own, saved, zeroed, loaded and compared bit
+   for bit.  Returns the number of tensors that differ, or the load's error
+   code when it fails. */
+int nn_ckpt_test_roundtrip_sizes(const char* path, const int* sizes, int n)
+{
+    ParamList pl;
+    param_list_init(&pl);
+    float** dev = (float**)calloc((size_t)n, sizeof(float*));
+    float** want = (float**)calloc((size_t)n, sizeof(float*));
+    for (int k = 0; k < n; ++k) {
+        const size_t m = (size_t)sizes[k];
+        want[k] = (float*)malloc((m ? m : 1) * sizeof(float));
+        for (size_t i = 0; i < m; ++i) want[k][i] = (float)(k + 1) + 1e-6f * (float)(i % 1000003);
+        dev[k] = nn_device_alloc(m ? m : 1);
+        if (m) NN_HIP_CHECK(hipMemcpy(dev[k], want[k], m * sizeof(float), hipMemcpyHostToDevice));
+        param_list_add(&pl, dev[k], NULL, sizes[k]);
+    }
+    int rc = checkpoint_save(path, &pl);
+    for (int k = 0; k < n && !rc; ++k)
+        if (sizes[k]) NN_HIP_CHECK(hipMemset(dev[k], 0, (size_t)sizes[k] * sizeof(float)));
+    if (!rc) rc = checkpoint_load(path, &pl);
+    int bad = 0;
+    for (int k = 0; k < n; ++k) {
+        const size_t m = (size_t)sizes[k];
+        if (!rc && m) {
+            float* got = (float*)malloc(m * sizeof(float));
+            NN_HIP_CHECK(hipMemcpy(got, dev[k], m * sizeof(float), hipMemcpyDeviceToHost));
+            bad += memcmp(got, want[k], m * sizeof(float)) != 0;
+            free(got);
+        }
+        (void)hipFree(dev[k]);
+        free(want[k]);
+    }
+    free(dev);
+    free(want);
+    param_list_free(&pl);
+    return rc ? rc : bad;
+}

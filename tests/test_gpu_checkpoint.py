@@ -136,3 +136,23 @@ def test_checkpoint_save_load_roundtrip_and_error_codes(ck, tmp_path):
     short = tmp_path / "short.cktr"
     short.write_bytes(t.read_bytes()[:-4])
     assert ck.nn_ckpt_test_load(str(short).encode(), _fp(out), TOTAL, counters) == -2   # short file
+    # a file that ends inside the size table: the sizes it holds are checked
+    # first, in file order (magic, count, then only the first size here)
+    cut = tmp_path / "cut.ckpt"
+    cut.write_bytes(w.read_bytes()[:12])
+    assert ck.nn_ckpt_test_load_mismatch(str(cut).encode(), 6, 0) == -4  # first size differs
+    assert ck.nn_ckpt_test_load_mismatch(str(cut).encode(), 5, 0) == -2  # sizes agree, file short
+
+
+def test_checkpoint_payload_across_staging_chunks(ck, tmp_path):
+    """Payloads stream through a 4 Mi-float staging buffer that may span
+    tensors: tensors that cross its boundary, an empty tensor and small ones
+    round-trip bit for bit."""
+    print("[case] checkpoint payloads across staging chunks", flush=True)
+    ck.nn_ckpt_test_roundtrip_sizes.argtypes = [C.c_char_p, C.POINTER(C.c_int), C.c_int]
+    ck.nn_ckpt_test_roundtrip_sizes.restype = C.c_int
+    sizes = [3, (1 << 22) - 1, 2, 0, (1 << 22) + 5, 7]
+    arr = (C.c_int * len(sizes))(*sizes)
+    path = tmp_path / "big.ckpt"
+    assert ck.nn_ckpt_test_roundtrip_sizes(str(path).encode(), arr, len(sizes)) == 0
+    assert path.stat().st_size == 4 + 4 + 4 * len(sizes) + 4 * sum(sizes)
