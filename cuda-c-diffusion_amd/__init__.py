@@ -47,6 +47,9 @@ _SIGS = {
     # runtime plumbing (nn_hip_rt.h)
     "nnhip_get_last_error": (I, [C.c_char_p, I], False),
     "nnhip_launch_allocations": (C.c_ulonglong, [], False),
+    "nnhip_rng_seed": (None, [P, C.c_uint64], False),
+    "nnhip_fill_normal": (I, [P, P, SZ, F, F], False),
+    "nnhip_fill_uniform": (I, [P, P, SZ], False),
     "nnhip_device_count": (I, [], False),
     "nnhip_set_device": (I, [I], False),
     "nnhip_device_info": (I, [C.c_char_p, I], False),

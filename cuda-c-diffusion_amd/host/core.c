@@ -39,34 +39,55 @@ static uint64_t xoshiro_next(uint64_t* s)
     return result;
 }
 
-double nn_rng_uniform(Context* ctx) /* [0, 1) with 53 random bits */
+static double rng_uniform(NnHostRng* g) /* [0, 1) with 53 random bits */
 {
-    return (double)(xoshiro_next(ctx->rng) >> 11) * (1.0 / 9007199254740992.0);
+    return (double)(xoshiro_next(g->s) >> 11) * (1.0 / 9007199254740992.0);
 }
 
-double nn_rng_normal(Context* ctx) /* Box-Muller, cosine branch */
+static double rng_normal(NnHostRng* g) /* Box-Muller, cosine branch */
 {
-    double u1 = 1.0 - nn_rng_uniform(ctx); /* (0, 1] */
-    double u2 = nn_rng_uniform(ctx);
+    double u1 = 1.0 - rng_uniform(g); /* (0, 1] */
+    double u2 = rng_uniform(g);
     return sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2);
 }
 
+void nnhip_rng_seed(NnHostRng* g, uint64_t seed)
+{
+    uint64_t s = seed;
+    for (int i = 0; i < 4; ++i) g->s[i] = splitmix64(&s);
+}
+
+int nnhip_fill_normal(NnHostRng* g, float* dst, size_t n, float mean, float std)
+{
+    if (n == 0) return 0;
+    float* h = (float*)malloc(n * sizeof(float));
+    for (size_t i = 0; i < n; ++i) h[i] = (float)((double)mean + (double)std * rng_normal(g));
+    const hipError_t e = hipMemcpy(dst, h, n * sizeof(float), hipMemcpyHostToDevice);
+    free(h);
+    return (int)e;
+}
+
+int nnhip_fill_uniform(NnHostRng* g, float* dst, size_t n)
+{
+    if (n == 0) return 0;
+    float* h = (float*)malloc(n * sizeof(float));
+    for (size_t i = 0; i < n; ++i) h[i] = (float)(xoshiro_next(g->s) >> 40) * (1.0f / 16777216.0f);
+    const hipError_t e = hipMemcpy(dst, h, n * sizeof(float), hipMemcpyHostToDevice);
+    free(h);
+    return (int)e;
+}
+
+double nn_rng_uniform(Context* ctx) { return rng_uniform(&ctx->rng); }
+double nn_rng_normal(Context* ctx) { return rng_normal(&ctx->rng); }
+
 void nn_fill_normal(Context* ctx, float* dst, size_t n, float mean, float std)
 {
-    if (n == 0) return;
-    float* h = (float*)malloc(n * sizeof(float));
-    for (size_t i = 0; i < n; ++i) h[i] = (float)((double)mean + (double)std * nn_rng_normal(ctx));
-    NN_HIP_CHECK(hipMemcpy(dst, h, n * sizeof(float), hipMemcpyHostToDevice));
-    free(h);
+    NN_HIP_CHECK((hipError_t)nnhip_fill_normal(&ctx->rng, dst, n, mean, std));
 }
 
 void nn_fill_uniform(Context* ctx, float* dst, size_t n)
 {
-    if (n == 0) return;
-    float* h = (float*)malloc(n * sizeof(float));
-    for (size_t i = 0; i < n; ++i) h[i] = (float)(xoshiro_next(ctx->rng) >> 40) * (1.0f / 16777216.0f);
-    NN_HIP_CHECK(hipMemcpy(dst, h, n * sizeof(float), hipMemcpyHostToDevice));
-    free(h);
+    NN_HIP_CHECK((hipError_t)nnhip_fill_uniform(&ctx->rng, dst, n));
 }
 
 /* ---- context ---- */
@@ -74,8 +95,7 @@ void nn_fill_uniform(Context* ctx, float* dst, size_t n)
 void nn_context_init(Context* ctx, uint64_t seed, hipStream_t stream)
 {
     memset(ctx, 0, sizeof *ctx);
-    uint64_t s = seed;
-    for (int i = 0; i < 4; ++i) ctx->rng[i] = splitmix64(&s);
+    nnhip_rng_seed(&ctx->rng, seed);
     ctx->stream = stream;
     NN_BLAS_CHECK(rocblas_create_handle(&ctx->blas));
     NN_BLAS_CHECK(rocblas_set_stream(ctx->blas, stream));

@@ -12,6 +12,7 @@
 #define NN_HIP_RT_H
 
 #include <stddef.h>
+#include <stdint.h>
 #include <hip/hip_runtime_api.h>
 
 #ifdef __cplusplus
@@ -79,6 +80,25 @@ int nnhip_graph_capture_begin(hipStream_t s);
 hipGraphExec_t nnhip_graph_capture_end(hipStream_t s);
 int nnhip_graph_launch(hipGraphExec_t g, hipStream_t s);
 int nnhip_graph_destroy(hipGraphExec_t g);
+
+/* ---- host generator for weight initialisation ----
+   The reference draws initial weights from a cuRAND generator held in its
+   Context (src/nn.h:73, the fill at src/nn.h:117-135).  A caller that keeps
+   the reference's host code holds one of these instead: xoshiro256**
+   (Blackman and Vigna) seeded through SplitMix64, draws made on the host and
+   copied into device memory with a synchronous copy (so a constructor may
+   use the buffer at once, as after the reference's fill).  The library's own
+   Context (nn_modules.h) carries the same generator. */
+typedef struct {
+    uint64_t s[4];
+} NnHostRng;
+void nnhip_rng_seed(NnHostRng* g, uint64_t seed);
+/* dst[i] = mean + std * z_i with z_i ~ N(0, 1) (Box-Muller in double) for n
+   floats of device memory.  Returns 0 or the HIP error of the copy. */
+int nnhip_fill_normal(NnHostRng* g, float* dst, size_t n, float mean, float std);
+/* dst[i] ~ U[0, 1) from the top 24 bits of one draw each.  Returns 0 or the
+   HIP error of the copy. */
+int nnhip_fill_uniform(NnHostRng* g, float* dst, size_t n);
 
 /* ---- calibration ---- */
 /* dst[i] = src[i] for n floats with the same 128-bit vector access pattern

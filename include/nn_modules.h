@@ -73,7 +73,7 @@ typedef struct {
 
 typedef struct {
     rocblas_handle blas;  /* GEMM outside the fused path */
-    uint64_t rng[4];      /* host xoshiro256** state (replaces the cuRAND generator) */
+    NnHostRng rng;        /* host xoshiro256** state (replaces the cuRAND generator) */
     hipStream_t stream;
     CondSlot cond[CTX_MAX_COND];
     int n_cond;

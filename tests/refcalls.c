@@ -8,7 +8,11 @@
  * arguments of the types those modules pass (struct fields of int / float /
  * float*, a Context-like stream member).  tests/test_abi.py compiles this
  * file with gcc -std=c11 -Wall -Wextra -Werror. */
+#include <stdio.h>
+#include <stdlib.h>
+
 #include "nn_hip.h"
+#include "nn_hip_rt.h"
 
 /* ---- the reference's prototypes, stream re-typed (src/nn.h:354-456) ---- */
 typedef void add_bias_t(float* Y, const float* b, int M, int N, hipStream_t s);
@@ -79,7 +83,10 @@ mp_ccat_t* const ref_mp_channel_cat = launch_mp_channel_cat;
 mp_csplit_t* const ref_mp_channel_split = launch_mp_channel_split;
 
 /* ---- call sites as the reference's host modules write them ---- */
-typedef struct { hipStream_t stream; } RefContext;           /* the stream member of src/nn.h:71-77 */
+typedef struct {                                              /* src/nn.h:71-77, re-typed for HIP */
+    NnHostRng rng;                                            /* was curandGenerator_t curand */
+    hipStream_t stream;
+} RefContext;
 typedef struct {                                              /* fields of the modules' state structs */
     int C, G, HW, dim, in, out, C_in, C_out, K, stride, pad, Hi, Wi, Ho, Wo, H, W;
     float eps, log_max_period, wa, wb, t;
@@ -140,4 +147,38 @@ void nn_reference_call_sites(RefState* st, RefContext* ctx, float* out, const fl
         ctx->stream);
     launch_mp_sum(out, in, st->h1, st->t, n, ctx->stream);
     launch_mp_cat(out, in, st->h1, st->t, batch, st->C_in, st->C_out, ctx->stream);
+}
+
+/* ---- weight initialisation, re-typed: NN_HIP_CHECK and the fill of
+   src/nn.h:13-21, 117-135 over the library's host generator, then the call
+   sites of the path's modules with ctx->curand replaced by &ctx->rng
+   (src/conv2d.c:124, 132, src/mp_linear.c:73, src/linear.c:62,
+   src/mp_fourier.c:49-50) and the generator's creation
+   (ddpm/main_ddpm.c:143-145) ---- */
+#define NN_HIP_CHECK(call)                                                                       \
+    do {                                                                                         \
+        hipError_t e_ = (call);                                                                  \
+        if (e_ != hipSuccess) {                                                                  \
+            fprintf(stderr, "HIP %s:%d: %s\n", __FILE__, __LINE__, hipGetErrorString(e_));      \
+            exit(1);                                                                             \
+        }                                                                                        \
+    } while (0)
+
+static inline void nn_fill_normal(NnHostRng* g, float* dst, size_t n, float mean, float std)
+{
+    NN_HIP_CHECK((hipError_t)nnhip_fill_normal(g, dst, n, mean, std));
+}
+
+void nn_reference_init_sites(RefState* st, RefContext* ctx, unsigned long long seed, int Kg, int in_dim,
+    int out_dim, int num_channels, float bandwidth);
+void nn_reference_init_sites(RefState* st, RefContext* ctx, unsigned long long seed, int Kg, int in_dim,
+    int out_dim, int num_channels, float bandwidth)
+{
+    nnhip_rng_seed(&ctx->rng, (uint64_t)seed);                                   /* main_ddpm.c:143-145 */
+    nn_fill_normal(&ctx->rng, st->W_, (size_t)Kg * st->C_out, 0.0f, 1.0f);        /* conv2d.c:124 */
+    nn_fill_normal(&ctx->rng, st->W_, (size_t)Kg * st->C_out, 0.0f, st->eps);     /* conv2d.c:132 */
+    nn_fill_normal(&ctx->rng, st->W_, (size_t)in_dim * out_dim, 0.0f, 1.0f);      /* mp_linear.c:73 */
+    nn_fill_normal(&ctx->rng, st->W_, (size_t)in_dim * out_dim, 0.0f, st->eps);   /* linear.c:62 */
+    nn_fill_normal(&ctx->rng, st->freqs, num_channels, 0.0f, bandwidth);         /* mp_fourier.c:49 */
+    NN_HIP_CHECK((hipError_t)nnhip_fill_uniform(&ctx->rng, st->phases, num_channels)); /* mp_fourier.c:50 */
 }
