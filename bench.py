@@ -481,6 +481,32 @@ def run_suite(L, nn, reps, with_cpu=True):
     _row("silu_bwd", "cfg4 [256,64,64,256]",
          T.median_us(lambda: L.launch_activation_backward(ga.p, ya.p, xa.p, n4, 3, stream), max(5, reps // 4)),
          12 * n4, cpu=cpu(lambda: orc.act_backward(h16b, h16, 3), 16.0, "16 of 256 samples x 16, 1 thread"))
+    # The drop-in path at the north-star shape: an unchanged reference caller's
+    # own sequence (src/conv_residual.c:28-29, 35-36 forward; 51-52, 62-63
+    # backward) through the reference-named launchers, their scratch drawn
+    # from the library's pool.  Each launch's compulsory bytes: GN forward
+    # R x W h0, SiLU forward R h0 W h1, SiLU backward R gh1 R h0 W gh0, GN
+    # backward R x R gh0 W dx: 40 B/elem, where the fused step moves 20.
+    Bd, HWd, Cd, Gd = 256, 64 * 64, 256, 32
+    gmd, btd = dev(1 + 0.1 * rng.standard_normal(Cd)), dev(0.1 * rng.standard_normal(Cd))
+    mud, rsd, ggd, gbd = L.alloc(Bd * Gd), L.alloc(Bd * Gd), L.alloc(Cd), L.alloc(Cd)
+    h1d, gh1d, gh0d = L.alloc(n4), dev(rng.standard_normal(n4, dtype=f32)), L.alloc(n4)
+    h0d, dxd = ya, ga
+
+    def dropin_fwd():
+        L.launch_groupnorm_forward(h0d.p, mud.p, rsd.p, xa.p, gmd.p, btd.p, Bd, HWd, Cd, Gd, 1e-5, stream)
+        L.launch_activation_forward(h1d.p, h0d.p, n4, 3, stream)
+
+    def dropin_bwd():
+        L.launch_activation_backward(gh0d.p, gh1d.p, h0d.p, n4, 3, stream)
+        L.launch_groupnorm_backward(dxd.p, ggd.p, gbd.p, gh0d.p, xa.p, gmd.p, mud.p, rsd.p, Bd, HWd, Cd, Gd, stream)
+    _row("gn_silu_dropin_fwd", "cfg4 [256,64,64,256] G32: launch_groupnorm_forward + launch_activation_forward",
+         T.median_us(dropin_fwd, max(5, reps // 4)), 16 * n4,
+         "the reference caller's sequence on pool scratch; 16 B/elem compulsory over 2 launches (fused: 8)")
+    _row("gn_silu_dropin_bwd", "cfg4: launch_activation_backward + launch_groupnorm_backward",
+         T.median_us(dropin_bwd, max(5, reps // 4)), 24 * n4,
+         "the reference caller's sequence on pool scratch; 24 B/elem compulsory over 2 launches (fused: 12)")
+    del h1d, gh1d, gh0d
     # DDPM block neighbours at the cfg4 shape (src/conv_residual.c:33, 44-45)
     emb = dev(rng.standard_normal(256 * 256))
     gemb = L.alloc(256 * 256)
