@@ -91,6 +91,8 @@ _SIGS = {
     "launch_conv2d_weight_grad_implicit": (None, [P, P, P] + [I] * 10 + [P, P], True),
     "nnhip_conv2d_wgrad_implicit_supported": (I, [I, I], False),
     "nnhip_conv2d_wgrad_workspace": (SZ, [I] * 6, False),
+    "launch_conv2d_forward_implicit_fused": (None, [P, P, P, P, P] + [I] * 10 + [P, P], True),
+    "launch_conv2d_input_grad_implicit_fused": (None, [P, P, P, P] + [I] * 7 + [P, P], True),
     # launch layer (nn_hip.h)
     "launch_add_bias": (None, [P, P, I, I, P], True),
     "launch_bias_grad": (None, [P, P, I, I, P], True),
@@ -142,6 +144,13 @@ class NnTensorSlot(C.Structure):
     """Mirror of NnTensorSlot in include/nn_hip.h."""
 
     _fields_ = [("p", P), ("m", P), ("v", P), ("g", P), ("shadow", P), ("n", LL)]
+
+
+class NnConvFusion(C.Structure):
+    """Mirror of NnConvFusion in include/nn_hip.h (pass C.addressof(f))."""
+
+    _fields_ = [("res", P), ("res_w", C.c_float), ("out_w", C.c_float), ("cond", P), ("y2", P),
+                ("act_in", P), ("act", C.c_int)]
 
 
 def header_functions() -> list[str]:

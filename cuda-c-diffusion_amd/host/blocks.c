@@ -21,6 +21,11 @@
  *     sums the gradient's pixels itself, as the reference does;
  *   * the EDM block's modulation gradient is a parallel reduction into a lent
  *     workspace;
+ *   * the passes next to the convolutions are folded into the implicit-GEMM
+ *     kernels (where those take the convolution): the residual add / mp_sum
+ *     into the last convolution's epilogue, the EDM modulation + MP-SiLU into
+ *     conv0's, and the MP-SiLU gradient with the wa residual into conv0's
+ *     input-gradient epilogue;
  *   * the arena holds only what the backward reads (the inputs of the
  *     children) plus two gradient tensors that the backward reuses as each
  *     one's last reader has run.
@@ -41,13 +46,11 @@ static void ddpm_fwd(Layer* L, const float* x, float* out, int batch, Context* c
 {
     Module** s = L->sub;
     float** t = L->buf;
-    const int n = batch * L->dim[DD_HW] * L->dim[DD_C];
     s[DS_GN1]->forward(s[DS_GN1], x, t[DT_A1], batch, ctx);                         /* a1 = silu(gn1(x)) */
     s[DS_CONV1]->forward(s[DS_CONV1], t[DT_A1], t[DT_H], batch, ctx);               /* h = conv1(a1) */
     s[DS_PROJ]->forward(s[DS_PROJ], ctx->cond[L->dim[DD_SLOT]].fwd, t[DT_C], batch, ctx); /* c = proj(emb) */
     groupnorm_shift_forward(s[DS_GN2], t[DT_H], t[DT_C], t[DT_A2], batch, ctx);      /* a2 = silu(gn2(h + c)) */
-    s[DS_CONV2]->forward(s[DS_CONV2], t[DT_A2], out, batch, ctx);                   /* out = conv2(a2) */
-    launch_weighted_sum(out, x, out, 1.0f, 1.0f, n, ctx->stream);                   /* out += x */
+    conv2d_forward_residual(s[DS_CONV2], t[DT_A2], out, x, 1.0f, 1.0f, batch, ctx);  /* out = x + conv2(a2) */
 }
 
 static void ddpm_bwd(Layer* L, const float* x, const float* out, const float* g_out, float* g_x, int batch,
@@ -111,12 +114,10 @@ static void edm_fwd(Layer* L, const float* x, float* out, int batch, Context* ct
     float** t = L->buf;
     const int n = batch * L->dim[ED_HW] * L->dim[ED_C];
     launch_activation_forward(t[ET_H0], x, n, ACT_MP_SILU, ctx->stream);              /* h0 = mp_silu(x) */
-    s[ES_CONV0]->forward(s[ES_CONV0], t[ET_H0], t[ET_H1], batch, ctx);                /* h1 = conv0(h0) */
     s[ES_LIN]->forward(s[ES_LIN], ctx->cond[L->dim[ED_SLOT]].fwd, t[ET_C], batch, ctx); /* c = lin(emb) */
-    launch_spatial_modulate_act_forward(t[ET_H3], t[ET_H1], t[ET_C], batch, L->dim[ED_HW], 1, L->dim[ED_C],
-        ACT_MP_SILU, ctx->stream);                                                    /* h3 = mp_silu(h1 (c+1)) */
-    s[ES_CONV1]->forward(s[ES_CONV1], t[ET_H3], out, batch, ctx);                     /* out = conv1(h3) */
-    launch_weighted_sum(out, x, out, L->k[0], L->k[1], n, ctx->stream);               /* mp_sum(x, out, t) */
+    conv2d_forward_modulate_act(s[ES_CONV0], t[ET_H0], t[ET_H1], t[ET_H3], t[ET_C], ACT_MP_SILU, batch,
+        ctx);                                                                         /* h1 = conv0(h0), h3 = mp_silu(h1 (c+1)) */
+    conv2d_forward_residual(s[ES_CONV1], t[ET_H3], out, x, L->k[0], L->k[1], batch, ctx); /* mp_sum(x, conv1(h3), t) */
 }
 
 static void edm_bwd(Layer* L, const float* x, const float* out, const float* g_out, float* g_x, int batch,
@@ -131,11 +132,10 @@ static void edm_bwd(Layer* L, const float* x, const float* out, const float* g_o
     s[ES_CONV1]->backward(s[ES_CONV1], t[ET_H3], NULL, t[ET_G0], t[ET_G1], batch, ctx); /* G1 = d h3 */
     launch_spatial_modulate_act_backward(t[ET_G0], t[ET_GC], t[ET_G1], t[ET_H1], t[ET_C], batch, L->dim[ED_HW], 1,
         L->dim[ED_C], ACT_MP_SILU, t[ET_RED], ctx->stream);                           /* G0 = d h1, dc */
-    s[ES_CONV0]->backward(s[ES_CONV0], t[ET_H0], NULL, t[ET_G0], t[ET_G1], batch, ctx); /* G1 = d h0 */
-    launch_activation_backward(t[ET_G0], t[ET_G1], x, n, ACT_MP_SILU, ctx->stream);   /* G0 = d x (branch) */
+    conv2d_backward_act_residual(s[ES_CONV0], t[ET_H0], t[ET_G0], g_x, x, ACT_MP_SILU, g_out, L->k[0], t[ET_G1],
+        batch, ctx);                                                                  /* d x = wa d out + d h0 mp_silu'(x) */
     s[ES_LIN]->backward(s[ES_LIN], slot->fwd, t[ET_C], t[ET_GC], t[ET_GEMB], batch, ctx);
     launch_weighted_sum(slot->grad, slot->grad, t[ET_GEMB], 1.0f, 1.0f, batch * L->dim[ED_EMB], ctx->stream);
-    launch_weighted_sum(g_x, g_out, t[ET_G0], L->k[0], 1.0f, n, ctx->stream);         /* + wa d out */
 }
 
 static const LayerKind kEdmBlock = {"cond_conv_residual", edm_fwd, edm_bwd};

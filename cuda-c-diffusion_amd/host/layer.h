@@ -89,4 +89,21 @@ void groupnorm_shift_forward(Module* gn, float* x, const float* shift, float* y,
 void groupnorm_shift_backward(Module* gn, const float* x, const float* shift, const float* g_y, float* g_x,
     float* g_shift, int batch, Context* ctx);
 
+/* conv2d modules (conv2d_create) with the pass that follows them in the
+   diffusion blocks folded into their kernels where the implicit-GEMM path
+   takes them (elsewhere the module runs and the pass follows as its own
+   launch, the reference's sequence):
+     conv2d_forward_residual:     out = res_w * res + out_w * conv(in)
+     conv2d_forward_modulate_act: out = conv(in), out2 = act(out * (cond[b, c] + 1))
+     conv2d_backward_act_residual: parameter gradients, and
+                                  grad_in = res_w * res + (dx * act'(act_in))
+   `tmp` holds the unfused path's intermediate (the module's input size);
+   act is ACT_SILU or ACT_MP_SILU for the fused kernels. */
+void conv2d_forward_residual(Module* m, const float* in, float* out, const float* res, float res_w, float out_w,
+    int batch, Context* ctx);
+void conv2d_forward_modulate_act(Module* m, const float* in, float* out, float* out2, const float* cond,
+    Activation act, int batch, Context* ctx);
+void conv2d_backward_act_residual(Module* m, const float* in, const float* grad_out, float* grad_in,
+    const float* act_in, Activation act, const float* res, float res_w, float* tmp, int batch, Context* ctx);
+
 #endif /* NN_LAYER_H */

@@ -439,6 +439,89 @@ static void conv_bwd(Layer* L, const float* in, const float* out, const float* g
 
 static const LayerKind kConv2d = {"conv2d", conv_fwd, conv_bwd};
 
+/* The convolution with a neighbouring pass of the diffusion blocks folded into
+   its implicit-GEMM kernels (launch_conv2d_*_implicit_fused), so that the
+   tensor between the two never goes through HBM.  Where the implicit kernels
+   do not take the convolution (channel counts, NNHIP_CONV_PATH=gemm), the
+   module's own forward/backward runs and the pass follows as a launch of its
+   own, the reference's sequence.  The results are the same either way. */
+
+static int conv_fused_fwd(const Layer* L) { return L->dim[CD_FWD] && !conv_gemm_path(L); }
+static int conv_fused_bwd(const Layer* L) { return L->dim[CD_WGRAD] && L->dim[CD_DGRAD] && !conv_gemm_path(L); }
+
+static void conv_fused_forward(Layer* L, const float* in, float* out, int batch, const NnConvFusion* f, Context* ctx)
+{
+    const int* d = L->dim;
+    float *w = L->buf[CB_W], *aux = L->buf[CB_AUX];
+    if (d[CD_MP]) launch_weight_normalize(w, d[CD_K] * d[CD_K] * d[CD_CIN], d[CD_COUT], L->k[0], ctx->stream);
+    conv_require_aligned(in, "the forward input");
+    launch_conv2d_forward_implicit_fused(out, in, w, d[CD_MP] ? NULL : aux, d[CD_MP] ? aux : NULL, batch, d[CD_HI],
+        d[CD_WI], d[CD_CIN], d[CD_COUT], d[CD_K], d[CD_S], d[CD_P], d[CD_HO], d[CD_WO], f, ctx->stream);
+}
+
+void conv2d_forward_residual(Module* m, const float* in, float* out, const float* res, float res_w, float out_w,
+    int batch, Context* ctx)
+{
+    Layer* L = as_layer(m);
+    const int* d = L->dim;
+    if (!conv_fused_fwd(L)) {
+        conv_fwd(L, in, out, batch, ctx);
+        launch_weighted_sum(out, res, out, res_w, out_w, batch * d[CD_HO] * d[CD_WO] * d[CD_COUT], ctx->stream);
+        return;
+    }
+    NnConvFusion f;
+    memset(&f, 0, sizeof f);
+    f.res = res;
+    f.res_w = res_w;
+    f.out_w = out_w;
+    conv_fused_forward(L, in, out, batch, &f, ctx);
+}
+
+void conv2d_forward_modulate_act(Module* m, const float* in, float* out, float* out2, const float* cond,
+    Activation act, int batch, Context* ctx)
+{
+    Layer* L = as_layer(m);
+    const int* d = L->dim;
+    if (!conv_fused_fwd(L) || (act != ACT_SILU && act != ACT_MP_SILU)) {
+        conv_fwd(L, in, out, batch, ctx);
+        launch_spatial_modulate_act_forward(out2, out, cond, batch, d[CD_HO] * d[CD_WO], 1, d[CD_COUT], act,
+            ctx->stream);
+        return;
+    }
+    NnConvFusion f;
+    memset(&f, 0, sizeof f);
+    f.cond = cond;
+    f.y2 = out2;
+    f.act = act;
+    conv_fused_forward(L, in, out, batch, &f, ctx);
+}
+
+void conv2d_backward_act_residual(Module* m, const float* in, const float* grad_out, float* grad_in,
+    const float* act_in, Activation act, const float* res, float res_w, float* tmp, int batch, Context* ctx)
+{
+    Layer* L = as_layer(m);
+    const int* d = L->dim;
+    const int n_in = batch * d[CD_HI] * d[CD_WI] * d[CD_CIN];
+    if (!conv_fused_bwd(L) || (act != ACT_SILU && act != ACT_MP_SILU)) {
+        conv_bwd(L, in, NULL, grad_out, tmp, batch, ctx);
+        launch_activation_backward(grad_in, tmp, act_in, n_in, act, ctx->stream);
+        launch_weighted_sum(grad_in, res, grad_in, res_w, 1.0f, n_in, ctx->stream);
+        return;
+    }
+    NN_ASSERT(grad_in != grad_out, "conv2d_backward_act_residual: grad_in must not alias grad_out");
+    conv_bwd(L, in, NULL, grad_out, NULL, batch, ctx); /* parameter gradients */
+    NnConvFusion f;
+    memset(&f, 0, sizeof f);
+    f.act_in = act_in;
+    f.act = act;
+    f.res = res;
+    f.res_w = res_w;
+    f.out_w = 1.0f;
+    conv_require_aligned(grad_out, "the output gradient");
+    launch_conv2d_input_grad_implicit_fused(grad_in, grad_out, L->buf[CB_W], d[CD_MP] ? L->buf[CB_AUX] : NULL, batch,
+        d[CD_HI], d[CD_WI], d[CD_CIN], d[CD_COUT], d[CD_K], d[CD_P], &f, ctx->stream);
+}
+
 Module* conv2d_create(Context* ctx, int C_in, int C_out, int K, int stride, int pad, int H, int W, int max_batch,
     int mp_mode, float gain)
 {

@@ -268,6 +268,37 @@ void launch_conv2d_input_grad_implicit(float* dx, const float* dy, const float* 
     int batch, int H, int W, int C_in, int C_out, int K, int pad, hipStream_t s);
 int nnhip_conv2d_input_grad_implicit_supported(int C_in, int C_out, int K, int stride, int pad);
 
+/* A neighbouring pass folded into an implicit-GEMM convolution kernel, so
+   that the tensor between the two is neither stored nor read back.  Each
+   fused form computes with the operation order of the pass it replaces, so
+   its results are those of the separate launches bit for bit.  Members that a
+   launcher does not take must be zero/NULL.
+     res, res_w, out_w: y = res_w * res + out_w * y, res shaped as y
+       (the block's launch_weighted_sum(y, res, y, res_w, out_w): mp_sum,
+       residual add; src/cond_conv_residual.c:35, 61, src/conv_residual.c:39, 65).
+     cond, y2, act (forward): y2 = act(y * (cond[b, c] + 1)) besides y
+       (launch_spatial_modulate_act_forward after the convolution,
+       src/cond_conv_residual.c:31-33); act ACT_SILU or ACT_MP_SILU.
+     act_in, act (input gradient): dx = dx * act'(act_in) before the residual
+       (launch_activation_backward, src/cond_conv_residual.c:54). */
+typedef struct NnConvFusion {
+    const float* res;
+    float res_w, out_w;
+    const float* cond;
+    float* y2;
+    const float* act_in;
+    Activation act;
+} NnConvFusion;
+
+/* launch_conv2d_forward_implicit with a fused epilogue: exactly one of
+   f->res (residual) and f->cond (modulate + activation into f->y2). */
+void launch_conv2d_forward_implicit_fused(float* y, const float* x, const float* Wt, const float* bias,
+    const float* gain, int batch, int H, int W, int C_in, int C_out, int K, int stride, int pad,
+    int H_out, int W_out, const NnConvFusion* f, hipStream_t s);
+/* launch_conv2d_input_grad_implicit with f->act_in and f->res (the EDM
+   block's conv0); act_in and res are [batch, H, W, C_in] as dx. */
+void launch_conv2d_input_grad_implicit_fused(float* dx, const float* dy, const float* Wt, const float* gain,
+    int batch, int H, int W, int C_in, int C_out, int K, int pad, const NnConvFusion* f, hipStream_t s);
 /* launch_spatial_reduce_sum with a lent workspace (may be NULL). */
 void launch_spatial_reduce_sum_ws(float* out, const float* in, int batch, int HW, int C,
     float* workspace, hipStream_t s);
