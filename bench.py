@@ -26,6 +26,7 @@ Prints ONE JSON line.  --gpus N > 1 is not supported (one GPU per box).
 from __future__ import annotations
 
 import argparse
+import ctypes as C
 import json
 import os
 import sys
@@ -441,7 +442,50 @@ def run_suite(L, nn, reps, with_cpu=True):
          4 * (Bn * H * Wd * (Ci + Co) + KKC * Co), "matrix-core bound", flops=conv_flops,
          cpu=cpu(lambda: orc.col2im(hgy @ hWt.T, him.shape, K, 1, 1), 8.0,
                  f"16 of 128 images x 8: numpy float32 matmul + oracle col2im ({os.cpu_count()} host cores)"))
-    del im, yc, gyc, gxc
+    # the EDM block's passes next to its convolutions (cfg2 = this shape, gain
+    # epilogue), fused into the implicit-GEMM epilogues vs the separate launches
+    gain_c = dev(np.array([0.9], np.float32))
+    cres, ccond, y2c = dev(rng.standard_normal(Bn * H * Wd * Co)), dev(0.5 * rng.standard_normal(Bn * Co)), \
+        L.alloc(Bn * H * Wd * Co)
+    wa_c, wb_c = nn.mp_sum_weights(0.3)
+    n_c = Bn * H * Wd * Co
+    f_res = nn.NnConvFusion(res=cres.p, res_w=wa_c, out_w=wb_c)
+    f_mod = nn.NnConvFusion(cond=ccond.p, y2=y2c.p, act=nn.ACT_MP_SILU)
+    f_dg = nn.NnConvFusion(act_in=im.p, act=nn.ACT_MP_SILU, res=cres.p, res_w=wa_c, out_w=1.0)
+    conv_geo = (Bn, H, Wd, Ci, Co, K, 1, 1, H, Wd)
+
+    def fused_note(extra):
+        return f"matrix-core bound; {extra}"
+    _row("conv_fwd_implicit_mp_sum", "cfg2 EDM conv1: conv * gain, then mp_sum in the epilogue",
+         T.median_us(lambda: L.launch_conv2d_forward_implicit_fused(yc.p, im.p, Wt.p, None, gain_c.p, *conv_geo,
+                                                                    C.addressof(f_res), stream), reps),
+         4 * (Bn * H * Wd * (Ci + 2 * Co) + KKC * Co), fused_note("+ 4 B/elem residual read"), flops=conv_flops)
+    _row("conv_fwd_implicit_then_mp_sum", "same as two launches (conv, launch_weighted_sum)",
+         T.median_us(lambda: (L.launch_conv2d_forward_implicit(yc.p, im.p, Wt.p, None, gain_c.p, *conv_geo, stream),
+                              L.launch_weighted_sum(yc.p, cres.p, yc.p, wa_c, wb_c, n_c, stream)), reps),
+         4 * (Bn * H * Wd * (Ci + 2 * Co) + KKC * Co), fused_note("reference sequence"), flops=conv_flops)
+    _row("conv_fwd_implicit_modulate_mp_silu", "cfg2 EDM conv0: conv * gain and mp_silu(y (c + 1)) in the epilogue",
+         T.median_us(lambda: L.launch_conv2d_forward_implicit_fused(yc.p, im.p, Wt.p, None, gain_c.p, *conv_geo,
+                                                                    C.addressof(f_mod), stream), reps),
+         4 * (Bn * H * Wd * (Ci + 2 * Co) + KKC * Co), fused_note("+ 4 B/elem second output"), flops=conv_flops)
+    _row("conv_fwd_implicit_then_modulate", "same as two launches (conv, launch_spatial_modulate_act_forward)",
+         T.median_us(lambda: (L.launch_conv2d_forward_implicit(yc.p, im.p, Wt.p, None, gain_c.p, *conv_geo, stream),
+                              L.launch_spatial_modulate_act_forward(y2c.p, yc.p, ccond.p, Bn, H, Wd, Co,
+                                                                    nn.ACT_MP_SILU, stream)), reps),
+         4 * (Bn * H * Wd * (Ci + 2 * Co) + KKC * Co), fused_note("reference sequence"), flops=conv_flops)
+    _row("conv_dgrad_implicit_mp_silu_residual", "cfg2 EDM conv0 input grad: * mp_silu'(x), + wa dout in the epilogue",
+         T.median_us(lambda: L.launch_conv2d_input_grad_implicit_fused(gxc.p, gyc.p, Wt.p, gain_c.p, Bn, H, Wd, Ci, Co,
+                                                                       K, 1, C.addressof(f_dg), stream), reps),
+         4 * (Bn * H * Wd * (3 * Ci + Co) + KKC * Co), fused_note("+ 8 B/elem act input and residual reads"),
+         flops=conv_flops)
+    _row("conv_dgrad_implicit_then_act_residual",
+         "same as three launches (input grad, launch_activation_backward, launch_weighted_sum)",
+         T.median_us(lambda: (L.launch_conv2d_input_grad_implicit(y2c.p, gyc.p, Wt.p, gain_c.p, Bn, H, Wd, Ci, Co, K,
+                                                                  1, stream),
+                              L.launch_activation_backward(gxc.p, y2c.p, im.p, n_c, nn.ACT_MP_SILU, stream),
+                              L.launch_weighted_sum(gxc.p, cres.p, gxc.p, wa_c, 1.0, n_c, stream)), reps),
+         4 * (Bn * H * Wd * (3 * Ci + Co) + KKC * Co), fused_note("reference sequence"), flops=conv_flops)
+    del im, yc, gyc, gxc, cres, y2c
 
     # cfg4: sinusoidal, LayerNorm, SiLU over the DDPM stack
     t = dev(rng.integers(0, 1000, 256))

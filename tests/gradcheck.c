@@ -248,6 +248,174 @@ static Module* with_scalar_param(Module* m, int k, float v)
     return m;
 }
 
+/* ------------------------------------------------------------------------
+ * Directional check for the diffusion blocks at sizes where the per-element
+ * check above drowns in fp32 noise (a sampled element moves L = <out, g> by
+ * eps * grad, against rounding noise of sqrt(n) * 6e-8 over n outputs).  Per
+ * group of inputs (the block input, the embedding, each parameter tensor) a
+ * random direction d over the whole group: the analytic directional
+ * derivative <grad, d> (double) against (L(+eps d) - L(-eps d)) / (2 eps)
+ * with L in double.  Both sides sum millions of terms, so the rounding noise
+ * averages out: relative error ~1e-4 at eps = 1e-2, where a wrong or missing
+ * gradient term is off by far more.  Parameter directions are scaled by the
+ * tensor's RMS (gamma ~ 1, weights ~ 1/sqrt(fan-in); 1 for the zero-initialised
+ * biases and betas, whose steps would otherwise vanish).  Returns the worst
+ * |num - ana| / max(|ana|, sqrt(sum (grad_i d_i)^2)) over the groups.
+ * kind 0: conv_residual (DDPM; groups = GroupNorm groups); kind 1:
+ * cond_conv_residual (EDM, t = 0.3, emb_lin gain set to 0.7).  ana_scale
+ * multiplies the analytic gradients (1 for the check; the test's sensitivity
+ * case passes 1.005, a 0.5% gradient error, which must fail the bar).
+ * ------------------------------------------------------------------------ */
+#define DC_EPS 1.0e-2
+
+static double dir_loss(Module* m, const float* d_in, float* d_out, float* h_out, const float* h_g, int batch,
+    int n_out)
+{
+    return loss_at(m, d_in, d_out, h_out, h_g, batch, n_out);
+}
+
+static double rms_host(const float* a, int n)
+{
+    double s = 0.0;
+    for (int i = 0; i < n; ++i) s += (double)a[i] * a[i];
+    return n ? sqrt(s / n) : 0.0;
+}
+
+/* One group: base values h_base (n floats, at device address d_dst), analytic
+   gradient h_ana, direction h_dir.  Restores the parameters and the group. */
+static double dir_group(const char* tag, Module* m, const ParamList* pl, float** snap, float* d_dst,
+    const float* h_base, const float* h_ana, const float* h_dir, int n, const float* d_in, float* d_out,
+    float* h_out, const float* h_g, int batch, int n_out, double ana_scale, int verbose)
+{
+    float* h_p = (float*)malloc((size_t)n * sizeof(float));
+    double ana = 0.0, floor2 = 0.0;
+    for (int i = 0; i < n; ++i) {
+        const double t = ana_scale * h_ana[i] * h_dir[i];
+        ana += t;
+        floor2 += t * t;
+    }
+    double l[2];
+    for (int sgn = 0; sgn < 2; ++sgn) {
+        const float e = (float)(sgn ? -DC_EPS : DC_EPS);
+        for (int i = 0; i < n; ++i) h_p[i] = h_base[i] + e * h_dir[i];
+        restore(pl, snap);
+        h2d(d_dst, h_p, n);
+        l[sgn] = dir_loss(m, d_in, d_out, h_out, h_g, batch, n_out);
+    }
+    restore(pl, snap);
+    h2d(d_dst, h_base, n);
+    const double num = (l[0] - l[1]) / (2.0 * DC_EPS);
+    const double scale = fmax(fabs(ana), sqrt(floor2));
+    const double rel = fabs(num - ana) / (scale > 0.0 ? scale : 1.0);
+    if (verbose) {
+        printf("    %-16s n=%-9d analytic %+.6e numeric %+.6e rel %.2e\n", tag, n, ana, num, rel);
+        fflush(stdout);
+    }
+    free(h_p);
+    return rel;
+}
+
+double nn_dircheck_block(int kind, int batch, int H, int W, int C, int groups, int emb, double ana_scale,
+    int verbose)
+{
+    nn_context_init(&g_ctx, 7ull, (hipStream_t)0);
+    int slot = ctx_add_cond(&g_ctx, emb, batch);
+    float* d_emb = nn_device_alloc((size_t)batch * emb);
+    nn_fill_normal(&g_ctx, d_emb, (size_t)batch * emb, 0.0f, 1.0f);
+    ctx_set_cond(&g_ctx, slot, d_emb);
+    Module* m = kind == 0 ? conv_residual_create(&g_ctx, C, emb, H, W, batch, groups, slot)
+                          : with_scalar_param(cond_conv_residual_create(&g_ctx, C, emb, H, W, batch, 0.3f, slot), 1,
+                                0.7f);
+    const int n_in = batch * m->in_dim, n_out = batch * m->out_dim, n_cond = batch * emb;
+    float* d_in = nn_device_alloc((size_t)n_in);
+    float* d_out = nn_device_alloc((size_t)n_out);
+    float* d_gout = nn_device_alloc((size_t)n_out);
+    float* d_gin = nn_device_alloc((size_t)n_in);
+    float* h_in = (float*)malloc((size_t)n_in * sizeof(float));
+    float* h_out = (float*)malloc((size_t)n_out * sizeof(float));
+    float* h_g = (float*)malloc((size_t)n_out * sizeof(float));
+    float* h_gin = (float*)malloc((size_t)n_in * sizeof(float));
+    float* h_dir = (float*)malloc((size_t)n_in * sizeof(float));
+    float* h_cond = (float*)malloc((size_t)n_cond * sizeof(float));
+    float* h_gcond = (float*)malloc((size_t)n_cond * sizeof(float));
+    for (int i = 0; i < n_in; ++i) h_in[i] = (float)nn_rng_normal(&g_ctx);
+    for (int i = 0; i < n_out; ++i) h_g[i] = (float)nn_rng_normal(&g_ctx);
+    h2d(d_in, h_in, n_in);
+    h2d(d_gout, h_g, n_out);
+    d2h(h_cond, d_emb, n_cond);
+
+    ParamList pl;
+    param_list_init(&pl);
+    m->parameters(m, &pl);
+    m->forward(m, d_in, d_out, batch, &g_ctx); /* warm-up: project MP weights */
+    NN_HIP_CHECK(hipDeviceSynchronize());
+    float** snap = (float**)calloc((size_t)pl.count, sizeof(float*));
+    float** ana = (float**)calloc((size_t)pl.count, sizeof(float*));
+    int n_max = n_in > n_cond ? n_in : n_cond;
+    for (int k = 0; k < pl.count; ++k) {
+        snap[k] = (float*)malloc((size_t)pl.items[k].size * sizeof(float));
+        ana[k] = (float*)malloc((size_t)pl.items[k].size * sizeof(float));
+        d2h(snap[k], pl.items[k].param, pl.items[k].size);
+        NN_HIP_CHECK(hipMemset(pl.items[k].grad, 0, (size_t)pl.items[k].size * sizeof(float)));
+        if (pl.items[k].size > n_max) n_max = pl.items[k].size;
+    }
+    m->forward(m, d_in, d_out, batch, &g_ctx);
+    ctx_zero_cond_grad(&g_ctx, batch);
+    m->backward(m, d_in, d_out, d_gout, d_gin, batch, &g_ctx);
+    NN_HIP_CHECK(hipDeviceSynchronize());
+    d2h(h_gin, d_gin, n_in);
+    d2h(h_gcond, g_ctx.cond[slot].grad, n_cond);
+    for (int k = 0; k < pl.count; ++k) d2h(ana[k], pl.items[k].grad, pl.items[k].size);
+    free(h_dir);
+    h_dir = (float*)malloc((size_t)n_max * sizeof(float));
+
+    double worst = 0.0;
+    for (int i = 0; i < n_in; ++i) h_dir[i] = (float)nn_rng_normal(&g_ctx);
+    worst = fmax(worst, dir_group("input", m, &pl, snap, d_in, h_in, h_gin, h_dir, n_in, d_in, d_out, h_out, h_g,
+                            batch, n_out, ana_scale, verbose));
+    for (int i = 0; i < n_cond; ++i) h_dir[i] = (float)nn_rng_normal(&g_ctx);
+    worst = fmax(worst, dir_group("embedding", m, &pl, snap, d_emb, h_cond, h_gcond, h_dir, n_cond, d_in, d_out,
+                            h_out, h_g, batch, n_out, ana_scale, verbose));
+    for (int k = 0; k < pl.count; ++k) {
+        const int n = pl.items[k].size;
+        double r = rms_host(snap[k], n);
+        if (r < 1e-2) r = 1.0; /* zero-initialised tensors (biases, beta): unit directions */
+        for (int i = 0; i < n; ++i) h_dir[i] = (float)(r * nn_rng_normal(&g_ctx));
+        char tag[32];
+        snprintf(tag, sizeof tag, "param %d", k);
+        worst = fmax(worst, dir_group(tag, m, &pl, snap, pl.items[k].param, snap[k], ana[k], h_dir, n, d_in, d_out,
+                                h_out, h_g, batch, n_out, ana_scale, verbose));
+    }
+    if (verbose) {
+        printf("  %s block [%d,%d,%d,%d]: worst directional rel error %.2e\n", kind == 0 ? "DDPM" : "EDM", batch, H,
+            W, C, worst);
+        fflush(stdout);
+    }
+    for (int k = 0; k < pl.count; ++k) {
+        free(snap[k]);
+        free(ana[k]);
+    }
+    free(snap);
+    free(ana);
+    param_list_free(&pl);
+    m->free(m);
+    ctx_free_cond(&g_ctx);
+    free(h_in);
+    free(h_out);
+    free(h_g);
+    free(h_gin);
+    free(h_dir);
+    free(h_cond);
+    free(h_gcond);
+    (void)hipFree(d_in);
+    (void)hipFree(d_out);
+    (void)hipFree(d_gout);
+    (void)hipFree(d_gin);
+    (void)hipFree(d_emb);
+    nn_context_destroy(&g_ctx);
+    return worst;
+}
+
 /* Returns the number of failing modules.  Module list: the reference's
  * gradcheck configs on the fused-kernel path (gradcheck.c:290-306), plus the
  * fused GroupNorm+activation module and GroupNorm shapes that take the

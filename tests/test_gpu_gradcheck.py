@@ -39,3 +39,46 @@ def test_sequential_views_stay_aligned_after_odd_links(L):
     gc = ctypes.CDLL(str(LIB))
     gc.nn_chaincheck_odd_run.restype = ctypes.c_int
     assert gc.nn_chaincheck_odd_run() == 0
+
+
+# Shapes whose GroupNorms take the streaming kernels (with the shift fused
+# into GN2 at 8 channels per group; the block's own add and pixel sum at 4),
+# and an EDM block whose convolutions take the implicit-GEMM kernels with the
+# fused epilogues.
+DIR_CASES = [(0, 16, 32, 32, 256, 32, 128), (0, 64, 32, 32, 128, 32, 64), (1, 16, 32, 32, 128, 0, 512)]
+DIR_IDS = ["ddpm-streaming-shift-fused", "ddpm-streaming-cpg4", "edm-implicit-fused"]
+DIR_BAR = 2e-3
+
+
+@pytest.mark.parametrize("case", DIR_CASES, ids=DIR_IDS)
+def test_block_directional_gradcheck(L, case):
+    """The blocks' backward at sizes where per-element finite differences
+    drown in fp32 noise: per input group (block input, embedding, each
+    parameter tensor) the directional derivative along a random direction over
+    the whole group, analytic <grad, d> against central differences of
+    L = <out, g> summed in double (eps = 1e-2).  The bar 2e-3 is relative to
+    max(|<grad, d>|, sqrt(sum (grad_i d_i)^2)): the truncation and rounding
+    error is ~1e-4 there, while a wrong or dropped gradient term is off by
+    orders of magnitude more."""
+    kind, B, H, W, C, G, emb = case
+    print(f"[case] directional gradcheck {case}", flush=True)
+    worst = _dircheck(case, 1.0)
+    print(f"directional gradcheck {case}: worst rel error {worst:.2e}", flush=True)
+    assert worst <= DIR_BAR
+
+
+def _dircheck(case, ana_scale):
+    gc = ctypes.CDLL(str(LIB))
+    gc.nn_dircheck_block.restype = ctypes.c_double
+    gc.nn_dircheck_block.argtypes = [ctypes.c_int] * 7 + [ctypes.c_double, ctypes.c_int]
+    return gc.nn_dircheck_block(*case, ana_scale, 1)
+
+
+def test_block_directional_gradcheck_sees_a_half_percent_error(L):
+    """The same check with every analytic gradient scaled by 1.005 (done in the
+    harness, after the backward): the bar must reject it, so a gradient that is
+    0.5% off anywhere would not pass."""
+    print("[case] directional gradcheck sensitivity", flush=True)
+    worst = _dircheck(DIR_CASES[0], 1.005)
+    print(f"directional gradcheck with gradients x 1.005: worst rel error {worst:.2e}", flush=True)
+    assert worst > DIR_BAR
