@@ -26,7 +26,7 @@ Prints ONE JSON line.  --gpus N > 1 is not supported (one GPU per box).
 from __future__ import annotations
 
 import argparse
-import ctypes as C
+import ctypes
 import json
 import os
 import sys
@@ -458,7 +458,7 @@ def run_suite(L, nn, reps, with_cpu=True):
         return f"matrix-core bound; {extra}"
     _row("conv_fwd_implicit_mp_sum", "cfg2 EDM conv1: conv * gain, then mp_sum in the epilogue",
          T.median_us(lambda: L.launch_conv2d_forward_implicit_fused(yc.p, im.p, Wt.p, None, gain_c.p, *conv_geo,
-                                                                    C.addressof(f_res), stream), reps),
+                                                                    ctypes.addressof(f_res), stream), reps),
          4 * (Bn * H * Wd * (Ci + 2 * Co) + KKC * Co), fused_note("+ 4 B/elem residual read"), flops=conv_flops)
     _row("conv_fwd_implicit_then_mp_sum", "same as two launches (conv, launch_weighted_sum)",
          T.median_us(lambda: (L.launch_conv2d_forward_implicit(yc.p, im.p, Wt.p, None, gain_c.p, *conv_geo, stream),
@@ -466,7 +466,7 @@ def run_suite(L, nn, reps, with_cpu=True):
          4 * (Bn * H * Wd * (Ci + 2 * Co) + KKC * Co), fused_note("reference sequence"), flops=conv_flops)
     _row("conv_fwd_implicit_modulate_mp_silu", "cfg2 EDM conv0: conv * gain and mp_silu(y (c + 1)) in the epilogue",
          T.median_us(lambda: L.launch_conv2d_forward_implicit_fused(yc.p, im.p, Wt.p, None, gain_c.p, *conv_geo,
-                                                                    C.addressof(f_mod), stream), reps),
+                                                                    ctypes.addressof(f_mod), stream), reps),
          4 * (Bn * H * Wd * (Ci + 2 * Co) + KKC * Co), fused_note("+ 4 B/elem second output"), flops=conv_flops)
     _row("conv_fwd_implicit_then_modulate", "same as two launches (conv, launch_spatial_modulate_act_forward)",
          T.median_us(lambda: (L.launch_conv2d_forward_implicit(yc.p, im.p, Wt.p, None, gain_c.p, *conv_geo, stream),
@@ -475,7 +475,7 @@ def run_suite(L, nn, reps, with_cpu=True):
          4 * (Bn * H * Wd * (Ci + 2 * Co) + KKC * Co), fused_note("reference sequence"), flops=conv_flops)
     _row("conv_dgrad_implicit_mp_silu_residual", "cfg2 EDM conv0 input grad: * mp_silu'(x), + wa dout in the epilogue",
          T.median_us(lambda: L.launch_conv2d_input_grad_implicit_fused(gxc.p, gyc.p, Wt.p, gain_c.p, Bn, H, Wd, Ci, Co,
-                                                                       K, 1, C.addressof(f_dg), stream), reps),
+                                                                       K, 1, ctypes.addressof(f_dg), stream), reps),
          4 * (Bn * H * Wd * (3 * Ci + Co) + KKC * Co), fused_note("+ 8 B/elem act input and residual reads"),
          flops=conv_flops)
     _row("conv_dgrad_implicit_then_act_residual",
