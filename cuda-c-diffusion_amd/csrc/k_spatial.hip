@@ -95,14 +95,14 @@ enum { kRedSum = 0, kRedModBwd = 1 };
 // Workgroup b S + s: rows [s R, min(HW, s R + R)) of sample b.  Lane layout:
 // CL lanes over the VW-float column units (a power of two <= 64), RP = kTpb / CL
 // row lanes.  part[(b S + s) C + c] receives the segment sum of channel c.
-template <int MODE, int ACT, int VW, bool NT>
-__global__ __launch_bounds__(kTpb) void spatial_reduce(float* __restrict__ part, float* __restrict__ gin,
+template <int MODE, int ACT, int VW, bool NT, int TPB = kTpb>
+__global__ __launch_bounds__(TPB) void spatial_reduce(float* __restrict__ part, float* __restrict__ gin,
     const float* __restrict__ gout, const float* __restrict__ x, const float* __restrict__ cond, int HW, int C,
     int S, int R, int CL) {
     typedef float vec __attribute__((ext_vector_type(VW)));
-    __shared__ vec red[kTpb];
+    __shared__ vec red[TPB];
     const int b = blockIdx.x / S, s = blockIdx.x % S;
-    const int lc = threadIdx.x % CL, lr = threadIdx.x / CL, RP = kTpb / CL;
+    const int lc = threadIdx.x % CL, lr = threadIdx.x / CL, RP = TPB / CL;
     const int CU = C / VW;  // column units per row
     const int r0 = s * R, r1 = min(HW, r0 + R);
     const size_t sample = (size_t)b * HW * C;
@@ -136,12 +136,43 @@ __global__ __launch_bounds__(kTpb) void spatial_reduce(float* __restrict__ part,
             };
             int r = r0 + lr;
             constexpr int kRows = 8;
-            for (; r + (kRows - 1) * RP < r1; r += kRows * RP) {
-                vec t[kRows];
+            if constexpr (TPB == 1024 && MODE == kRedModBwd) {
+                // one workgroup per sample: the 8 rows' 16 loads in flight at
+                // once (the stores of gin between them would otherwise keep the
+                // compiler from hoisting the later rows' loads).  With 256
+                // threads the registers this takes cost more occupancy than
+                // the loads in flight gain (measured).
+                for (; r + (kRows - 1) * RP < r1; r += kRows * RP) {
+                    vec gv[kRows], xv[kRows];
 #pragma unroll
-                for (int u = 0; u < kRows; ++u) t[u] = elem(r + u * RP);
+                    for (int u = 0; u < kRows; ++u) {
+                        const size_t k = sample + (size_t)(r + u * RP) * C + cu * VW;
+                        gv[u] = NT ? __builtin_nontemporal_load(reinterpret_cast<const vec*>(gout + k))
+                                   : *reinterpret_cast<const vec*>(gout + k);
+                        xv[u] = NT ? __builtin_nontemporal_load(reinterpret_cast<const vec*>(x + k))
+                                   : *reinterpret_cast<const vec*>(x + k);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);  // all 16 loads issued before the first use
 #pragma unroll
-                for (int u = 0; u < kRows; ++u) acc += t[u];
+                    for (int u = 0; u < kRows; ++u) {
+                        const size_t k = sample + (size_t)(r + u * RP) * C + cu * VW;
+                        vec g2;
+#pragma unroll
+                        for (int j = 0; j < VW; ++j) g2[j] = gv[u][j] * act_grad<ACT, false>(xv[u][j] * m[j]);
+                        const vec gi = g2 * m;
+                        if constexpr (NT) __builtin_nontemporal_store(gi, reinterpret_cast<vec*>(gin + k));
+                        else *reinterpret_cast<vec*>(gin + k) = gi;
+                        acc += g2 * xv[u];
+                    }
+                }
+            } else {
+                for (; r + (kRows - 1) * RP < r1; r += kRows * RP) {
+                    vec t[kRows];
+#pragma unroll
+                    for (int u = 0; u < kRows; ++u) t[u] = elem(r + u * RP);
+#pragma unroll
+                    for (int u = 0; u < kRows; ++u) acc += t[u];
+                }
             }
             for (; r < r1; r += RP) acc += elem(r);
         }
@@ -222,8 +253,16 @@ void launch_ew(const char* what, float* out, const float* in, const float* v, in
 
 // Reduction plan: segments per sample and rows per segment.
 struct RedPlan {
-    int VW, CL, S, R;
+    int VW, CL, S, R, TPB;
 };
+
+// One 1024-thread workgroup per sample when there are enough samples to give
+// every CU of the device (256 on MI355X) one and each is large: same-box A/B
+// of the modulate backward at [256, 4096, 64] and [256, 1024, 256]: 146.6 and
+// 146.1 us against 162.7 and 162.1 us segmented.  At [256, 1024, 128] (131K
+// elements a sample) it was 5 % slower, and at 128 samples (half the CUs) 20 %.
+constexpr int kBigBatch = 256;
+constexpr long long kBigSample = 1 << 18;
 
 RedPlan red_plan(int B, int HW, int C, bool vec) {
     RedPlan p;
@@ -231,6 +270,14 @@ RedPlan red_plan(int B, int HW, int C, bool vec) {
     const int CU = C / p.VW;
     p.CL = 1;
     while (p.CL * 2 <= CU && p.CL * 2 <= 64) p.CL *= 2;
+    if (vec && B >= kBigBatch && (long long)HW * C >= kBigSample && HW >= 8 * (1024 / p.CL)) {
+        // one workgroup per sample: no segment partials, no second launch
+        p.TPB = 1024;
+        p.S = 1;
+        p.R = HW;
+        return p;
+    }
+    p.TPB = kTpb;
     const int RP = kTpb / p.CL;
     // enough workgroups to fill the device (~2048), segments of >= 8 row passes
     int S = (2048 + B - 1) / (B > 0 ? B : 1);
@@ -290,10 +337,15 @@ void launch_red(const char* what, float* out, float* gin, const float* gout, con
     bool ok;
 #define NNK_RED(VW_)                                                                                           \
     ok = NNK_ACT_DISPATCH(act, A, {                                                                            \
-        if (nt) spatial_reduce<MODE, A, VW_, true><<<grid, kTpb, 0, s>>>(part, gin, gout, x, cond, HW, C, p.S,  \
-            p.R, p.CL);                                                                                             \
-        else spatial_reduce<MODE, A, VW_, false><<<grid, kTpb, 0, s>>>(part, gin, gout, x, cond, HW, C, p.S,    \
-            p.R, p.CL);                                                                                             \
+        if (p.TPB == 1024) {                                                                                   \
+            if (nt) spatial_reduce<MODE, A, VW_, true, 1024><<<grid, 1024, 0, s>>>(part, gin, gout, x, cond, HW, \
+                C, p.S, p.R, p.CL);                                                                            \
+            else spatial_reduce<MODE, A, VW_, false, 1024><<<grid, 1024, 0, s>>>(part, gin, gout, x, cond, HW,  \
+                C, p.S, p.R, p.CL);                                                                            \
+        } else if (nt) spatial_reduce<MODE, A, VW_, true><<<grid, kTpb, 0, s>>>(part, gin, gout, x, cond, HW, C, \
+            p.S, p.R, p.CL);                                                                                   \
+        else spatial_reduce<MODE, A, VW_, false><<<grid, kTpb, 0, s>>>(part, gin, gout, x, cond, HW, C, p.S,   \
+            p.R, p.CL);                                                                                        \
     })
     if (HW == 0) {
         // empty sums: zero gradients (the reference writes 0 for each (b, c))

@@ -99,6 +99,29 @@ def test_spatial_modulate_act_fused(L, orc, rng, shape, act):
         assert_bits_equal(gin2.download(), gin.download(), f"grad_in ws vs scratch, launch {rep}")
 
 
+def test_spatial_modulate_act_one_workgroup_per_sample(L, orc, rng):
+    """256 samples of 256 K elements each take the plan with one 1024-thread
+    workgroup per sample (no segment partials): grad_in bit-exact, grad_cond
+    within the bar of the double sums, lent workspace and library scratch
+    bit-identical."""
+    B, HW, C, act = 256, 1024, 256, 5
+    print(f"[case] spatial modulate+act backward, one workgroup per sample {(B, HW, C)}", flush=True)
+    x, c, g = _inputs(rng, B, HW, C)
+    xd, cd, gd = L.to_device(x), L.to_device(c), L.to_device(g)
+    gin, gc = L.alloc(x.size), L.alloc(B * C)
+    L.launch_spatial_modulate_act_backward(gin.p, gc.p, gd.p, xd.p, cd.p, B, HW, 1, C, act, None, None)
+    L.sync()
+    gin_ref, gc_ref = orc.spatial_modulate_act_backward(g, x, c, act)
+    assert_bits_equal(gin.download(shape=x.shape), gin_ref, "grad_in")
+    g2 = orc.act_backward(g, orc.spatial_modulate(x, c), act)
+    assert rel_err(gc.download(shape=(B, C)), gc_ref, floor=_sum_floor(g2 * x)) <= TOL
+    ws = _zeroed(L, L.nnhip_spatial_reduce_workspace(B, HW, C))
+    gc2 = L.alloc(B * C)
+    L.launch_spatial_modulate_act_backward(gin.p, gc2.p, gd.p, xd.p, cd.p, B, HW, 1, C, act, ws.p, None)
+    L.sync()
+    assert_bits_equal(gc2.download(), gc.download(), "grad_cond ws vs scratch")
+
+
 def _zeroed(L, n):
     a = L.alloc(max(1, n))
     a.fill_bytes(0)
