@@ -237,6 +237,34 @@ class _Timer:
         return float(np.median(out))
 
 
+class _OnceTimer:
+    """For `--traffic`: each row's launch sequence runs once, between two
+    marker launches (fills of TRAFFIC_MARKS floats: grids of 12 and 24
+    workgroups, which no row's own launches use), so that a counter trace can be
+    cut into rows.  The time it returns is a single cold launch and is not a
+    measurement."""
+
+    def __init__(self, L, stream):
+        self.L, self.stream = L, stream
+        self.ev = [L.dll.nnhip_event_create() for _ in range(2)]
+        self.mark = L.alloc(max(TRAFFIC_MARKS))
+
+    def median_us(self, fn, reps=1, warmup=0, warm_s=0.0):
+        L = self.L
+        L.dll.nnhip_stream_synchronize(self.stream)
+        L.nnhip_fill_f32(self.mark.p, 0.0, TRAFFIC_MARKS[0], self.stream)
+        L.dll.nnhip_event_record(self.ev[0], self.stream)
+        fn()
+        L.dll.nnhip_event_record(self.ev[1], self.stream)
+        L.nnhip_fill_f32(self.mark.p, 0.0, TRAFFIC_MARKS[1], self.stream)
+        L.dll.nnhip_event_synchronize(self.ev[1])
+        L.dll.nnhip_stream_synchronize(self.stream)
+        L.check("traffic")
+        return float(1e3 * L.dll.nnhip_event_elapsed_ms(self.ev[0], self.ev[1]))
+
+
+TRAFFIC_MARKS = (3000, 6000)  # fill_f32_kernel grids of 12 and 24 workgroups of 256: row start, row end
+
 FP32_MFMA_PEAK_TFLOPS = 157.3
 
 
@@ -273,10 +301,10 @@ def _row(name, cfg, us, algo_bytes, note="", flops=None, cpu=None):
         log(f"[suite] {name:34s} {us:9.2f} us  " + (f"{gbs:7.0f} GB/s ({gbs / HBM_PEAK_GBS:.3f})" if gbs else ""))
 
 
-def run_suite(L, nn, reps, with_cpu=True):
+def run_suite(L, nn, reps, with_cpu=True, once=False):
     rng = np.random.default_rng(SEED)
     stream = L.dll.nnhip_stream_create()
-    T = _Timer(L, stream)
+    T = _OnceTimer(L, stream) if once else _Timer(L, stream)
     f32 = np.float32
     from oracle import oracle as orc
     orc.set_threads(1)
@@ -729,6 +757,9 @@ def main() -> int:
                     help="skip the CPU leg (the self-check of sample 0 against the oracle and the CPU baseline)")
     ap.add_argument("--suite", action="store_true",
                     help="time every hot-path row at its BASELINE config (one JSON line per row) instead")
+    ap.add_argument("--traffic", action="store_true",
+                    help="run every suite row once, each after a marker launch, for per-row rocprofv3 counters "
+                         "(FETCH_SIZE, WRITE_SIZE) instead; its times are single cold launches, not measurements")
     ap.add_argument("--calibrate", action="store_true",
                     help="run the 1 GiB -> 1 GiB calibration copy (for scaling rocprofv3 FETCH/WRITE_SIZE) instead")
     ap.add_argument("--batch-sweep", action="store_true",
@@ -749,9 +780,9 @@ def main() -> int:
         print("bench.py: no HIP device", file=sys.stderr)
         return 1
     info = L.device_info()
-    if args.suite:
+    if args.suite or args.traffic:
         log(f"[suite] device {info}")
-        run_suite(L, nn, max(5, args.steps), with_cpu=not args.no_cpu)
+        run_suite(L, nn, max(5, args.steps), with_cpu=not args.no_cpu and not args.traffic, once=args.traffic)
         return 0
     if args.calibrate:
         run_calibration(L, max(1, args.steps))
