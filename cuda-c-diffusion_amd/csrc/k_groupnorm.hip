@@ -67,12 +67,20 @@ __global__ __launch_bounds__(kGenTpb) void gn_fwd_generic(float* __restrict__ y,
     }
 }
 
-template <int ACT>
+// PART: cpg is a power of two <= 64, so each thread always meets the same
+// channel (threadIdx.x % cpg) and the kernel also writes that sample's
+// dgamma/dbeta partials part_g/part_b[b*C + c] (sum over the pixels of d*xhat
+// and of d): per thread in element order, then a fixed xor tree over the
+// wave's lanes of the channel, then the waves in order.  Otherwise
+// gn_param_partial_generic computes them in a launch of its own.
+template <int ACT, bool PART = false>
 __global__ __launch_bounds__(kGenTpb) void gn_bwd_dx_generic(float* __restrict__ dx,
     const float* __restrict__ dy, const float* __restrict__ x, const float* __restrict__ gamma,
     const float* __restrict__ beta, const float* __restrict__ mu, const float* __restrict__ rstd,
-    int G, int HW, int C, int cpg, FastDiv div_cpg) {
+    int G, int HW, int C, int cpg, FastDiv div_cpg, float* __restrict__ part_g = nullptr,
+    float* __restrict__ part_b = nullptr) {
     __shared__ float red[2 * kGenNw];
+    __shared__ float cred[PART ? 2 : 1][kGenNw][PART ? kWave : 1];
     const int work = blockIdx.x;
     const int b = work / G;
     const int g = work - b * G;
@@ -97,6 +105,7 @@ __global__ __launch_bounds__(kGenTpb) void gn_bwd_dx_generic(float* __restrict__
     block_sum2<kGenNw>(pg, pgx, red);
     const float inv_n = 1.0f / (float)n;
     const float m1 = pg * inv_n;
+    float sg = 0.0f, sb = 0.0f;
     for (int i = threadIdx.x; i < n; i += kGenTpb) {
         uint32_t hw, cl;
         div_cpg.divmod((uint32_t)i, hw, cl);
@@ -107,6 +116,32 @@ __global__ __launch_bounds__(kGenTpb) void gn_bwd_dx_generic(float* __restrict__
         if constexpr (ACT != ACT_IDENTITY) d = d * act_grad<ACT>(gamma[c] * xh + beta[c]);
         const float gg = d * gamma[c];
         dx[o] = rs * ((gg - m1) - xh * pgx * inv_n);
+        if constexpr (PART) {
+            sg += d * xh;
+            sb += d;
+        }
+    }
+    if constexpr (PART) {
+        const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+        for (int o = kWave / 2; o >= cpg; o >>= 1) {
+            sg += __shfl_xor(sg, o);
+            sb += __shfl_xor(sb, o);
+        }
+        if (lane < cpg) {
+            cred[0][wid][lane] = sg;
+            cred[1][wid][lane] = sb;
+        }
+        __syncthreads();
+        if (threadIdx.x < cpg) {
+            float ag = cred[0][0][threadIdx.x], ab = cred[1][0][threadIdx.x];
+#pragma unroll
+            for (int w = 1; w < kGenNw; ++w) {
+                ag += cred[0][w][threadIdx.x];
+                ab += cred[1][w][threadIdx.x];
+            }
+            part_g[(size_t)b * C + g * cpg + threadIdx.x] = ag;
+            part_b[(size_t)b * C + g * cpg + threadIdx.x] = ab;
+        }
     }
 }
 
@@ -382,11 +417,21 @@ void gn_backward_impl(const char* what, float* dx, float* ggamma, float* gbeta, 
             mu, rstd, B, G, HW, C, s);
     if (!launched) {
         const FastDiv dv((uint32_t)cpg);
-        NNK_ACT_DISPATCH(act, A,
-            gn_bwd_dx_generic<A><<<dim3((unsigned)(B * G)), dim3(kGenTpb), 0, s>>>(dx, dy, x, gamma,
-                beta, mu, rstd, G, HW, C, cpg, dv);
-            gn_param_partial_generic<A><<<dim3((unsigned)((C + kWave - 1) / kWave), (unsigned)B),
-                dim3(kGenTpb), 0, s>>>(part_g, part_b, dy, x, gamma, beta, mu, rstd, G, HW, C, cpg));
+        // powers of two up to 64 channels per group: the partials come out of
+        // the dx kernel (one launch fewer, and the separate kernel has only
+        // ceil(C / 64) * B workgroups: 8 at the reference DDPM's first level)
+        const bool fused_part = cpg <= kWave && (cpg & (cpg - 1)) == 0;
+        NNK_ACT_DISPATCH(act, A, {
+            if (fused_part) {
+                gn_bwd_dx_generic<A, true><<<dim3((unsigned)(B * G)), dim3(kGenTpb), 0, s>>>(dx, dy, x, gamma,
+                    beta, mu, rstd, G, HW, C, cpg, dv, part_g, part_b);
+            } else {
+                gn_bwd_dx_generic<A><<<dim3((unsigned)(B * G)), dim3(kGenTpb), 0, s>>>(dx, dy, x, gamma,
+                    beta, mu, rstd, G, HW, C, cpg, dv);
+                gn_param_partial_generic<A><<<dim3((unsigned)((C + kWave - 1) / kWave), (unsigned)B),
+                    dim3(kGenTpb), 0, s>>>(part_g, part_b, dy, x, gamma, beta, mu, rstd, G, HW, C, cpg);
+            }
+        });
     }
     gn_param_reduce<<<dim3((unsigned)((C + kWave - 1) / kWave)), dim3(kRedTpb), 0, s>>>(ggamma,
         gbeta, part_g, part_b, B, C);

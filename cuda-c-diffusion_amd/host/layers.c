@@ -357,6 +357,30 @@ static int conv_gemm_forced(void)
     return e && strcmp(e, "gemm") == 0;
 }
 
+static int conv_implicit_forced(void)
+{
+    const char* e = getenv("NNHIP_CONV_PATH");
+    return e && strcmp(e, "implicit") == 0;
+}
+
+/* Whether the implicit-GEMM kernel (igemm_fwd: the forward, and the stride-1
+   input gradient) beats im2col + rocBLAS for an M x N x K product, by a cost
+   model fitted on MI355X.  A 128 x BN output tile takes ~2.25 us per 32-deep k
+   slice with one workgroup per CU (cfg3's forward: 36 slices, 1024 tiles,
+   four tiles per CU: 320 us), so few tiles leave the device idle: at the
+   reference DDPM's 7 x 7 x 128 level (M = 392 at batch 8, 4 tiles) the kernel
+   takes ~83 us where the GEMM path takes ~10.  The GEMM path: ~10 us of fixed
+   cost, the GEMM at ~70 TFLOP/s (rocBLAS fp32, measured at cfg3) and the
+   im2col matrix written and read at ~6 TB/s. */
+static int conv_implicit_wins(long long M, int N, int K)
+{
+    const int bn = N % 128 == 0 ? 128 : 64;
+    const double tiles = (double)((M + 127) / 128) * (N / bn);
+    const double t_impl = (K / 32.0) * 2.25 * ceil(tiles / 256.0);
+    const double t_gemm = 10.0 + 2.0 * (double)M * N * K / 70e6 + 8.0 * (double)M * K / 6e6;
+    return t_impl <= t_gemm;
+}
+
 /* the reference's sequence asked for at this call (needs the im2col buffer) */
 static int conv_gemm_path(const Layer* L)
 {
@@ -540,9 +564,15 @@ Module* conv2d_create(Context* ctx, int C_in, int C_out, int K, int stride, int 
     d[CD_HO] = Ho;
     d[CD_WO] = Wo;
     d[CD_MP] = mp_mode != 0;
-    d[CD_FWD] = nnhip_conv2d_implicit_supported(C_in, C_out);
+    /* the implicit kernels where the channel counts allow them and, for the
+       forward and input gradient, where they beat the GEMM path at max_batch
+       (NNHIP_CONV_PATH=implicit at creation: wherever allowed) */
+    const int forced = conv_implicit_forced();
+    d[CD_FWD] = nnhip_conv2d_implicit_supported(C_in, C_out) &&
+                (forced || conv_implicit_wins((long long)max_batch * Ho * Wo, C_out, kg));
     d[CD_WGRAD] = nnhip_conv2d_wgrad_implicit_supported(C_in, C_out);
-    d[CD_DGRAD] = nnhip_conv2d_input_grad_implicit_supported(C_in, C_out, K, stride, pad);
+    d[CD_DGRAD] = nnhip_conv2d_input_grad_implicit_supported(C_in, C_out, K, stride, pad) &&
+                  (forced || conv_implicit_wins((long long)max_batch * H * W, C_in, K * K * C_out));
     L->k[0] = 1e-4f;
     const int aux_n = mp_mode ? 1 : C_out;
     layer_buf(L, nw, 0);

@@ -444,12 +444,15 @@ int nn_gradcheck_run(int verbose)
     fails += check_module("conv3x3_s2", conv2d_create(&g_ctx, 4, 4, 3, 2, 1, 7, 7, B, 0, 1.0f), B, 2e-2);
     fails += check_module("linear", linear_create(&g_ctx, 12, 8), B, 2e-2);
     /* channel counts that take the implicit-GEMM forward, weight gradient and
-       (C_in % 128 == 0, stride 1) input gradient */
+       (C_in % 128 == 0, stride 1) input gradient; forced, since at these few
+       pixels the module's cost model would pick im2col + rocBLAS */
+    setenv("NNHIP_CONV_PATH", "implicit", 1);
     fails += check_module("conv3x3_implicit", conv2d_create(&g_ctx, 128, 128, 3, 1, 1, 4, 4, B, 0, 1.0f), B, 2e-2);
     fails += check_module("conv3x3_implicit_mp", conv2d_create(&g_ctx, 128, 128, 3, 1, 1, 4, 4, B, 1, 1.0f), B,
         2e-2);
     fails += check_module("conv3x3_s2_implicit", conv2d_create(&g_ctx, 32, 128, 3, 2, 1, 5, 5, B, 0, 1.0f), B, 2e-2);
     fails += check_module("conv3x3_implicit_c64", conv2d_create(&g_ctx, 64, 64, 3, 1, 1, 4, 4, B, 1, 1.0f), B, 2e-2);
+    unsetenv("NNHIP_CONV_PATH");
     /* diffusion blocks with an embedding slot; the EDM block's emb_lin gain is
        zero at creation (src/cond_conv_residual.c:113), so it is set to 0.7
        here to exercise the modulation path */
