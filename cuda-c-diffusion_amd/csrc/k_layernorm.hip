@@ -8,9 +8,9 @@
 //   forward : read x, write y           =  8 B/elem
 //   backward: read x, dy, write dx      = 12 B/elem
 //             + per-workgroup channel partials (2*C floats per 64 rows),
-//               summed in a fixed order in two levels: ln_colsum_seg sums
-//               segments of 64 partial rows on many workgroups, ln_colsum2
-//               adds the segment sums.
+//               stored in 16-channel chunks and summed in a fixed order by
+//               one more launch, ln_colsum_chunk (one workgroup per chunk
+//               and kind, reading its chunk as one contiguous run).
 // Generic path: one 256-thread block per row plus a coalesced partial kernel.
 // The fast path streams x, dy, y, dx with nontemporal loads and stores when
 // the launch is large (use_nt).
@@ -23,6 +23,13 @@ using namespace nnk;
 constexpr int kTpb = 256;
 constexpr int kNw = kTpb / kWave;
 constexpr int kRowsPerWg = 64;  // backward partial granularity (both paths)
+// The dgamma/dbeta partials of partial row p (one per kRowsPerWg rows) lie in
+// chunks of kCw channels: channel c at part[((c / kCw) * P + p) * kCw + c % kCw],
+// P partial rows.  A chunk's P rows are one contiguous run of P * 64 bytes.
+constexpr int kCw = 16;
+__device__ __forceinline__ size_t part_index(int c, int p, int P) {
+    return ((size_t)(c / kCw) * P + p) * kCw + (c % kCw);
+}
 
 // ----------------------------------------------------------------------------
 // Fast forward: NV float4 per lane per row, RB rows per wave at a time.
@@ -98,7 +105,7 @@ __global__ __launch_bounds__(kTpb) void ln_fwd_wave(float* __restrict__ y,
 // ----------------------------------------------------------------------------
 // Fast backward: workgroup b owns rows [64b, 64b+64); each wave walks 16 of
 // them RB at a time, then the 4 waves' channel sums are combined in LDS into
-// part_g/part_b[b*C + c].
+// partial row b of part_g/part_b (part_index, P = gridDim.x).
 // ----------------------------------------------------------------------------
 template <int NV, int RB, bool NT>
 __global__ __launch_bounds__(kTpb) void ln_bwd_wave(float* __restrict__ dx,
@@ -212,7 +219,7 @@ __global__ __launch_bounds__(kTpb) void ln_bwd_wave(float* __restrict__ dx,
                 a.z += b.z;
                 a.w += b.w;
             }
-            st4((kind == 0 ? part_g : part_b) + (size_t)blockIdx.x * C + 4 * c4, a);
+            st4((kind == 0 ? part_g : part_b) + part_index(4 * c4, blockIdx.x, gridDim.x), a);
         }
     }
 }
@@ -266,7 +273,8 @@ __global__ __launch_bounds__(kTpb) void ln_bwd_dx_generic(float* __restrict__ dx
     }
 }
 
-// part[chunk*C + c] over rows [64*chunk, 64*chunk+64): lanes walk 64 channels.
+// partial row y (rows [64 y, 64 y + 64)) of part_g/part_b, stored at
+// part_index(c, y, P = gridDim.y): lanes walk 64 channels.
 __global__ __launch_bounds__(kTpb) void ln_param_partial_generic(float* __restrict__ part_g,
     float* __restrict__ part_b, const float* __restrict__ dy, const float* __restrict__ x,
     const float* __restrict__ mu, const float* __restrict__ rstd, int rows, int C) {
@@ -290,85 +298,79 @@ __global__ __launch_bounds__(kTpb) void ln_param_partial_generic(float* __restri
     lb[wid][lane] = sb;
     __syncthreads();
     if (wid == 0 && c < C) {
-        part_g[(size_t)blockIdx.y * C + c] = ((lg[0][lane] + lg[1][lane]) + lg[2][lane]) + lg[3][lane];
-        part_b[(size_t)blockIdx.y * C + c] = ((lb[0][lane] + lb[1][lane]) + lb[2][lane]) + lb[3][lane];
+        const size_t o = part_index(c, blockIdx.y, gridDim.y);
+        part_g[o] = ((lg[0][lane] + lg[1][lane]) + lg[2][lane]) + lg[3][lane];
+        part_b[o] = ((lb[0][lane] + lb[1][lane]) + lb[2][lane]) + lb[3][lane];
     }
 }
 
-// First level of the dgamma/dbeta column sum: workgroup (x, s) sums partial
-// rows p in [64 s, 64 s + 64) of channels 64 x + lane; wave w takes
-// p = 64 s + w, + 4, ... (all 16 loads in flight), then the 4 wave sums are
-// added in wave order.  out[s*C + c].
+// dgamma/dbeta column sums over the P partial rows, in one launch: workgroup
+// (chunk, kind) sums the kCw channels of its chunk.  Fixed order, in two
+// levels:
+//   segment s (partial rows [64 s, 64 s + 64)): four chains, chain w adding
+//     rows 64 s + w, + 4, ... in row order from 0 (a row past P adds 0), then
+//     ((chain 0 + chain 1) + chain 2) + chain 3;
+//   total: four chains, chain w adding segments w, w + 4, ... in order from 0,
+//     then ((chain 0 + chain 1) + chain 2) + chain 3.
+// Segments are taken kSegB at a time: thread (s, w, q) of a batch runs one
+// first-level chain over channel quad q with its 16 loads in flight; the
+// chains are combined in LDS, and threads (w, j) < 64 carry the second-level
+// chains across the batches.
 constexpr int kSeg = 64;
-__global__ __launch_bounds__(kTpb) void ln_colsum_seg(float* __restrict__ og, float* __restrict__ ob,
+constexpr int kPer = kSeg / 4;                  // rows per first-level chain
+constexpr int kSegB = kTpb / (4 * (kCw / 4));   // segments per batch (16)
+__global__ __launch_bounds__(kTpb) void ln_colsum_chunk(float* __restrict__ og, float* __restrict__ ob,
     const float* __restrict__ pg, const float* __restrict__ pb, int P, int C) {
-    __shared__ float lg[kNw][kWave];
-    __shared__ float lb[kNw][kWave];
-    constexpr int kPer = kSeg / kNw;
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wid = threadIdx.x / kWave;
-    const int c = blockIdx.x * kWave + lane;
-    const int p0 = blockIdx.y * kSeg, p1 = min(P, p0 + kSeg);
-    float sg = 0.0f, sb = 0.0f;
-    if (c < C) {
-        float vg[kPer], vb[kPer];
+    __shared__ float4 lchain[kSegB][4][kCw / 4];
+    __shared__ float lseg[kSegB][kCw];
+    __shared__ float lfin[4][kCw];
+    const int t = threadIdx.x;
+    const int q = t % (kCw / 4), w = (t / (kCw / 4)) % 4, sl = t / kCw;
+    const float* part = (blockIdx.y ? pb : pg) + (size_t)blockIdx.x * P * kCw;
+    const int S = (P + kSeg - 1) / kSeg;
+    float acc = 0.0f;  // second-level chain t / kCw, channel t % kCw (t < 4 kCw)
+    for (int s0 = 0; s0 < S; s0 += kSegB) {
+        const int s = s0 + sl;
+        if (s < S) {
+            const int p0 = s * kSeg, p1 = min(P, p0 + kSeg);
+            float4 v[kPer];
 #pragma unroll
-        for (int u = 0; u < kPer; ++u) {
-            const int p = p0 + wid + u * kNw;
-            vg[u] = p < p1 ? pg[(size_t)p * C + c] : 0.0f;
-            vb[u] = p < p1 ? pb[(size_t)p * C + c] : 0.0f;
-        }
-#pragma unroll
-        for (int u = 0; u < kPer; ++u) {
-            sg += vg[u];
-            sb += vb[u];
-        }
-    }
-    lg[wid][lane] = sg;
-    lb[wid][lane] = sb;
-    __syncthreads();
-    if (wid == 0 && c < C) {
-        og[(size_t)blockIdx.y * C + c] = ((lg[0][lane] + lg[1][lane]) + lg[2][lane]) + lg[3][lane];
-        ob[(size_t)blockIdx.y * C + c] = ((lb[0][lane] + lb[1][lane]) + lb[2][lane]) + lb[3][lane];
-    }
-}
-
-// out[c] = sum_p part[p*C + c] over P partial rows; wave w takes p = w, w+4, ...
-__global__ __launch_bounds__(kTpb) void ln_colsum2(float* __restrict__ og, float* __restrict__ ob,
-    const float* __restrict__ pg, const float* __restrict__ pb, int P, int C) {
-    __shared__ float lg[kNw][kWave];
-    __shared__ float lb[kNw][kWave];
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wid = threadIdx.x / kWave;
-    const int c = blockIdx.x * kWave + lane;
-    float sg = 0.0f, sb = 0.0f;
-    if (c < C) {
-        // kB rows of each in flight (a short last batch too: its loads are
-        // predicated, not left to a loop of one load each), added in row order
-        constexpr int kB = 8;
-        for (int p = wid; p < P; p += kB * kNw) {
-            float vg[kB], vb[kB];
-#pragma unroll
-            for (int u = 0; u < kB; ++u) {
-                const bool in = p + u * kNw < P;
-                vg[u] = in ? pg[(size_t)(p + u * kNw) * C + c] : 0.0f;
-                vb[u] = in ? pb[(size_t)(p + u * kNw) * C + c] : 0.0f;
+            for (int u = 0; u < kPer; ++u) {
+                const int p = p0 + w + 4 * u;
+                v[u] = p < p1 ? ld4(part + (size_t)p * kCw + 4 * q) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             }
+            float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-            for (int u = 0; u < kB; ++u) {
-                if (p + u * kNw < P) {
-                    sg += vg[u];
-                    sb += vb[u];
-                }
+            for (int u = 0; u < kPer; ++u) {
+                a.x += v[u].x;
+                a.y += v[u].y;
+                a.z += v[u].z;
+                a.w += v[u].w;
+            }
+            lchain[sl][w][q] = a;
+        }
+        __syncthreads();
+        {
+            const int ss = t / kCw, j = t % kCw;
+            if (s0 + ss < S) {
+                const float* ch = reinterpret_cast<const float*>(&lchain[ss][0][0]);
+                lseg[ss][j] = ((ch[j] + ch[kCw + j]) + ch[2 * kCw + j]) + ch[3 * kCw + j];
+            }
+        }
+        __syncthreads();
+        if (t < 4 * kCw) {
+            const int w2 = t / kCw, j = t % kCw;
+#pragma unroll
+            for (int u = 0; u < kSegB / 4; ++u) {
+                if (s0 + w2 + 4 * u < S) acc += lseg[w2 + 4 * u][j];
             }
         }
     }
-    lg[wid][lane] = sg;
-    lb[wid][lane] = sb;
+    if (t < 4 * kCw) lfin[t / kCw][t % kCw] = acc;
     __syncthreads();
-    if (wid == 0 && c < C) {
-        og[c] = ((lg[0][lane] + lg[1][lane]) + lg[2][lane]) + lg[3][lane];
-        ob[c] = ((lb[0][lane] + lb[1][lane]) + lb[2][lane]) + lb[3][lane];
+    if (t < kCw) {
+        const int c = blockIdx.x * kCw + t;
+        if (c < C) (blockIdx.y ? ob : og)[c] = ((lfin[0][t] + lfin[1][t]) + lfin[2][t]) + lfin[3][t];
     }
 }
 
@@ -389,8 +391,9 @@ int fast_nv(int C, const void* a, const void* b, const void* c, const void* d) {
 }
 
 int num_chunks(int rows) { return (rows + kRowsPerWg - 1) / kRowsPerWg; }
-int num_segments(int P) { return (P + kSeg - 1) / kSeg; }
-size_t pad4(size_t n) { return (n + 3) / 4 * 4; }
+int num_col_chunks(int C) { return (C + kCw - 1) / kCw; }
+// floats of one kind's partials (whole chunks)
+size_t part_floats(int P, int C) { return (size_t)P * num_col_chunks(C) * kCw; }
 
 void ln_backward_impl(const char* what, float* dx, float* ggamma, float* gbeta, const float* dy,
     const float* x, const float* gamma, const float* mu, const float* rstd, int rows, int C,
@@ -405,19 +408,16 @@ void ln_backward_impl(const char* what, float* dx, float* ggamma, float* gbeta, 
     NNK_REQUIRE(dx && dy && x && gamma && mu && rstd, what, "%s: null pointer", what);
     NNK_REQUIRE(ws == nullptr || aligned16(ws), what, "%s: workspace must be 16-byte aligned", what);
     const int P = num_chunks(rows);
-    const int S = num_segments(P);
-    const size_t pc = pad4((size_t)P * C), sc = pad4((size_t)S * C);
+    const size_t pc = part_floats(P, C);
     float* scratch = ws;
     if (!scratch) {
-        scratch = nnk_scratch_acquire(2 * pc + 2 * sc, s, what);
+        scratch = nnk_scratch_acquire(2 * pc, s, what);
         if (!scratch) return;
     }
     float* part_g = scratch;
     float* part_b = scratch + pc;
-    float* seg_g = scratch + 2 * pc;
-    float* seg_b = seg_g + sc;
     const int nv = fast_nv(C, dx, dy, x, gamma);
-    if (nv && (C % 4 == 0) && aligned16(part_b)) {
+    if (nv) {
         const bool nt = use_nt(12LL * rows * C);
 #define NNK_LN_BWD(NV_, RB_)                                                                                \
     (nt ? ln_bwd_wave<NV_, RB_, true><<<P, kTpb, 0, s>>>(dx, part_g, part_b, dy, x, gamma, mu, rstd, rows, C) \
@@ -433,9 +433,7 @@ void ln_backward_impl(const char* what, float* dx, float* ggamma, float* gbeta, 
         ln_param_partial_generic<<<dim3((unsigned)((C + kWave - 1) / kWave), (unsigned)P), kTpb, 0, s>>>(
             part_g, part_b, dy, x, mu, rstd, rows, C);
     }
-    const unsigned cblocks = (unsigned)((C + kWave - 1) / kWave);
-    ln_colsum_seg<<<dim3(cblocks, (unsigned)S), kTpb, 0, s>>>(seg_g, seg_b, part_g, part_b, P, C);
-    ln_colsum2<<<dim3(cblocks), kTpb, 0, s>>>(ggamma, gbeta, seg_g, seg_b, S, C);
+    ln_colsum_chunk<<<dim3((unsigned)num_col_chunks(C), 2u), kTpb, 0, s>>>(ggamma, gbeta, part_g, part_b, P, C);
     if (!ws) nnk_scratch_release(scratch, s);
     nnk_after_launch(what, s);
 }
@@ -495,9 +493,8 @@ void launch_layernorm_backward_ws(float* grad_in, float* ggamma, float* gbeta,
 
 size_t nnhip_layernorm_backward_workspace(int batch, int C) {
     if (batch <= 0 || C <= 0) return 0;
-    // partials (2 P C) and segment sums (2 S C), each padded to a float4 multiple
-    const int P = num_chunks(batch);
-    return 2 * pad4((size_t)P * C) + 2 * pad4((size_t)num_segments(P) * C);
+    // dgamma and dbeta partials, P rows of whole 16-channel chunks each
+    return 2 * part_floats(num_chunks(batch), C);
 }
 
 }  // extern "C"

@@ -13,7 +13,9 @@ pytestmark = pytest.mark.gpu
 
 # (64 * 70 + 5, 64): 71 partial rows of 64 rows each, a last partial segment.
 # (64 * 2048, 16) and (64 * 2048 + 7, 8): 32 and 33 segments of 64 partial
-# rows (the second-level sum runs past its batch of 8 segments per wave).
+# rows (the column sum takes its segments 16 at a time: two batches, and three
+# with a partial last one).  C = 8, 48, 1000 and 1030 end on a partial
+# 16-channel chunk of partials.
 SHAPES = [(256 * 16 * 16, 256), (2, 16), (37, 48), (5, 1000), (3, 1030), (64, 4), (1, 7), (130, 2048), (1, 1),
           (64 * 70 + 5, 64), (64 * 2048, 16), (64 * 2048 + 7, 8)]
 
