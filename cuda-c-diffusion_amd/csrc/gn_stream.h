@@ -492,8 +492,10 @@ __global__ __launch_bounds__(Gm::TPB) void gns_fwd(float* __restrict__ y, float*
         float m = s / nthr, q = 0.0f;
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
-            const float a = v[k].x - m, bb = v[k].y - m, c = v[k].z - m, d = v[k].w - m;
-            q += (a * a + bb * bb) + (c * c + d * d);
+            q = fmaf(v[k].x - m, v[k].x - m, q);
+            q = fmaf(v[k].y - m, v[k].y - m, q);
+            q = fmaf(v[k].z - m, v[k].z - m, q);
+            q = fmaf(v[k].w - m, v[k].w - m, q);
         }
         float cnt = nthr;
         for_group_xor<Gm>([&](auto o) {
@@ -884,15 +886,15 @@ __global__ __launch_bounds__(Gm::TPB) void gns_bwd(float* __restrict__ dx, float
             xh.w = fmaf(v[k].w, rs, nms);
             d = v[NV + k];
             if constexpr (ACT != ACT_IDENTITY) {
-                d.x = d.x * act_grad<ACT>(gm.x * xh.x + bt.x);
-                d.y = d.y * act_grad<ACT>(gm.y * xh.y + bt.y);
-                d.z = d.z * act_grad<ACT>(gm.z * xh.z + bt.z);
-                d.w = d.w * act_grad<ACT>(gm.w * xh.w + bt.w);
+                d.x = d.x * act_grad<ACT>(fmaf(gm.x, xh.x, bt.x));
+                d.y = d.y * act_grad<ACT>(fmaf(gm.y, xh.y, bt.y));
+                d.z = d.z * act_grad<ACT>(fmaf(gm.z, xh.z, bt.z));
+                d.w = d.w * act_grad<ACT>(fmaf(gm.w, xh.w, bt.w));
             }
-            cg.x += d.x * xh.x;
-            cg.y += d.y * xh.y;
-            cg.z += d.z * xh.z;
-            cg.w += d.w * xh.w;
+            cg.x = fmaf(d.x, xh.x, cg.x);
+            cg.y = fmaf(d.y, xh.y, cg.y);
+            cg.z = fmaf(d.z, xh.z, cg.z);
+            cg.w = fmaf(d.w, xh.w, cg.w);
             cbs.x += d.x;
             cbs.y += d.y;
             cbs.z += d.z;
