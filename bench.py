@@ -52,7 +52,7 @@ SEED = 410293
 ROOFLINE_KERNEL = "gns_bwd<Geom<1024, 64, 32, 2>, 3, 1, true, false>"
 ROOFLINE_SEQUENCE = ROOFLINE_KERNEL + " (launch_groupnorm_act_backward_ws)"
 _PMC_KIB = {  # kernel: (FETCH_SIZE, WRITE_SIZE) per dispatch
-    ROOFLINE_KERNEL: (1_084_622, 1_081_881),
+    ROOFLINE_KERNEL: (1_084_811, 1_081_885),
 }
 TRAFFIC_BYTES = sum(2 * f + w for f, w in _PMC_KIB.values()) * 1024
 
