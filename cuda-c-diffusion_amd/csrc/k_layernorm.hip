@@ -321,7 +321,11 @@ constexpr int kPer = kSeg / 4;                  // rows per first-level chain
 constexpr int kSegB = kTpb / (4 * (kCw / 4));   // segments per batch (16)
 __global__ __launch_bounds__(kTpb) void ln_colsum_chunk(float* __restrict__ og, float* __restrict__ ob,
     const float* __restrict__ pg, const float* __restrict__ pb, int P, int C) {
-    __shared__ float4 lchain[kSegB][4][kCw / 4];
+    // chain sums [segment][chain][channel], each segment's row padded by 16
+    // floats: a wave's 128-bit stores (one segment) cover the 64 banks once,
+    // and the segment step's reads of four segments fall in different banks
+    constexpr int kLp = 4 * kCw + 16;
+    __shared__ __align__(16) float lchain[kSegB][kLp];
     __shared__ float lseg[kSegB][kCw];
     __shared__ float lfin[4][kCw];
     const int t = threadIdx.x;
@@ -347,13 +351,13 @@ __global__ __launch_bounds__(kTpb) void ln_colsum_chunk(float* __restrict__ og, 
                 a.z += v[u].z;
                 a.w += v[u].w;
             }
-            lchain[sl][w][q] = a;
+            *reinterpret_cast<float4*>(&lchain[sl][w * kCw + 4 * q]) = a;
         }
         __syncthreads();
         {
             const int ss = t / kCw, j = t % kCw;
             if (s0 + ss < S) {
-                const float* ch = reinterpret_cast<const float*>(&lchain[ss][0][0]);
+                const float* ch = lchain[ss];
                 lseg[ss][j] = ((ch[j] + ch[kCw + j]) + ch[2 * kCw + j]) + ch[3 * kCw + j];
             }
         }
