@@ -375,7 +375,7 @@ static int conv_implicit_forced(void)
 static int conv_implicit_wins(long long M, int N, int K)
 {
     const int bn = N % 128 == 0 ? 128 : 64;
-    const double tiles = (double)((M + 127) / 128) * (N / bn);
+    const double tiles = (double)((M + 127) / 128) * ((N + bn - 1) / bn);
     const double t_impl = (K / 32.0) * 2.25 * ceil(tiles / 256.0);
     const double t_gemm = 10.0 + 2.0 * (double)M * N * K / 70e6 + 8.0 * (double)M * K / 6e6;
     return t_impl <= t_gemm;
