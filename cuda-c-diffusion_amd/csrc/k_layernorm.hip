@@ -7,10 +7,13 @@
 // l owns float4 slots l, l+64, ...; each wave keeps RB rows in flight.
 //   forward : read x, write y           =  8 B/elem
 //   backward: read x, dy, write dx      = 12 B/elem
-//             + per-workgroup channel partials (2*C floats per 64 rows),
-//               stored in 16-channel chunks and summed in a fixed order by
-//               one more launch, ln_colsum_chunk (one workgroup per chunk
-//               and kind, reading its chunk as one contiguous run).
+//             + per-workgroup channel partials (2*C floats per 64 rows with
+//               4-wave workgroups; per 256 rows with 16-wave workgroups, which
+//               C <= 256 takes when the rows give every CU one), stored in
+//               16-channel chunks and summed in a fixed order by one more
+//               launch (one workgroup per chunk and kind, reading its chunk
+//               as one contiguous run): ln_colsum_small up to 256 partial
+//               rows, ln_colsum_chunk above.
 // Generic path: one 256-thread block per row plus a coalesced partial kernel.
 // The fast path streams x, dy, y, dx with nontemporal loads and stores when
 // the launch is large (use_nt).
@@ -22,8 +25,13 @@ using namespace nnk;
 
 constexpr int kTpb = 256;
 constexpr int kNw = kTpb / kWave;
-constexpr int kRowsPerWg = 64;  // backward partial granularity (both paths)
-// The dgamma/dbeta partials of partial row p (one per kRowsPerWg rows) lie in
+constexpr int kRowsPerWave = 16;  // fast backward: rows per wave
+// Backward partial granularity: 64 rows per partial row on the generic path
+// and the fast path's 4-wave workgroups, NWV * 16 with NWV waves; 64 is the
+// smallest, so the workspace is sized by it.
+constexpr int kRowsPerWg = 64;
+static_assert(kRowsPerWg == 4 * kRowsPerWave, "a 4-wave workgroup writes one partial row per kRowsPerWg rows");
+// The dgamma/dbeta partials of partial row p lie in
 // chunks of kCw channels: channel c at part[((c / kCw) * P + p) * kCw + c % kCw],
 // P partial rows.  A chunk's P rows are one contiguous run of P * 64 bytes.
 constexpr int kCw = 16;
@@ -103,16 +111,21 @@ __global__ __launch_bounds__(kTpb) void ln_fwd_wave(float* __restrict__ y,
 }
 
 // ----------------------------------------------------------------------------
-// Fast backward: workgroup b owns rows [64b, 64b+64); each wave walks 16 of
-// them RB at a time, then the 4 waves' channel sums are combined in LDS into
-// partial row b of part_g/part_b (part_index, P = gridDim.x).
+// Fast backward: workgroup b owns rows [NWV 16 b, NWV 16 (b + 1)); each of its
+// NWV waves walks 16 of them RB at a time (PIPE: the next RB rows' loads are
+// issued before the current rows' maths), then the waves' channel sums are
+// added in LDS in wave order into partial row b of part_g/part_b
+// (part_index, P = gridDim.x).
 // ----------------------------------------------------------------------------
-template <int NV, int RB, bool NT>
-__global__ __launch_bounds__(kTpb) void ln_bwd_wave(float* __restrict__ dx,
+template <int NV, int RB, int NWV, bool PIPE, bool NT>
+__global__ __launch_bounds__(NWV * kWave) void ln_bwd_wave(float* __restrict__ dx,
     float* __restrict__ part_g, float* __restrict__ part_b, const float* __restrict__ dy,
     const float* __restrict__ x, const float* __restrict__ gamma,
     const float* __restrict__ mu, const float* __restrict__ rstd, int rows, int C) {
-    __shared__ float4 lds[kNw][2][NV][kWave];
+    constexpr int TPB = NWV * kWave;
+    constexpr int kSteps = kRowsPerWave / RB;
+    static_assert(kRowsPerWave % RB == 0, "whole steps");
+    __shared__ float4 lds[NWV][2][NV][kWave];
     const int lane = threadIdx.x & (kWave - 1);
     const int wid = threadIdx.x / kWave;
     const int C4 = C / 4;
@@ -128,10 +141,10 @@ __global__ __launch_bounds__(kTpb) void ln_bwd_wave(float* __restrict__ dx,
         cb[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
 
-    constexpr int kRowsPerWave = kRowsPerWg / kNw;
-    const int wrow0 = blockIdx.x * kRowsPerWg + wid * kRowsPerWave;
-    for (int it = 0; it < kRowsPerWave; it += RB) {
-        float4 xv[RB][NV], gv[RB][NV];
+    const int wrow0 = blockIdx.x * (NWV * kRowsPerWave) + wid * kRowsPerWave;
+    constexpr int NB = PIPE ? 2 : 1;  // row buffers
+    float4 xv[NB][RB][NV], gv[NB][RB][NV];
+    auto load = [&](int buf, int it) {
 #pragma unroll
         for (int r = 0; r < RB; ++r) {
             const int row = wrow0 + it + r;
@@ -139,14 +152,16 @@ __global__ __launch_bounds__(kTpb) void ln_bwd_wave(float* __restrict__ dx,
             for (int k = 0; k < NV; ++k) {
                 const int c4 = lane + k * kWave;
                 if (row < rows && c4 < C4) {
-                    xv[r][k] = ldS<NT>(x + (size_t)row * C + 4 * c4);
-                    gv[r][k] = ldS<NT>(dy + (size_t)row * C + 4 * c4);
+                    xv[buf][r][k] = ldS<NT>(x + (size_t)row * C + 4 * c4);
+                    gv[buf][r][k] = ldS<NT>(dy + (size_t)row * C + 4 * c4);
                 } else {
-                    xv[r][k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                    gv[r][k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    xv[buf][r][k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    gv[buf][r][k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
                 }
             }
         }
+    };
+    auto compute = [&](int buf, int it) {
 #pragma unroll
         for (int r = 0; r < RB; ++r) {
             const int row = wrow0 + it + r;
@@ -157,11 +172,11 @@ __global__ __launch_bounds__(kTpb) void ln_bwd_wave(float* __restrict__ dx,
             for (int k = 0; k < NV; ++k) {
                 if (lane + k * kWave < C4) {
                     float4 xh, g;
-                    xh.x = (xv[r][k].x - m) * rs;
-                    xh.y = (xv[r][k].y - m) * rs;
-                    xh.z = (xv[r][k].z - m) * rs;
-                    xh.w = (xv[r][k].w - m) * rs;
-                    const float4 d = gv[r][k];
+                    xh.x = (xv[buf][r][k].x - m) * rs;
+                    xh.y = (xv[buf][r][k].y - m) * rs;
+                    xh.z = (xv[buf][r][k].z - m) * rs;
+                    xh.w = (xv[buf][r][k].w - m) * rs;
+                    const float4 d = gv[buf][r][k];
                     cg[k].x += d.x * xh.x;
                     cg[k].y += d.y * xh.y;
                     cg[k].z += d.z * xh.z;
@@ -176,8 +191,8 @@ __global__ __launch_bounds__(kTpb) void ln_bwd_wave(float* __restrict__ dx,
                     g.w = d.w * gm[k].w;
                     pg += (g.x + g.y) + (g.z + g.w);
                     pgx += (g.x * xh.x + g.y * xh.y) + (g.z * xh.z + g.w * xh.w);
-                    xv[r][k] = xh;
-                    gv[r][k] = g;
+                    xv[buf][r][k] = xh;
+                    gv[buf][r][k] = g;
                 }
             }
             const float S1 = wave_sum(pg), S2 = wave_sum(pgx);
@@ -187,13 +202,27 @@ __global__ __launch_bounds__(kTpb) void ln_bwd_wave(float* __restrict__ dx,
                 const int c4 = lane + k * kWave;
                 if (c4 < C4) {
                     float4 o;
-                    o.x = rs * ((gv[r][k].x - m1) - xv[r][k].x * S2 * invC);
-                    o.y = rs * ((gv[r][k].y - m1) - xv[r][k].y * S2 * invC);
-                    o.z = rs * ((gv[r][k].z - m1) - xv[r][k].z * S2 * invC);
-                    o.w = rs * ((gv[r][k].w - m1) - xv[r][k].w * S2 * invC);
+                    o.x = rs * ((gv[buf][r][k].x - m1) - xv[buf][r][k].x * S2 * invC);
+                    o.y = rs * ((gv[buf][r][k].y - m1) - xv[buf][r][k].y * S2 * invC);
+                    o.z = rs * ((gv[buf][r][k].z - m1) - xv[buf][r][k].z * S2 * invC);
+                    o.w = rs * ((gv[buf][r][k].w - m1) - xv[buf][r][k].w * S2 * invC);
                     stS<NT>(dx + (size_t)row * C + 4 * c4, o);
                 }
             }
+        }
+    };
+    if constexpr (PIPE) {
+        load(0, 0);
+#pragma unroll
+        for (int st = 0; st < kSteps; ++st) {
+            if (st + 1 < kSteps) load((st + 1) & 1, (st + 1) * RB);
+            compute(st & 1, st * RB);
+        }
+    } else {
+#pragma unroll
+        for (int st = 0; st < kSteps; ++st) {
+            load(0, st * RB);
+            compute(0, st * RB);
         }
     }
 
@@ -203,8 +232,8 @@ __global__ __launch_bounds__(kTpb) void ln_bwd_wave(float* __restrict__ dx,
         lds[wid][1][k][lane] = cb[k];
     }
     __syncthreads();
-    // thread t < 2*NV*64 combines one (kind, k, lane) float4 over the 4 waves
-    for (int t = threadIdx.x; t < 2 * NV * kWave; t += kTpb) {
+    // thread t < 2*NV*64 adds one (kind, k, lane) float4 over the waves in order
+    for (int t = threadIdx.x; t < 2 * NV * kWave; t += TPB) {
         const int kind = t / (NV * kWave);
         const int k = (t / kWave) % NV;
         const int l = t % kWave;
@@ -212,7 +241,7 @@ __global__ __launch_bounds__(kTpb) void ln_bwd_wave(float* __restrict__ dx,
         if (c4 < C4) {
             float4 a = lds[0][kind][k][l];
 #pragma unroll
-            for (int w = 1; w < kNw; ++w) {
+            for (int w = 1; w < NWV; ++w) {
                 const float4 b = lds[w][kind][k][l];
                 a.x += b.x;
                 a.y += b.y;
@@ -378,6 +407,51 @@ __global__ __launch_bounds__(kTpb) void ln_colsum_chunk(float* __restrict__ og, 
     }
 }
 
+// The same column sums for P <= 256 partial rows, in one short step: thread
+// (r = t / 4, channel quad q = t % 4) adds partial rows r, r + 64, r + 128,
+// r + 192 in that order (rows past P add nothing); lanes (group g, channel j)
+// then add the chains 4g .. 4g + 3 in order, and one lane per channel the 16
+// groups in order.  Every thread loads: one round trip instead of the general
+// kernel's per-segment chains.
+constexpr int kSmallP = 256;
+__global__ __launch_bounds__(kTpb) void ln_colsum_small(float* __restrict__ og, float* __restrict__ ob,
+    const float* __restrict__ pg, const float* __restrict__ pb, int P, int C) {
+    static_assert(kTpb == 4 * 64 && kCw == 16, "64 row lanes x 4 channel quads; 16 groups x 16 channels");
+    __shared__ __align__(16) float lchain[64][kCw + 4];  // rows padded to 80 bytes (16-byte aligned)
+    __shared__ float lgrp[16][kCw + 1];
+    const int t = threadIdx.x;
+    const int q = t % 4, r = t / 4;
+    const float* part = (blockIdx.y ? pb : pg) + (size_t)blockIdx.x * P * kCw;
+    float4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int p = r + 64 * u;
+        v[u] = p < P ? ld4(part + (size_t)p * kCw + 4 * q) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    float4 a = v[0];
+#pragma unroll
+    for (int u = 1; u < 4; ++u) {
+        a.x += v[u].x;
+        a.y += v[u].y;
+        a.z += v[u].z;
+        a.w += v[u].w;
+    }
+    *reinterpret_cast<float4*>(&lchain[r][4 * q]) = a;
+    __syncthreads();
+    {
+        const int j = t % kCw, g = t / kCw;
+        lgrp[g][j] = ((lchain[4 * g][j] + lchain[4 * g + 1][j]) + lchain[4 * g + 2][j]) + lchain[4 * g + 3][j];
+    }
+    __syncthreads();
+    if (t < kCw) {
+        float sum = lgrp[0][t];
+#pragma unroll
+        for (int g = 1; g < 16; ++g) sum += lgrp[g][t];
+        const int c = blockIdx.x * kCw + t;
+        if (c < C) (blockIdx.y ? ob : og)[c] = sum;
+    }
+}
+
 __global__ void fill_zero2(float* __restrict__ a, float* __restrict__ b, int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) {
@@ -421,23 +495,40 @@ void ln_backward_impl(const char* what, float* dx, float* ggamma, float* gbeta, 
     float* part_g = scratch;
     float* part_b = scratch + pc;
     const int nv = fast_nv(C, dx, dy, x, gamma);
+    int Pw = P;  // partial rows written
     if (nv) {
         const bool nt = use_nt(12LL * rows * C);
-#define NNK_LN_BWD(NV_, RB_)                                                                                \
-    (nt ? ln_bwd_wave<NV_, RB_, true><<<P, kTpb, 0, s>>>(dx, part_g, part_b, dy, x, gamma, mu, rstd, rows, C) \
-        : ln_bwd_wave<NV_, RB_, false><<<P, kTpb, 0, s>>>(dx, part_g, part_b, dy, x, gamma, mu, rstd, rows, C))
-        switch (nv) {
-        case 1: NNK_LN_BWD(1, 4); break;
-        case 2: NNK_LN_BWD(2, 2); break;
-        default: NNK_LN_BWD(4, 1); break;
-        }
+        // One 1024-thread workgroup (16 waves, 256 rows) per CU when the rows
+        // fill every CU with one, for C <= 256: a quarter of the partial rows
+        // of the 4-wave workgroups, and each wave's next two rows in flight
+        // while it works on the current two.  Same-box A/B at [65536, 256],
+        // three boxes: 35.8-36.2 us against 38.1-39.2 us for the 4-wave grid.
+        // Fewer rows would leave CUs idle that 4-wave workgroups still fill.
+        const int cus = nnk_device_cus(s);
+        const bool wide = nv == 1 && cus > 0 && (rows + 16 * kRowsPerWave - 1) / (16 * kRowsPerWave) >= cus;
+        if (wide) {
+            Pw = (rows + 16 * kRowsPerWave - 1) / (16 * kRowsPerWave);
+            if (nt) ln_bwd_wave<1, 2, 16, true, true><<<Pw, 16 * kWave, 0, s>>>(dx, part_g, part_b, dy, x, gamma, mu, rstd, rows, C);
+            else ln_bwd_wave<1, 2, 16, true, false><<<Pw, 16 * kWave, 0, s>>>(dx, part_g, part_b, dy, x, gamma, mu, rstd, rows, C);
+        } else {
+#define NNK_LN_BWD(NV_, RB_)                                                                                          \
+    (nt ? ln_bwd_wave<NV_, RB_, 4, false, true><<<P, kTpb, 0, s>>>(dx, part_g, part_b, dy, x, gamma, mu, rstd, rows, C) \
+        : ln_bwd_wave<NV_, RB_, 4, false, false><<<P, kTpb, 0, s>>>(dx, part_g, part_b, dy, x, gamma, mu, rstd, rows, C))
+            switch (nv) {
+            case 1: NNK_LN_BWD(1, 4); break;
+            case 2: NNK_LN_BWD(2, 2); break;
+            default: NNK_LN_BWD(4, 1); break;
+            }
 #undef NNK_LN_BWD
+        }
     } else {
         ln_bwd_dx_generic<<<rows, kTpb, 0, s>>>(dx, dy, x, gamma, mu, rstd, C);
         ln_param_partial_generic<<<dim3((unsigned)((C + kWave - 1) / kWave), (unsigned)P), kTpb, 0, s>>>(
             part_g, part_b, dy, x, mu, rstd, rows, C);
     }
-    ln_colsum_chunk<<<dim3((unsigned)num_col_chunks(C), 2u), kTpb, 0, s>>>(ggamma, gbeta, part_g, part_b, P, C);
+    const dim3 cgrid((unsigned)num_col_chunks(C), 2u);
+    if (Pw <= kSmallP) ln_colsum_small<<<cgrid, kTpb, 0, s>>>(ggamma, gbeta, part_g, part_b, Pw, C);
+    else ln_colsum_chunk<<<cgrid, kTpb, 0, s>>>(ggamma, gbeta, part_g, part_b, Pw, C);
     if (!ws) nnk_scratch_release(scratch, s);
     nnk_after_launch(what, s);
 }

@@ -450,6 +450,9 @@ void nnk_set_error(int code, const char* fmt, ...);
 void nnk_after_launch(const char* what, hipStream_t s);
 // Whether stream s is capturing a graph (no synchronisation or allocation then).
 bool nnk_capturing(hipStream_t s);
+// Compute units of the device that stream s (or, for the null stream, the
+// current device) belongs to, cached per device; 0 if unknown.
+int nnk_device_cus(hipStream_t s);
 void nnk_path_note(const char* fmt, ...);
 // Stream-ordered scratch for launchers that need partial sums.
 float* nnk_scratch_acquire(size_t n_floats, hipStream_t s, const char* what);

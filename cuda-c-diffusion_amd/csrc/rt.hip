@@ -5,6 +5,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <atomic>
 #include <mutex>
 #include <vector>
 
@@ -62,6 +63,25 @@ void nnk_path_note(const char* fmt, ...) {
 bool nnk_capturing(hipStream_t s) {
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     return s && hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+}
+
+int nnk_device_cus(hipStream_t s) {
+    constexpr int kDev = 16;
+    static std::atomic<int> cus_of[kDev];  // 0 = not yet queried (relaxed: racing callers store the same value)
+    int dev = -1;
+    if ((s ? hipStreamGetDevice(s, &dev) : hipGetDevice(&dev)) != hipSuccess || dev < 0 || dev >= kDev) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    int n = cus_of[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+            (void)hipGetLastError();
+            return 0;
+        }
+        cus_of[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
 }
 
 // Allocations the launch layer makes by itself (the scratch pools, their
