@@ -111,13 +111,15 @@ __global__ __launch_bounds__(kTpb) void ln_fwd_wave(float* __restrict__ y,
 }
 
 // ----------------------------------------------------------------------------
-// Fast backward: workgroup b owns rows [NWV 16 b, NWV 16 (b + 1)); each of its
-// NWV waves walks 16 of them RB at a time (PIPE: the next RB rows' loads are
-// issued before the current rows' maths), then the waves' channel sums are
-// added in LDS in wave order into partial row b of part_g/part_b
-// (part_index, P = gridDim.x).
+// Fast backward: each of the NWV waves of workgroup b walks 16 rows, RB at a
+// time (PIPE: the next RB rows' loads are issued before the current rows'
+// maths), then the waves' channel sums are added in LDS in wave order into
+// partial row b of part_g/part_b (part_index, P = gridDim.x).  The rows of
+// wave w: with CYC, i * (waves of the grid) + (b NWV + w) for i = 0..15, so
+// that each step of the grid reads one contiguous band of rows; otherwise the
+// block [NWV 16 b + 16 w, + 16).
 // ----------------------------------------------------------------------------
-template <int NV, int RB, int NWV, bool PIPE, bool NT>
+template <int NV, int RB, int NWV, bool PIPE, bool CYC, bool NT>
 __global__ __launch_bounds__(NWV * kWave) void ln_bwd_wave(float* __restrict__ dx,
     float* __restrict__ part_g, float* __restrict__ part_b, const float* __restrict__ dy,
     const float* __restrict__ x, const float* __restrict__ gamma,
@@ -142,12 +144,14 @@ __global__ __launch_bounds__(NWV * kWave) void ln_bwd_wave(float* __restrict__ d
     }
 
     const int wrow0 = blockIdx.x * (NWV * kRowsPerWave) + wid * kRowsPerWave;
+    const int gw = blockIdx.x * NWV + wid, nwt = gridDim.x * NWV;
+    auto row_of = [&](int i) { return CYC ? i * nwt + gw : wrow0 + i; };
     constexpr int NB = PIPE ? 2 : 1;  // row buffers
     float4 xv[NB][RB][NV], gv[NB][RB][NV];
     auto load = [&](int buf, int it) {
 #pragma unroll
         for (int r = 0; r < RB; ++r) {
-            const int row = wrow0 + it + r;
+            const int row = row_of(it + r);
 #pragma unroll
             for (int k = 0; k < NV; ++k) {
                 const int c4 = lane + k * kWave;
@@ -164,7 +168,7 @@ __global__ __launch_bounds__(NWV * kWave) void ln_bwd_wave(float* __restrict__ d
     auto compute = [&](int buf, int it) {
 #pragma unroll
         for (int r = 0; r < RB; ++r) {
-            const int row = wrow0 + it + r;
+            const int row = row_of(it + r);
             if (row >= rows) break;  // wave-uniform
             const float m = mu[row], rs = rstd[row];
             float pg = 0.0f, pgx = 0.0f;
@@ -417,8 +421,12 @@ constexpr int kSmallP = 256;
 __global__ __launch_bounds__(kTpb) void ln_colsum_small(float* __restrict__ og, float* __restrict__ ob,
     const float* __restrict__ pg, const float* __restrict__ pb, int P, int C) {
     static_assert(kTpb == 4 * 64 && kCw == 16, "64 row lanes x 4 channel quads; 16 groups x 16 channels");
-    __shared__ __align__(16) float lchain[64][kCw + 4];  // rows padded to 80 bytes (16-byte aligned)
-    __shared__ float lgrp[16][kCw + 1];
+    // chain sums of rows 4g .. 4g + 3 in lchain[g], each group padded by 16
+    // floats: the 16 lanes of a 128-bit store (four rows of one group) cover
+    // the 64 banks once, and a wave's reads (four groups, one row each) fall
+    // in four disjoint 16-bank ranges
+    __shared__ __align__(16) float lchain[16][4 * kCw + 16];
+    __shared__ float lgrp[16][kCw];
     const int t = threadIdx.x;
     const int q = t % 4, r = t / 4;
     const float* part = (blockIdx.y ? pb : pg) + (size_t)blockIdx.x * P * kCw;
@@ -436,11 +444,12 @@ __global__ __launch_bounds__(kTpb) void ln_colsum_small(float* __restrict__ og, 
         a.z += v[u].z;
         a.w += v[u].w;
     }
-    *reinterpret_cast<float4*>(&lchain[r][4 * q]) = a;
+    *reinterpret_cast<float4*>(&lchain[r / 4][(r % 4) * kCw + 4 * q]) = a;
     __syncthreads();
     {
         const int j = t % kCw, g = t / kCw;
-        lgrp[g][j] = ((lchain[4 * g][j] + lchain[4 * g + 1][j]) + lchain[4 * g + 2][j]) + lchain[4 * g + 3][j];
+        const float* ch = lchain[g];
+        lgrp[g][j] = ((ch[j] + ch[kCw + j]) + ch[2 * kCw + j]) + ch[3 * kCw + j];
     }
     __syncthreads();
     if (t < kCw) {
@@ -498,22 +507,26 @@ void ln_backward_impl(const char* what, float* dx, float* ggamma, float* gbeta, 
     int Pw = P;  // partial rows written
     if (nv) {
         const bool nt = use_nt(12LL * rows * C);
-        // One 1024-thread workgroup (16 waves, 256 rows) per CU when the rows
-        // fill every CU with one, for C <= 256: a quarter of the partial rows
-        // of the 4-wave workgroups, and each wave's next two rows in flight
-        // while it works on the current two.  Same-box A/B at [65536, 256],
-        // three boxes: 35.8-36.2 us against 38.1-39.2 us for the 4-wave grid.
+        // One 1024-thread workgroup (16 waves) per CU when the rows fill
+        // every CU with one, for C <= 256: a quarter of the partial rows of
+        // the 4-wave workgroups, each wave's next two rows in flight while it
+        // works on the current two, and rows dealt out cyclically over the
+        // grid's waves.  With each workgroup on a contiguous 256-row block
+        // instead, 256 streams 256 KB apart, the kernel ran 46.3 us on some
+        // boxes.  Same-box A/B at [65536, 256] on such a box: 36.5 us against
+        // 38.9 us for the 4-wave grid (46.3 us contiguous); on others the
+        // contiguous 16-wave form ran 35.8-36.3 us against 38.1-39.2 us.
         // Fewer rows would leave CUs idle that 4-wave workgroups still fill.
         const int cus = nnk_device_cus(s);
         const bool wide = nv == 1 && cus > 0 && (rows + 16 * kRowsPerWave - 1) / (16 * kRowsPerWave) >= cus;
         if (wide) {
             Pw = (rows + 16 * kRowsPerWave - 1) / (16 * kRowsPerWave);
-            if (nt) ln_bwd_wave<1, 2, 16, true, true><<<Pw, 16 * kWave, 0, s>>>(dx, part_g, part_b, dy, x, gamma, mu, rstd, rows, C);
-            else ln_bwd_wave<1, 2, 16, true, false><<<Pw, 16 * kWave, 0, s>>>(dx, part_g, part_b, dy, x, gamma, mu, rstd, rows, C);
+            if (nt) ln_bwd_wave<1, 2, 16, true, true, true><<<Pw, 16 * kWave, 0, s>>>(dx, part_g, part_b, dy, x, gamma, mu, rstd, rows, C);
+            else ln_bwd_wave<1, 2, 16, true, true, false><<<Pw, 16 * kWave, 0, s>>>(dx, part_g, part_b, dy, x, gamma, mu, rstd, rows, C);
         } else {
-#define NNK_LN_BWD(NV_, RB_)                                                                                          \
-    (nt ? ln_bwd_wave<NV_, RB_, 4, false, true><<<P, kTpb, 0, s>>>(dx, part_g, part_b, dy, x, gamma, mu, rstd, rows, C) \
-        : ln_bwd_wave<NV_, RB_, 4, false, false><<<P, kTpb, 0, s>>>(dx, part_g, part_b, dy, x, gamma, mu, rstd, rows, C))
+#define NNK_LN_BWD(NV_, RB_)                                                                                                 \
+    (nt ? ln_bwd_wave<NV_, RB_, 4, false, false, true><<<P, kTpb, 0, s>>>(dx, part_g, part_b, dy, x, gamma, mu, rstd, rows, C) \
+        : ln_bwd_wave<NV_, RB_, 4, false, false, false><<<P, kTpb, 0, s>>>(dx, part_g, part_b, dy, x, gamma, mu, rstd, rows, C))
             switch (nv) {
             case 1: NNK_LN_BWD(1, 4); break;
             case 2: NNK_LN_BWD(2, 2); break;
