@@ -90,3 +90,76 @@ def test_layernorm_empty_batch_zeroes_param_grads(L):
     L.launch_layernorm_backward(d.p, gg.p, gb.p, d.p, d.p, d.p, d.p, d.p, 0, C, None)
     L.sync()
     assert np.all(gg.download() == 0) and np.all(gb.download() == 0)
+
+
+def test_layernorm_graph_replay(L, orc, rng):
+    """Forward + backward with a lent workspace at cfg4's [65536, 256] (the
+    backward's 16-wave path and its one-step column sum) captured into a HIP
+    graph and replayed on alternating inputs: every replay matches the eager
+    launches on the same inputs bit for bit, with eager launches on the same
+    workspace between the replays."""
+    print("[case] layernorm graph capture and replay [65536, 256]", flush=True)
+    from helpers import assert_bits_equal
+
+    R, C = 256 * 16 * 16, 256
+    sets = [_inputs(rng, R, C) for _ in range(2)]
+    xd, dyd, yd, dxd = L.alloc(R * C), L.alloc(R * C), L.alloc(R * C), L.alloc(R * C)
+    gd, bd = L.to_device(sets[0][1]), L.to_device(sets[0][2])
+    mud, rsd, ggd, gbd = L.alloc(R), L.alloc(R), L.alloc(C), L.alloc(C)
+    ws = L.alloc(L.nnhip_layernorm_backward_workspace(R, C))
+    ws.fill_bytes(0)
+    s = L.dll.nnhip_stream_create()
+    assert s
+    outs = (yd, mud, rsd, dxd, ggd, gbd)
+
+    def issue():
+        L.launch_layernorm_forward(yd.p, mud.p, rsd.p, xd.p, gd.p, bd.p, R, C, 1e-5, s)
+        L.launch_layernorm_backward_ws(dxd.p, ggd.p, gbd.p, dyd.p, xd.p, gd.p, mud.p, rsd.p, R, C, ws.p, s)
+
+    def load(k):
+        L.dll.nnhip_stream_synchronize(s)  # the uploads are not ordered with s
+        xd.upload(sets[k][0])
+        dyd.upload(sets[k][3])
+
+    def results():
+        L.dll.nnhip_stream_synchronize(s)
+        L.sync()
+        return [o.download() for o in outs]
+
+    graph = None
+    try:
+        refs = []
+        for k in range(2):
+            load(k)
+            issue()
+            refs.append(results())
+        assert L.dll.nnhip_graph_capture_begin(s) == 0
+        issue()
+        graph = L.dll.nnhip_graph_capture_end(s)
+        assert graph, "graph capture failed"
+        names = ("y", "mu", "rstd", "dx", "dgamma", "dbeta")
+        for replay in range(4):
+            k = replay % 2
+            load(k)
+            for o in outs:
+                o.fill_bytes(0)
+            L.sync()
+            assert L.dll.nnhip_graph_launch(graph, s) == 0
+            for got, ref, name in zip(results(), refs[k], names):
+                assert_bits_equal(got, ref, f"replay {replay} {name}")
+            issue()
+            for got, ref, name in zip(results(), refs[k], names):
+                assert_bits_equal(got, ref, f"eager after replay {replay} {name}")
+        # the eager backward of set 1 against the oracle
+        x, gamma, beta, dy = sets[1][0], sets[0][1], sets[0][2], sets[1][3]
+        _, mu_ref, rs_ref = orc.layernorm_forward(x, gamma, beta, 1e-5)
+        dx_ref, gg_ref, gb_ref = orc.layernorm_backward(dy, x, gamma, mu_ref, rs_ref)
+        fg, fb = _param_floor(dy, x, mu_ref, rs_ref)
+        assert rel_err(refs[1][3].reshape(x.shape), dx_ref) <= TOL
+        assert rel_err(refs[1][4], gg_ref, floor=fg) <= TOL
+        assert rel_err(refs[1][5], gb_ref, floor=fb) <= TOL
+    finally:
+        if graph:
+            L.dll.nnhip_graph_destroy(graph)
+        L.dll.nnhip_stream_synchronize(s)
+        L.dll.nnhip_stream_destroy(s)
