@@ -747,6 +747,95 @@ def run_batch_sweep(L, reps):
     L.dll.nnhip_stream_destroy(stream)
 
 
+def run_dip_child(mode, steps, warmup):
+    """One protocol run from an idle device: `warmup` untimed steps, then
+    `steps` steps between two events on the launch stream (the default run's
+    timing), then `steps` more the same way once the clock has settled.  A
+    step is the fused GroupNorm+SiLU pair (mode "fused", the north-star
+    launches) or the plain SiLU streams of the same bytes (mode "plain":
+    launch_activation_forward + launch_activation_backward, 8 + 12 B/elem)."""
+    from __graft_entry__ import load_package
+
+    nn = load_package()
+    L = nn.lib()
+    B, HW, C, G = 256, 4096, 256, 32
+    n = B * HW * C
+    x, dy, gamma, beta = make_inputs(B, HW, C, SEED)
+    xd, dyd = L.to_device(x), L.to_device(dy)
+    del x, dy
+    yd, dxd = L.alloc(n), L.alloc(n)
+    gd, bd = L.to_device(gamma), L.to_device(beta)
+    mu, rs, gg, gb = L.alloc(B * G), L.alloc(B * G), L.alloc(C), L.alloc(C)
+    ws = L.to_device(np.zeros(L.nnhip_groupnorm_backward_workspace(B, HW, C, G), np.float32))
+    fws = L.to_device(np.zeros(max(1, L.nnhip_groupnorm_forward_workspace(B, HW, C, G)), np.float32))
+    s = L.dll.nnhip_stream_create()
+    if mode == "fused":
+        def step():
+            L.launch_groupnorm_act_forward_ws(yd.p, mu.p, rs.p, xd.p, gd.p, bd.p, B, HW, C, G, 1e-5, nn.ACT_SILU,
+                                              fws.p, s)
+            L.launch_groupnorm_act_backward_ws(dxd.p, gg.p, gb.p, dyd.p, xd.p, gd.p, bd.p, mu.p, rs.p, B, HW, C, G,
+                                               nn.ACT_SILU, ws.p, s)
+    else:
+        def step():
+            L.launch_activation_forward(yd.p, xd.p, n, nn.ACT_SILU, s)
+            L.launch_activation_backward(dxd.p, dyd.p, xd.p, n, nn.ACT_SILU, s)
+    ev = [L.dll.nnhip_event_create() for _ in range(3)]
+    for _ in range(warmup):
+        step()
+    L.dll.nnhip_stream_synchronize(s)
+    L.dll.nnhip_event_record(ev[0], s)
+    for _ in range(steps):
+        step()
+    L.dll.nnhip_event_record(ev[1], s)
+    for _ in range(steps):
+        step()
+    L.dll.nnhip_event_record(ev[2], s)
+    L.dll.nnhip_event_synchronize(ev[2])
+    L.check("dip")
+    for w in (fws, ws):
+        if L.nnhip_groupnorm_workspace_status(w.p) != 0:
+            raise RuntimeError("dip: a statistics wait ran out of polls")
+    timed = 1e3 * L.dll.nnhip_event_elapsed_ms(ev[0], ev[1]) / steps
+    settled = 1e3 * L.dll.nnhip_event_elapsed_ms(ev[1], ev[2]) / steps
+    print(json.dumps({"mode": mode, "steps": steps, "warmup": warmup, "timed_step_us": round(timed, 2),
+                      "settled_step_us": round(settled, 2)}), flush=True)
+
+
+def run_dip(steps, warmup, reps=2, idle_s=3.0):
+    """--dip: the default run's protocol for the fused pair and for the plain
+    SiLU streams of the same bytes, alternated, each in a child process
+    started after `idle_s` seconds of an idle device.  This process never
+    touches the GPU.  One JSON line per child, then one per mode with the
+    medians: how much of the timed step's excess over the settled one the
+    plain streams show too."""
+    import subprocess
+
+    got = {"fused": [], "plain": []}
+    for rep in range(reps):
+        for mode in ("plain", "fused"):
+            time.sleep(idle_s)
+            r = subprocess.run([sys.executable, str(Path(__file__).resolve()), "--dip-child", mode,
+                                "--steps", str(steps), "--warmup", str(warmup)],
+                               capture_output=True, text=True, timeout=600)
+            if r.returncode != 0:
+                sys.stderr.write(r.stderr[-4000:])
+                return r.returncode
+            rec = json.loads(r.stdout.strip().splitlines()[-1])
+            rec["rep"] = rep
+            got[mode].append(rec)
+            print(json.dumps(rec), flush=True)
+            log(f"[dip] {mode:5s} rep {rep}: timed {rec['timed_step_us']:.1f} us per step, "
+                f"settled {rec['settled_step_us']:.1f} us")
+    algo = 20.0 * 256 * 4096 * 256
+    for mode, recs in got.items():
+        t = float(np.median([r["timed_step_us"] for r in recs]))
+        st = float(np.median([r["settled_step_us"] for r in recs]))
+        print(json.dumps({"mode": mode, "median_timed_step_us": round(t, 2), "median_settled_step_us": round(st, 2),
+                          "timed_hbm_frac": round(algo / (t * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                          "settled_hbm_frac": round(algo / (st * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -765,12 +854,21 @@ def main() -> int:
     ap.add_argument("--batch-sweep", action="store_true",
                     help="time the north-star launches and the plain SiLU streams over batches and fit "
                          "per-sample and fixed costs instead")
+    ap.add_argument("--dip", action="store_true",
+                    help="run the default run's protocol (--warmup, --steps) for the fused pair and for the plain "
+                         "SiLU streams of the same bytes, each from an idle device in a child process, instead")
+    ap.add_argument("--dip-child", choices=("fused", "plain"), help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one GPU "
               f"(the path would shard over the batch, exchanging only a 2*C-float "
               f"dgamma/dbeta all-reduce)", file=sys.stderr)
         return 2
+    if args.dip:  # before anything in this process touches the GPU
+        return run_dip(args.steps, args.warmup)
+    if args.dip_child:
+        run_dip_child(args.dip_child, args.steps, args.warmup)
+        return 0
 
     from __graft_entry__ import load_package
 
