@@ -26,6 +26,7 @@ using namespace nnk;
 constexpr int kTpb = 256;
 constexpr int kNw = kTpb / kWave;
 constexpr int kRowsPerWave = 16;  // fast backward: rows per wave
+constexpr int kWideWaves = 16;    // fast backward: waves of a 1024-thread workgroup
 // Backward partial granularity: 64 rows per partial row on the generic path
 // and the fast path's 4-wave workgroups, NWV * 16 with NWV waves; 64 is the
 // smallest, so the workspace is sized by it.
@@ -507,22 +508,24 @@ void ln_backward_impl(const char* what, float* dx, float* ggamma, float* gbeta, 
     int Pw = P;  // partial rows written
     if (nv) {
         const bool nt = use_nt(12LL * rows * C);
-        // One 1024-thread workgroup (16 waves) per CU when the rows fill
-        // every CU with one, for C <= 256: a quarter of the partial rows of
-        // the 4-wave workgroups, each wave's next two rows in flight while it
-        // works on the current two, and rows dealt out cyclically over the
+        // One 1024-thread workgroup (kWideWaves waves) per CU when the rows
+        // fill every CU with one, for C <= 256: a quarter of the partial rows
+        // of the 4-wave workgroups, each wave's next two rows in flight while
+        // it works on the current two, and rows dealt out cyclically over the
         // grid's waves.  With each workgroup on a contiguous 256-row block
-        // instead, 256 streams 256 KB apart, the kernel ran 46.3 us on some
-        // boxes.  Same-box A/B at [65536, 256] on such a box: 36.5 us against
-        // 38.9 us for the 4-wave grid (46.3 us contiguous); on others the
-        // contiguous 16-wave form ran 35.8-36.3 us against 38.1-39.2 us.
-        // Fewer rows would leave CUs idle that 4-wave workgroups still fill.
+        // instead (256 streams 256 KB apart), the two launches took 46.3 us
+        // on some boxes.  Same-box A/B at [65536, 256] on such a box: 36.5 us
+        // against 38.9 us for the 4-wave grid; on other boxes the contiguous
+        // 16-wave form took 35.8-36.3 us against 38.1-39.2 us.  Fewer rows
+        // would leave CUs idle that 4-wave workgroups still fill.
+        constexpr int kWideRows = kWideWaves * kRowsPerWave;
         const int cus = nnk_device_cus(s);
-        const bool wide = nv == 1 && cus > 0 && (rows + 16 * kRowsPerWave - 1) / (16 * kRowsPerWave) >= cus;
+        const bool wide = nv == 1 && cus > 0 && (rows + kWideRows - 1) / kWideRows >= cus;
         if (wide) {
-            Pw = (rows + 16 * kRowsPerWave - 1) / (16 * kRowsPerWave);
-            if (nt) ln_bwd_wave<1, 2, 16, true, true, true><<<Pw, 16 * kWave, 0, s>>>(dx, part_g, part_b, dy, x, gamma, mu, rstd, rows, C);
-            else ln_bwd_wave<1, 2, 16, true, true, false><<<Pw, 16 * kWave, 0, s>>>(dx, part_g, part_b, dy, x, gamma, mu, rstd, rows, C);
+            Pw = (rows + kWideRows - 1) / kWideRows;
+            constexpr int T = kWideWaves * kWave;
+            if (nt) ln_bwd_wave<1, 2, kWideWaves, true, true, true><<<Pw, T, 0, s>>>(dx, part_g, part_b, dy, x, gamma, mu, rstd, rows, C);
+            else ln_bwd_wave<1, 2, kWideWaves, true, true, false><<<Pw, T, 0, s>>>(dx, part_g, part_b, dy, x, gamma, mu, rstd, rows, C);
         } else {
 #define NNK_LN_BWD(NV_, RB_)                                                                                                 \
     (nt ? ln_bwd_wave<NV_, RB_, 4, false, false, true><<<P, kTpb, 0, s>>>(dx, part_g, part_b, dy, x, gamma, mu, rstd, rows, C) \
