@@ -137,25 +137,30 @@ __global__ __launch_bounds__(TPB) void spatial_reduce(float* __restrict__ part, 
             int r = r0 + lr;
             constexpr int kRows = 8;
             if constexpr (TPB == 1024 && MODE == kRedModBwd) {
-                // one workgroup per sample: the 8 rows' 16 loads in flight at
-                // once (the stores of gin between them would otherwise keep the
-                // compiler from hoisting the later rows' loads).  With 256
-                // threads the registers this takes cost more occupancy than
-                // the loads in flight gain (measured).
-                for (; r + (kRows - 1) * RP < r1; r += kRows * RP) {
-                    vec gv[kRows], xv[kRows];
+                // one workgroup per sample, rows in batches of kP per lane,
+                // double-buffered: the next batch's loads are issued before
+                // the current batch's activation gradient, so with one
+                // workgroup per CU the arithmetic overlaps the memory traffic
+                // (the schedule barriers keep the compiler from sinking those
+                // loads below the current batch's stores of gin).  Rows are
+                // added in the same order as one row at a time.
+                constexpr int kP = 4;
+                const int step = kP * RP;
+                auto load_batch = [&](vec (&gv)[kP], vec (&xv)[kP], int rr) {
 #pragma unroll
-                    for (int u = 0; u < kRows; ++u) {
-                        const size_t k = sample + (size_t)(r + u * RP) * C + cu * VW;
+                    for (int u = 0; u < kP; ++u) {
+                        const size_t k = sample + (size_t)(rr + u * RP) * C + cu * VW;
                         gv[u] = NT ? __builtin_nontemporal_load(reinterpret_cast<const vec*>(gout + k))
                                    : *reinterpret_cast<const vec*>(gout + k);
                         xv[u] = NT ? __builtin_nontemporal_load(reinterpret_cast<const vec*>(x + k))
                                    : *reinterpret_cast<const vec*>(x + k);
                     }
-                    __builtin_amdgcn_sched_barrier(0);  // all 16 loads issued before the first use
+                    __builtin_amdgcn_sched_barrier(0);
+                };
+                auto use_batch = [&](const vec (&gv)[kP], const vec (&xv)[kP], int rr) {
 #pragma unroll
-                    for (int u = 0; u < kRows; ++u) {
-                        const size_t k = sample + (size_t)(r + u * RP) * C + cu * VW;
+                    for (int u = 0; u < kP; ++u) {
+                        const size_t k = sample + (size_t)(rr + u * RP) * C + cu * VW;
                         vec g2;
 #pragma unroll
                         for (int j = 0; j < VW; ++j) g2[j] = gv[u][j] * act_grad<ACT, false>(xv[u][j] * m[j]);
@@ -163,6 +168,25 @@ __global__ __launch_bounds__(TPB) void spatial_reduce(float* __restrict__ part, 
                         if constexpr (NT) __builtin_nontemporal_store(gi, reinterpret_cast<vec*>(gin + k));
                         else *reinterpret_cast<vec*>(gin + k) = gi;
                         acc += g2 * xv[u];
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                };
+                if (r + (kP - 1) * RP < r1) {
+                    vec ga[kP], xa[kP], gb[kP], xb[kP];
+                    load_batch(ga, xa, r);
+                    for (;;) {
+                        const int ra = r + step;  // the batch after the one in (ga, xa)
+                        const bool more_a = ra + (kP - 1) * RP < r1;
+                        if (more_a) load_batch(gb, xb, ra);
+                        use_batch(ga, xa, r);
+                        r = ra;
+                        if (!more_a) break;
+                        const int rb = r + step;  // the batch after the one in (gb, xb)
+                        const bool more_b = rb + (kP - 1) * RP < r1;
+                        if (more_b) load_batch(ga, xa, rb);
+                        use_batch(gb, xb, r);
+                        r = rb;
+                        if (!more_b) break;
                     }
                 }
             } else {
